@@ -1,0 +1,144 @@
+/*
+ * gdn_oracle.h -- CPU restatement of the OrionsBelt GDN hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
+ * implementation in orionsbelt_amd/.  Only tests/, __graft_entry__.smoke()
+ * and the cpu_baseline leg of bench.py may load it.  The product library
+ * (libkai_gdn_hip.so) never links, loads or calls anything in oracle/.
+ *
+ * Every function restates one reference routine in plain scalar C, in the
+ * reference's own evaluation order, and cites the file:line it follows
+ * (paths relative to the OrionsBelt tree).  Compiled with -ffp-contract=off
+ * so that a*b+c is two roundings, as the reference's portable scalar branch
+ * is on a target without FMA contraction.
+ *
+ * Pinning (what checks each function; see tests/):
+ *   orc_cumdecay_f32, orc_gated_scan_f32, orc_causal_dwconv1d_f32_k4,
+ *   orc_gemv_f32            -- bit-identical to the reference kai sources
+ *                              compiled in oracle/_ref, plus closed forms.
+ *   orc_*_f16 / orc_*_bf16  -- bit-identical to the reference gdn_sve.c
+ *                              compiled in oracle/_ref (clang), plus numpy
+ *                              float16 / RNE-bfloat16 conversion checks.
+ *   orc_causal_dwconv1d_silu_f32_k4 -- conv part as above; SiLU checked
+ *                              against torch.nn.functional.silu.
+ *   orc_delta_rule_head     -- known answers (k=e_i, beta=0, decay=0) and
+ *                              a double-precision brute force.
+ *   orc_delta_rule_decode_f32 -- the per-head routine above looped; matched
+ *                              against HF torch_recurrent_gated_delta_rule
+ *                              golden vectors (tests/golden).
+ *   orc_chunk_gdr_f32/_f64  -- HF torch_chunk_gated_delta_rule golden
+ *                              vectors, and equality with T stepped decodes.
+ */
+#ifndef ORC_GDN_ORACLE_H
+#define ORC_GDN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- kai ukernels, portable scalar branch ------------------------------ */
+
+/* decay[t][c] = prod_{i<=t} a[i][c]; running product starts at 1.0f.
+ * kleidiai_submission/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.c:122-129 */
+void orc_cumdecay_f32(const float *a, float *decay, size_t seq, size_t channels);
+
+/* acc = x + acc*g per channel, state in/out.
+ * kleidiai_submission/kai/ukernels/gdn/kai_gdn_gated_scan_f32_sve.c:86-95 */
+void orc_gated_scan_f32(const float *g, const float *x, float *s, float *state,
+                        size_t seq, size_t channels);
+
+/* out = h0*w0 + h1*w1 + h2*w2 + cur*w3, hist[3][C] in/out.
+ * kleidiai_submission/kai/ukernels/gdn/kai_gdn_causal_dwconv1d_f32_k4_sve.c:149-166 */
+void orc_causal_dwconv1d_f32_k4(const float *in, const float *w, float *out,
+                                float *hist, size_t seq, size_t channels);
+
+/* Same conv followed by SiLU y = x / (1 + exp(-x)).  The kai kernel has no
+ * activation; the SiLU epilogue is HF Qwen3.5 causal_conv1d_fn with
+ * activation="silu" (transformers modeling_qwen3_5.py:222-239). */
+void orc_causal_dwconv1d_silu_f32_k4(const float *in, const float *w, float *out,
+                                     float *hist, size_t seq, size_t channels);
+
+/* c[j] = sum_k a[k]*b[k][j], k-loop inner, acc from 0.0f.
+ * kleidiai_submission/kai/ukernels/gdn/kai_gdn_gemv_f32_f32_f32_1x4_neon.c:78-86 */
+void orc_gemv_f32(const float *a, const float *b, float *c, size_t k, size_t n);
+
+/* ---- mixed precision (gdn_sve.c scalar branches) ------------------------ */
+/* fp16 values are passed as IEEE binary16 bit patterns (uint16_t), bf16 as the
+ * upper half of a binary32 (uint16_t).  Conversions are round-to-nearest-even. */
+
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+/* src/orionsbelt/engines/cpu/kernels/gdn_sve.c:81-87 */
+uint16_t orc_f32_to_bf16(float f);
+/* src/orionsbelt/engines/cpu/kernels/gdn_sve.c:89-94 */
+float orc_bf16_to_f32(uint16_t b);
+
+/* gdn_sve.c:589-600 */
+void orc_cumdecay_f16(const float *a, uint16_t *decay, size_t seq, size_t channels);
+/* gdn_sve.c:511-523 */
+void orc_gated_scan_f16(const float *g, const float *x, float *s, uint16_t *state,
+                        size_t seq, size_t channels);
+/* gdn_sve.c:754-765 */
+void orc_cumdecay_bf16(const float *a, uint16_t *decay, size_t seq, size_t channels);
+/* gdn_sve.c:682-694 */
+void orc_gated_scan_bf16(const float *g, const float *x, float *s, uint16_t *state,
+                         size_t seq, size_t channels);
+
+/* ---- matrix-state delta rule ------------------------------------------- */
+
+/* One head, one token, in the reference order:
+ *   S *= decay; for each column i: kv = sum_j S[j][i]*k[j];
+ *   delta = (v[i]-kv)*beta; S[:,i] += k*delta; out[i] = sum_j S[j][i]*q[j].
+ * S is [hkd][hvd] row-major.  gpu/gdn_gpu_validate.c:100-118 */
+void orc_delta_rule_head(float *S, const float *k, const float *v, const float *q,
+                         float beta, float decay, float *out, size_t hkd, size_t hvd);
+
+/* Batched single-token decode with per-(sequence, value-head) gates:
+ *   S  [B][Hv][dk][dv] fp32, in/out
+ *   q,k [B][Hk][dk], v [B][Hv][dv], g,beta [B][Hv], o [B][Hv][dv]
+ * Value head h reads key head h / (Hv/Hk) (HF repeat_interleave,
+ * modeling_qwen3_5.py:500-502).  decay = expf(g) (HF :366), q is scaled by
+ * q_scale before the read-out (HF :356-357; 1 reproduces the reference's
+ * unscaled ref_delta_rule).  Per head this is orc_delta_rule_head. */
+void orc_delta_rule_decode_f32(float *S, const float *q, const float *k,
+                               const float *v, const float *g, const float *beta,
+                               float *o, int B, int Hv, int Hk, int dk, int dv,
+                               float q_scale);
+
+/* Same step with the state stored as fp16 bit patterns: widen on load, fp32
+ * arithmetic, narrow (RNE) on store -- the narrow-storage / wide-compute rule
+ * of gdn_sve.c:433-441 applied to the matrix state. */
+void orc_delta_rule_decode_f16state(uint16_t *S, const float *q, const float *k,
+                                    const float *v, const float *g,
+                                    const float *beta, float *o, int B, int Hv,
+                                    int Hk, int dk, int dv, float q_scale);
+
+/* ---- chunkwise (WY) gated delta rule, HF torch_chunk_gated_delta_rule ----
+ * transformers/models/qwen3_5/modeling_qwen3_5.py:248-328 restated per
+ * (batch, value head).  Layouts (token-major, as HF's [B, T, H, D]):
+ *   q,k [B][T][Hk][dk]  v [B][T][Hv][dv]  g,beta [B][T][Hv]
+ *   o [B][T][Hv][dv]    S [B][Hv][dk][dv] (initial state in, final out)
+ * q/k are used as given (no L2 norm inside; HF applies it in the caller with
+ * use_qk_l2norm_in_kernel); q is multiplied by q_scale (HF :278-279).
+ * T need not be a multiple of `chunk`; the tail chunk is zero-padded (HF
+ * :270-276).  _f32 computes in float, _f64 in double (inputs and outputs
+ * are float in both). */
+void orc_chunk_gdr_f32(const float *q, const float *k, const float *v,
+                       const float *g, const float *beta, float *o, float *S,
+                       int B, int T, int Hv, int Hk, int dk, int dv, int chunk,
+                       float q_scale);
+void orc_chunk_gdr_f64(const float *q, const float *k, const float *v,
+                       const float *g, const float *beta, float *o, float *S,
+                       int B, int T, int Hv, int Hk, int dk, int dv, int chunk,
+                       float q_scale);
+
+/* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
+int orc_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ORC_GDN_ORACLE_H */

@@ -1,0 +1,197 @@
+"""ctypes binding of the CPU oracle (liborb_oracle.so) and of the reference
+builds in oracle/_ref.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py as the checker; the product library never uses it.
+All array arguments are numpy arrays (C-contiguous, float32 / uint16).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liborb_oracle.so")
+REF_DIR = os.path.join(HERE, "_ref")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_sz = ctypes.c_size_t
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+
+def build() -> None:
+    """Compile liborb_oracle.so (and oracle/_ref when the reference tree is
+    present).  Raises CalledProcessError on a compiler error."""
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+    if os.path.isdir("/root/reference"):
+        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+def _load(path: str) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built (run oracle/Makefile)")
+    return ctypes.CDLL(path)
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = _load(LIB_PATH)
+        _lib.orc_f32_to_f16.restype = ctypes.c_uint16
+        _lib.orc_f32_to_f16.argtypes = [_flt]
+        _lib.orc_f16_to_f32.restype = ctypes.c_float
+        _lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        _lib.orc_f32_to_bf16.restype = ctypes.c_uint16
+        _lib.orc_f32_to_bf16.argtypes = [_flt]
+        _lib.orc_bf16_to_f32.restype = ctypes.c_float
+        _lib.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        _lib.orc_num_threads.restype = ctypes.c_int
+    return _lib
+
+
+def ref_kai() -> ctypes.CDLL | None:
+    """The reference kai ukernels compiled from /root/reference (scalar
+    branch), or None when oracle/_ref was not built."""
+    p = os.path.join(REF_DIR, "libkai_ref.so")
+    return ctypes.CDLL(p) if os.path.exists(p) else None
+
+
+def ref_sve() -> ctypes.CDLL | None:
+    """The reference gdn_sve.c compiled from /root/reference, or None."""
+    p = os.path.join(REF_DIR, "libgdn_sve_ref.so")
+    return ctypes.CDLL(p) if os.path.exists(p) else None
+
+
+def P(a: np.ndarray):
+    """Pointer to the data of a C-contiguous float32 or uint16 array."""
+    assert a.flags["C_CONTIGUOUS"], "array must be C-contiguous"
+    if a.dtype == np.float32:
+        return a.ctypes.data_as(_f32p)
+    if a.dtype == np.uint16:
+        return a.ctypes.data_as(_u16p)
+    raise TypeError(f"unsupported dtype {a.dtype}")
+
+
+# ---- kai-shaped entry points (the same argument order as the kai ABI) -----
+
+def cumdecay_f32(a, seq, ch, L=None):
+    L = L or lib()
+    out = np.empty(seq * ch, np.float32)
+    fn = getattr(L, "orc_cumdecay_f32", None) or L.kai_run_gdn_cumdecay_f32_sve
+    fn(P(a), P(out), _sz(seq), _sz(ch))
+    return out
+
+
+def gated_scan_f32(g, x, state, seq, ch, L=None):
+    L = L or lib()
+    s = np.empty(seq * ch, np.float32)
+    st = np.array(state, np.float32, copy=True)
+    fn = getattr(L, "orc_gated_scan_f32", None) or L.kai_run_gdn_gated_scan_f32_sve
+    fn(P(g), P(x), P(s), P(st), _sz(seq), _sz(ch))
+    return s, st
+
+
+def conv_f32(inp, w, hist, seq, ch, silu=False, L=None):
+    L = L or lib()
+    out = np.empty(seq * ch, np.float32)
+    h = np.array(hist, np.float32, copy=True)
+    if silu:
+        fn = L.orc_causal_dwconv1d_silu_f32_k4
+    else:
+        fn = getattr(L, "orc_causal_dwconv1d_f32_k4", None) or \
+            L.kai_run_gdn_causal_dwconv1d_f32_k4_sve
+    fn(P(inp), P(w), P(out), P(h), _sz(seq), _sz(ch))
+    return out, h
+
+
+def gemv_f32(a, b, k, n, L=None):
+    L = L or lib()
+    c = np.empty(max(n, 1), np.float32)
+    fn = getattr(L, "orc_gemv_f32", None) or L.kai_run_gdn_gemv_f32_f32_f32_1x4_neon
+    fn(P(a), P(b), P(c), _sz(k), _sz(n))
+    return c[:n]
+
+
+def cumdecay_narrow(a, seq, ch, fmt, L=None, prefix="orc_"):
+    L = L or lib()
+    out = np.empty(seq * ch, np.uint16)
+    getattr(L, f"{prefix}cumdecay_{fmt}")(P(a), P(out), _sz(seq), _sz(ch))
+    return out
+
+
+def gated_scan_narrow(g, x, state16, seq, ch, fmt, L=None, prefix="orc_"):
+    L = L or lib()
+    s = np.empty(seq * ch, np.float32)
+    st = np.array(state16, np.uint16, copy=True)
+    getattr(L, f"{prefix}gated_scan_{fmt}")(P(g), P(x), P(s), P(st), _sz(seq), _sz(ch))
+    return s, st
+
+
+# ---- matrix-state delta rule ----------------------------------------------
+
+def delta_rule_head(S, k, v, q, beta, decay, hkd, hvd):
+    S = np.array(S, np.float32, copy=True)
+    out = np.empty(hvd, np.float32)
+    lib().orc_delta_rule_head(P(S), P(k), P(v), P(q), _flt(beta), _flt(decay), P(out),
+                              _sz(hkd), _sz(hvd))
+    return S, out
+
+
+def delta_rule_decode(S, q, k, v, g, beta, B, Hv, Hk, dk, dv, q_scale):
+    """One decode step; returns (S_new, o).  S is [B][Hv][dk][dv] fp32."""
+    S = np.array(S, np.float32, copy=True)
+    o = np.empty((B, Hv, dv), np.float32)
+    lib().orc_delta_rule_decode_f32(P(S), P(q), P(k), P(v), P(g), P(beta), P(o),
+                                    _int(B), _int(Hv), _int(Hk), _int(dk), _int(dv),
+                                    _flt(q_scale))
+    return S, o
+
+
+def delta_rule_decode_f16state(S16, q, k, v, g, beta, B, Hv, Hk, dk, dv, q_scale):
+    S16 = np.array(S16, np.uint16, copy=True)
+    o = np.empty((B, Hv, dv), np.float32)
+    lib().orc_delta_rule_decode_f16state(P(S16), P(q), P(k), P(v), P(g), P(beta), P(o),
+                                         _int(B), _int(Hv), _int(Hk), _int(dk), _int(dv),
+                                         _flt(q_scale))
+    return S16, o
+
+
+def chunk_gdr(q, k, v, g, beta, S0, B, T, Hv, Hk, dk, dv, chunk=64, q_scale=None,
+              precision="f32"):
+    """HF chunkwise gated delta rule; returns (o [B][T][Hv][dv], S_final)."""
+    if q_scale is None:
+        q_scale = 1.0 / np.sqrt(dk)
+    S = np.array(S0, np.float32, copy=True)
+    o = np.empty((B, T, Hv, dv), np.float32)
+    fn = lib().orc_chunk_gdr_f32 if precision == "f32" else lib().orc_chunk_gdr_f64
+    fn(P(np.ascontiguousarray(q, np.float32)), P(np.ascontiguousarray(k, np.float32)),
+       P(np.ascontiguousarray(v, np.float32)), P(np.ascontiguousarray(g, np.float32)),
+       P(np.ascontiguousarray(beta, np.float32)), P(o), P(S), _int(B), _int(T), _int(Hv),
+       _int(Hk), _int(dk), _int(dv), _int(chunk), _flt(q_scale))
+    return o, S
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
+
+
+# ---- narrow-format helpers -------------------------------------------------
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bfloat16 bit patterns (vectorised form
+    of orc_f32_to_bf16)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    return ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)

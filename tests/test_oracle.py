@@ -1,0 +1,387 @@
+"""Pins the CPU oracle (oracle/gdn_oracle.c) before anything is compared
+against it.  CPU only.
+
+Each oracle function is checked against (a) the reference's own sources
+compiled in oracle/_ref (bit-identical), (b) the committed golden fixtures in
+tests/golden (bit-identical for the kai / gdn_sve vectors, tolerance for the
+HuggingFace delta-rule vectors), and (c) closed forms and brute force chosen
+so that a dropped term, a wrong index or a transposed operand fails.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    orc.lib()  # raises if liborb_oracle.so is missing
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    assert a.shape == b.shape
+    return np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                          b.view(np.uint32) if b.dtype == np.float32 else b)
+
+
+# --------------------------------------------------------------------------
+# kai ukernels vs the reference golden vectors (kai_ref.npz)
+# --------------------------------------------------------------------------
+
+def test_kai_golden_cumdecay(golden):
+    d = golden("kai_ref.npz")
+    for n in ("cd1", "cd2"):
+        seq, ch = d[f"{n}_shape"]
+        assert bits_equal(orc.cumdecay_f32(d[f"{n}_a"], seq, ch), d[f"{n}_out"])
+
+
+def test_kai_golden_gated_scan(golden):
+    d = golden("kai_ref.npz")
+    for n in ("sc1", "sc2"):
+        seq, ch = d[f"{n}_shape"]
+        s, st = orc.gated_scan_f32(d[f"{n}_g"], d[f"{n}_x"], d[f"{n}_state"], seq, ch)
+        assert bits_equal(s, d[f"{n}_s"]) and bits_equal(st, d[f"{n}_state_out"])
+
+
+def test_kai_golden_conv(golden):
+    d = golden("kai_ref.npz")
+    for n in ("cv1", "cv2", "cv3"):
+        seq, ch = d[f"{n}_shape"]
+        out, h = orc.conv_f32(d[f"{n}_in"], d[f"{n}_w"], d[f"{n}_hist"], seq, ch)
+        assert bits_equal(out, d[f"{n}_out"]) and bits_equal(h, d[f"{n}_hist_out"])
+
+
+def test_kai_golden_gemv(golden):
+    d = golden("kai_ref.npz")
+    for n in ("gv1", "gv2"):
+        k, nn = d[f"{n}_shape"]
+        assert bits_equal(orc.gemv_f32(d[f"{n}_a"], d[f"{n}_b"], k, nn), d[f"{n}_c"])
+
+
+# --------------------------------------------------------------------------
+# kai ukernels vs the live reference build (oracle/_ref), full test sweep
+# --------------------------------------------------------------------------
+
+REF_SEQS = [1, 4, 16, 64]                                  # test_kai_gdn.c:167
+REF_CHANS = [1, 3, 7, 8, 12, 16, 17, 32, 33, 128]          # test_kai_gdn.c:168
+
+
+@pytest.fixture(scope="module")
+def refkai():
+    L = orc.ref_kai()
+    if L is None:
+        pytest.skip("oracle/_ref not built (needs the reference tree)")
+    return L
+
+
+def test_ref_sweep_bit_identical(refkai):
+    rs = np.random.RandomState(7)
+    for seq in REF_SEQS:
+        for ch in REF_CHANS + [129, 255, 2051]:
+            n = seq * ch
+            a = rs.uniform(0.1, 1.5, n).astype(np.float32)
+            assert bits_equal(orc.cumdecay_f32(a, seq, ch), orc.cumdecay_f32(a, seq, ch, L=refkai))
+            g = rs.uniform(-0.99, 0.99, n).astype(np.float32)
+            x = rs.uniform(-2, 2, n).astype(np.float32)
+            st = rs.uniform(-1, 1, ch).astype(np.float32)
+            r1 = orc.gated_scan_f32(g, x, st, seq, ch)
+            r2 = orc.gated_scan_f32(g, x, st, seq, ch, L=refkai)
+            assert bits_equal(r1[0], r2[0]) and bits_equal(r1[1], r2[1])
+            w = rs.uniform(-1, 1, 4 * ch).astype(np.float32)
+            h = rs.uniform(-1, 1, 3 * ch).astype(np.float32)
+            c1 = orc.conv_f32(x, w, h, seq, ch)
+            c2 = orc.conv_f32(x, w, h, seq, ch, L=refkai)
+            assert bits_equal(c1[0], c2[0]) and bits_equal(c1[1], c2[1])
+    for k in (0, 1, 4, 128, 1024):
+        for n in (1, 3, 7, 130, 257):
+            a = rs.uniform(-1, 1, max(k, 1)).astype(np.float32)
+            b = rs.uniform(-1, 1, max(k * n, 1)).astype(np.float32)
+            assert bits_equal(orc.gemv_f32(a, b, k, n), orc.gemv_f32(a, b, k, n, L=refkai))
+
+
+def test_degenerate_writes_nothing():
+    """seq=0 / channels=0 leave outputs and state untouched
+    (test_kai_gdn.c:520-637)."""
+    L = orc.lib()
+    sentinel = np.full(8, 42.0, np.float32)
+    out = sentinel.copy()
+    L.orc_cumdecay_f32(orc.P(sentinel), orc.P(out), orc._sz(0), orc._sz(8))
+    assert bits_equal(out, sentinel)
+    st = np.array([1, -2, 3, -4], np.float32)
+    s = orc.gated_scan_f32(sentinel, sentinel, st, 0, 4)[1]
+    assert bits_equal(s, st)
+    hist = np.arange(6, dtype=np.float32)
+    assert bits_equal(orc.conv_f32(sentinel, sentinel, hist, 0, 2)[1], hist)
+    assert np.all(orc.gemv_f32(sentinel, sentinel, 0, 8) == 0.0)
+
+
+# --------------------------------------------------------------------------
+# Closed forms
+# --------------------------------------------------------------------------
+
+def test_cumdecay_closed_form_powers_of_two():
+    seq, ch = 100, 5
+    a = np.full(seq * ch, 0.5, np.float32)
+    d = orc.cumdecay_f32(a, seq, ch).reshape(seq, ch)
+    expect = np.ldexp(np.float32(1), -(np.arange(seq) + 1)).astype(np.float32)
+    assert bits_equal(d, np.repeat(expect[:, None], ch, axis=1))
+
+
+def test_scan_closed_forms():
+    seq, ch = 50, 3
+    x = np.random.RandomState(1).randint(-8, 8, seq * ch).astype(np.float32)
+    st = np.array([1, 2, 3], np.float32)
+    s, st2 = orc.gated_scan_f32(np.ones(seq * ch, np.float32), x, st, seq, ch)
+    expect = np.cumsum(x.reshape(seq, ch), axis=0) + st  # integer-valued: exact
+    assert bits_equal(s.reshape(seq, ch), expect.astype(np.float32))
+    assert bits_equal(st2, expect[-1].astype(np.float32))
+    s0, _ = orc.gated_scan_f32(np.zeros(seq * ch, np.float32), x, st, seq, ch)
+    assert bits_equal(s0, x)
+
+
+def test_conv_impulse_returns_taps():
+    seq, ch = 8, 4
+    w = np.random.RandomState(2).randn(4 * ch).astype(np.float32)
+    x = np.zeros((seq, ch), np.float32)
+    x[0] = 1.0
+    out, hist = orc.conv_f32(x.ravel(), w, np.zeros(3 * ch, np.float32), seq, ch)
+    out = out.reshape(seq, ch)
+    # out[t] = w[3 - t] for t < 4, then 0
+    for t in range(4):
+        assert bits_equal(out[t], w.reshape(4, ch)[3 - t])
+    assert np.all(out[4:] == 0)
+
+
+def test_conv_silu_epilogue_matches_torch():
+    torch = pytest.importorskip("torch")
+    rs = np.random.RandomState(3)
+    seq, ch = 33, 65
+    x = rs.randn(seq * ch).astype(np.float32)
+    w = (0.25 * rs.randn(4 * ch)).astype(np.float32)
+    h = rs.randn(3 * ch).astype(np.float32)
+    plain, h1 = orc.conv_f32(x, w, h, seq, ch)
+    silu, h2 = orc.conv_f32(x, w, h, seq, ch, silu=True)
+    assert bits_equal(h1, h2)
+    ref = torch.nn.functional.silu(torch.from_numpy(plain)).numpy()
+    np.testing.assert_allclose(silu, ref, rtol=2e-6, atol=1e-7)
+
+
+# --------------------------------------------------------------------------
+# Narrow formats (gdn_sve.c mixed precision)
+# --------------------------------------------------------------------------
+
+def test_f16_conversion_matches_numpy():
+    rs = np.random.RandomState(4)
+    bits = rs.randint(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    vals = np.concatenate([
+        bits.view(np.float32),
+        np.float32([0.0, -0.0, 65504, 65520, 65519.99, 6.1035156e-05, 5.9604645e-08,
+                    2.9802322e-08, 2.9802326e-08, 8.940697e-08, 1e-10, np.inf, -np.inf]),
+        (rs.randn(20000) * 1e-5).astype(np.float32),
+    ])
+    vals = vals[~np.isnan(vals)]
+    L = orc.lib()
+    got = np.array([L.orc_f32_to_f16(float(v)) for v in vals], np.uint16)
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    h = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    h = h[(h & 0x7C00) != 0x7C00]  # finite halves
+    back = np.array([L.orc_f16_to_f32(int(x)) for x in h], np.float32)
+    assert bits_equal(back, h.view(np.float16).astype(np.float32))
+
+
+def test_bf16_conversion_rne():
+    L = orc.lib()
+    # halfway cases round to even; above-half rounds up
+    cases = {0x3F808000: 0x3F80, 0x3F818000: 0x3F82, 0x3F808001: 0x3F81, 0x3F807FFF: 0x3F80}
+    for u, b in cases.items():
+        f = np.array([u], np.uint32).view(np.float32)[0]
+        assert L.orc_f32_to_bf16(float(f)) == b
+        assert orc.f32_to_bf16_bits(np.array([f], np.float32))[0] == b
+
+
+def test_mixed_precision_vs_reference_gdn_sve(golden):
+    d = golden("sve_mixed.npz")
+    T, C = d["shape"]
+    for scen in ("warm", "cold"):
+        for fmt in ("f16", "bf16"):
+            cd = orc.cumdecay_narrow(d[f"{scen}_a"], T, C, fmt)
+            assert np.array_equal(cd, d[f"{scen}_cd_{fmt}"]), (scen, fmt)
+            s, st = orc.gated_scan_narrow(d[f"{scen}_g"], d[f"{scen}_x"],
+                                          d[f"{scen}_st16_{fmt}"], T, C, fmt)
+            assert bits_equal(s, d[f"{scen}_scan_s_{fmt}"]), (scen, fmt)
+            assert np.array_equal(st, d[f"{scen}_scan_st_{fmt}"]), (scen, fmt)
+
+
+# --------------------------------------------------------------------------
+# Matrix-state delta rule
+# --------------------------------------------------------------------------
+
+def test_delta_rule_hand_computed():
+    """d=2: S0=0, beta=1 -> S = k (x) v and o = S^T q."""
+    k = np.float32([0.8, 0.6])
+    v = np.float32([1.0, 2.0])
+    q = np.float32([0.6, 0.8])
+    S, o = orc.delta_rule_head(np.zeros(4, np.float32), k, v, q, 1.0, 0.7, 2, 2)
+    np.testing.assert_allclose(S.reshape(2, 2), [[0.8, 1.6], [0.6, 1.2]], rtol=1e-7)
+    np.testing.assert_allclose(o, [0.96, 1.92], rtol=1e-6)
+
+
+def test_delta_rule_known_answers():
+    rs = np.random.RandomState(5)
+    dk, dv = 16, 12
+    S0 = rs.randn(dk * dv).astype(np.float32)
+    q = rs.randn(dk).astype(np.float32)
+    v = rs.randn(dv).astype(np.float32)
+    # k = e_i, beta = 1, decay = 1: row i becomes v (to rounding), others kept
+    i = 5
+    k = np.zeros(dk, np.float32)
+    k[i] = 1.0
+    S, _ = orc.delta_rule_head(S0, k, v, q, 1.0, 1.0, dk, dv)
+    S, S0m = S.reshape(dk, dv), S0.reshape(dk, dv)
+    np.testing.assert_allclose(S[i], v, rtol=0, atol=4 * np.finfo(np.float32).eps * 4)
+    assert bits_equal(np.delete(S, i, 0), np.delete(S0m, i, 0))
+    # beta = 0: pure decay, o = (decay S)^T q
+    kk = rs.randn(dk).astype(np.float32)
+    S, o = orc.delta_rule_head(S0, kk, v, q, 0.0, 0.75, dk, dv)
+    assert bits_equal(S, (S0 * np.float32(0.75)).astype(np.float32))
+    np.testing.assert_allclose(o, (S0m.astype(np.float64) * 0.75).T @ q, rtol=1e-5)
+    # decay = 0: S = beta k (x) v, o = beta (k.q) v
+    S, o = orc.delta_rule_head(S0, kk, v, q, 0.4, 0.0, dk, dv)
+    np.testing.assert_allclose(S.reshape(dk, dv), 0.4 * np.outer(kk, v), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(o, 0.4 * float(kk @ q) * v, rtol=1e-5, atol=1e-6)
+
+
+def _delta_rule_f64(S, k, v, q, beta, decay):
+    S = S * decay
+    kv = S.T @ k
+    S = S + np.outer(k, (v - kv) * beta)
+    return S, S.T @ q
+
+
+def test_delta_rule_brute_force_f64():
+    rs = np.random.RandomState(6)
+    for d in (2, 3, 5, 8, 32, 128):
+        S0 = rs.randn(d, d)
+        k, v, q = rs.randn(d), rs.randn(d), rs.randn(d)
+        k /= np.linalg.norm(k)
+        S, o = orc.delta_rule_head(S0.astype(np.float32).ravel(), k.astype(np.float32),
+                                   v.astype(np.float32), q.astype(np.float32), 0.6, 0.9, d, d)
+        S2, o2 = _delta_rule_f64(S0.astype(np.float32).astype(np.float64),
+                                 k.astype(np.float32).astype(np.float64),
+                                 v.astype(np.float32).astype(np.float64),
+                                 q.astype(np.float32).astype(np.float64), 0.6, 0.9)
+        np.testing.assert_allclose(S.reshape(d, d), S2, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(o, o2, rtol=1e-4, atol=1e-4 * np.abs(S2).sum() / d)
+
+
+def _unpack(d, name):
+    B, T, Hk, Hv, dk, dv, chunk = (int(x) for x in d[f"{name}_dims"])
+    return (d[f"{name}_q"], d[f"{name}_k"], d[f"{name}_v"], d[f"{name}_g"],
+            d[f"{name}_beta"], d[f"{name}_S0"], B, T, Hk, Hv, dk, dv, chunk)
+
+
+def test_decode_vs_hf_recurrent(golden):
+    d = golden("hf_gdr.npz")
+    for name in ("rc_step", "rc_multi"):
+        q, k, v, g, beta, S0, B, T, Hk, Hv, dk, dv, _ = _unpack(d, name)
+        S = S0.copy()
+        o = np.empty((B, T, Hv, dv), np.float32)
+        for t in range(T):
+            S, ot = orc.delta_rule_decode(
+                S, np.ascontiguousarray(q[:, t]), np.ascontiguousarray(k[:, t]),
+                np.ascontiguousarray(v[:, t]), np.ascontiguousarray(g[:, t]),
+                np.ascontiguousarray(beta[:, t]), B, Hv, Hk, dk, dv, 1.0 / math.sqrt(dk))
+            o[:, t] = ot
+        np.testing.assert_allclose(o, d[f"{name}_o"], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(S, d[f"{name}_S"], rtol=1e-5, atol=1e-6)
+
+
+def test_decode_unscaled_equals_reference_loop():
+    """q_scale=1 is the reference's ref_delta_rule looped over heads, with
+    v-head h reading k-head h // (Hv/Hk)."""
+    rs = np.random.RandomState(8)
+    B, Hv, Hk, dk, dv = 2, 4, 2, 8, 8
+    S0 = rs.randn(B, Hv, dk, dv).astype(np.float32)
+    q, k = rs.randn(B, Hk, dk).astype(np.float32), rs.randn(B, Hk, dk).astype(np.float32)
+    v = rs.randn(B, Hv, dv).astype(np.float32)
+    g, beta = -rs.rand(B, Hv).astype(np.float32), rs.rand(B, Hv).astype(np.float32)
+    S, o = orc.delta_rule_decode(S0, q, k, v, g, beta, B, Hv, Hk, dk, dv, 1.0)
+    import ctypes
+    expf = ctypes.CDLL("libm.so.6").expf
+    expf.restype, expf.argtypes = ctypes.c_float, [ctypes.c_float]
+    for b in range(B):
+        for h in range(Hv):
+            Sh, oh = orc.delta_rule_head(S0[b, h].ravel(), k[b, h // 2], v[b, h], q[b, h // 2],
+                                         float(beta[b, h]), expf(float(g[b, h])),
+                                         dk, dv)
+            assert bits_equal(Sh, S[b, h].ravel()) and bits_equal(oh, o[b, h])
+
+
+# --------------------------------------------------------------------------
+# Chunkwise prefill
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("precision", ["f32", "f64"])
+def test_chunk_vs_hf(golden, precision):
+    d = golden("hf_gdr.npz")
+    for name in ("ck_small", "ck_tail", "ck_b2"):
+        q, k, v, g, beta, S0, B, T, Hk, Hv, dk, dv, chunk = _unpack(d, name)
+        o, S = orc.chunk_gdr(q, k, v, g, beta, S0, B, T, Hv, Hk, dk, dv, chunk,
+                             precision=precision)
+        scale_o = np.abs(d[f"{name}_o"]).max()
+        np.testing.assert_allclose(o, d[f"{name}_o"], rtol=1e-4, atol=2e-5 * scale_o)
+        np.testing.assert_allclose(S, d[f"{name}_S"], rtol=1e-4, atol=2e-5 * np.abs(S).max())
+
+
+def test_chunk_equals_stepped_recurrence():
+    """The WY chunk form and T single-token steps compute the same recurrence
+    (exact in real arithmetic); in double they agree to ~1e-6."""
+    from tests.golden.gen_golden import _inputs
+    rs = np.random.RandomState(9)
+    B, T, Hk, Hv, dk, dv = 1, 70, 1, 2, 16, 16
+    q, k, v, g, beta, S0 = _inputs(rs, B, T, Hk, Hv, dk, dv)
+    oc, Sc = orc.chunk_gdr(q, k, v, g, beta, S0, B, T, Hv, Hk, dk, dv, 32, precision="f64")
+    S = S0.copy()
+    for t in range(T):
+        S, ot = orc.delta_rule_decode(
+            S, np.ascontiguousarray(q[:, t]), np.ascontiguousarray(k[:, t]),
+            np.ascontiguousarray(v[:, t]), np.ascontiguousarray(g[:, t]),
+            np.ascontiguousarray(beta[:, t]), B, Hv, Hk, dk, dv, 1.0 / math.sqrt(dk))
+        np.testing.assert_allclose(oc[:, t], ot, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(Sc, S, rtol=1e-4, atol=1e-5)
+
+
+def test_chunk_state_carry_two_calls():
+    """Splitting at a chunk boundary and carrying S gives bit-identical
+    results (same chunks, same operation order)."""
+    from tests.golden.gen_golden import _inputs
+    rs = np.random.RandomState(10)
+    B, T, Hk, Hv, dk, dv, C = 1, 96, 1, 2, 16, 16, 16
+    q, k, v, g, beta, S0 = _inputs(rs, B, T, Hk, Hv, dk, dv)
+    o, S = orc.chunk_gdr(q, k, v, g, beta, S0, B, T, Hv, Hk, dk, dv, C)
+    T1 = 48
+    sl = [lambda x, a=a, b=b: np.ascontiguousarray(x[:, a:b]) for a, b in ((0, T1), (T1, T))]
+    o1, S1 = orc.chunk_gdr(*(sl[0](x) for x in (q, k, v, g, beta)), S0, B, T1, Hv, Hk, dk, dv, C)
+    o2, S2 = orc.chunk_gdr(*(sl[1](x) for x in (q, k, v, g, beta)), S1, B, T - T1, Hv, Hk, dk,
+                           dv, C)
+    assert bits_equal(np.concatenate([o1, o2], axis=1), o) and bits_equal(S2, S)
+
+
+def test_chunk_gate_sensitivity():
+    """A dropped decay mask or a dropped beta would be caught: perturbing
+    either input changes the HF-pinned output well beyond the tolerance."""
+    from tests.golden.gen_golden import _inputs
+    rs = np.random.RandomState(11)
+    B, T, Hk, Hv, dk, dv = 1, 40, 1, 1, 8, 8
+    q, k, v, g, beta, S0 = _inputs(rs, B, T, Hk, Hv, dk, dv)
+    o, _ = orc.chunk_gdr(q, k, v, g, beta, S0, B, T, Hv, Hk, dk, dv, 16)
+    o_nog, _ = orc.chunk_gdr(q, k, v, np.zeros_like(g), beta, S0, B, T, Hv, Hk, dk, dv, 16)
+    o_nob, _ = orc.chunk_gdr(q, k, v, g, np.ones_like(beta), S0, B, T, Hv, Hk, dk, dv, 16)
+    assert np.abs(o - o_nog).max() > 1e-2 * np.abs(o).max()
+    assert np.abs(o - o_nob).max() > 1e-2 * np.abs(o).max()
