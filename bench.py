@@ -1,0 +1,318 @@
+#!/usr/bin/env python3
+"""Benchmark of the GDN hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline workload: one decode step of the
+single-token gated delta rule across 24 GDN layers, batch 64 sequences,
+32 value heads / 16 key heads, d_k = d_v = 128, fp32 state.  A step is 24
+launches of the decode kernel (one per layer, each with its own 128 MiB
+state and inputs), all resident in HBM before timing starts.
+value = 64 tokens / step time.
+
+The JSON line also carries:
+  roofline      the decode kernel: algorithmic bytes per launch / its mean
+                launch time from HIP events on the launch stream, vs 8 TB/s
+  cpu_baseline  the CPU oracle (oracle/, OpenMP over (sequence, head)) on a
+                bounded sample of the same step, on this host's cores
+  secondary     prefill (config 3, T=16K), conv+SiLU (config 1) and
+                cumulative decay ([4096][8192]) throughput and roofline
+Synthetic inputs with the BASELINE distributions; random state.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+# Decode
+B_DEC, HV, HK, DK, DV, LAYERS = 64, 32, 16, 128, 128, 24
+DEC_BYTES = (2 * B_DEC * HV * DK * DV * 4            # state read + write
+             + 2 * B_DEC * HK * DK * 4               # q, k
+             + 2 * B_DEC * HV * DV * 4               # v, o
+             + 2 * B_DEC * HV * 4)                   # g, beta
+assert DEC_BYTES == 271_597_568
+# Prefill: dense-GEMM FLOPs per (chunk, value head)
+PF_T = 16384
+PF_FLOP_PER_CHUNK_HEAD = 5 * (2 * 64 * 64 * 128) + 3 * (2 * 64 * 128 * 128)
+assert PF_FLOP_PER_CHUNK_HEAD == 11_534_336
+# Conv and decay
+CONV_T, CONV_C = 4096, 8192
+CONV_BYTES = (2 * CONV_T * CONV_C + 4 * CONV_C + 2 * 3 * CONV_C) * 4
+assert CONV_BYTES == 268_763_136
+DEC_T, DEC_C = 4096, 8192
+DECAY_BYTES = 2 * DEC_T * DEC_C * 4
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def profile_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by a copy-kernel calibration), when committed."""
+    p = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+class Timer:
+    """HIP-event timing on torch's current stream (the stream every entry
+    point is called with)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time_ms(self, fn, reps):
+        t = self.torch
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        t.cuda.synchronize()
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / reps
+
+    def per_launch_ms(self, fns):
+        """Mean duration of each launch in `fns`, bracketed by its own events."""
+        t = self.torch
+        evs = [(t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)) for _ in fns]
+        t.cuda.synchronize()
+        for (s, e), fn in zip(evs, fns):
+            s.record()
+            fn()
+            e.record()
+        t.cuda.synchronize()
+        return [s.elapsed_time(e) for s, e in evs]
+
+
+def bench_decode(L, ob, torch, steps, warmup, timer):
+    from tests.gdn_inputs import decode_inputs
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    qs = 1.0 / math.sqrt(DK)
+    layers = []
+    for l in range(LAYERS):
+        S, q, k, v, g, beta = decode_inputs(1000 + l, B_DEC, HV, HK, DK, DV)
+        t = {n: torch.from_numpy(a).cuda() for n, a in
+             dict(S=S, q=q, k=k, v=v, g=g, beta=beta).items()}
+        t["o"] = torch.empty((B_DEC, HV, DV), dtype=torch.float32, device="cuda")
+        layers.append(t)
+    torch.cuda.synchronize()
+    fn = L.kai_run_gdn_delta_rule_decode_f32_hip
+
+    def launch(t):
+        rc = fn(t["S"].data_ptr(), t["q"].data_ptr(), t["k"].data_ptr(), t["v"].data_ptr(),
+                t["g"].data_ptr(), t["beta"].data_ptr(), t["o"].data_ptr(), B_DEC, HV, HK, DK,
+                DV, qs, stream)
+        if rc:
+            ob.check(rc, "decode")
+
+    def step():
+        for t in layers:
+            launch(t)
+
+    for _ in range(warmup):
+        step()
+    ms_step = timer.time_ms(step, steps)
+    # per-launch durations of the decode kernel over the same number of steps
+    durs = []
+    for _ in range(steps):
+        durs += timer.per_launch_ms([lambda t=t: launch(t) for t in layers])
+    kern_ms = float(np.mean(durs))
+    return ms_step, kern_ms, layers
+
+
+def cpu_decode_baseline(budget_s=12.0):
+    """The oracle (OpenMP over (sequence, head)) on the same per-layer step;
+    runs whole layers until the budget is spent, reports tokens/s of a
+    24-layer step."""
+    from oracle import oracle as orc
+    from tests.gdn_inputs import decode_inputs
+    S, q, k, v, g, beta = decode_inputs(1000, B_DEC, HV, HK, DK, DV)
+    orc.delta_rule_decode(S, q, k, v, g, beta, B_DEC, HV, HK, DK, DV, 1 / math.sqrt(DK))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        S, _ = orc.delta_rule_decode(S, q, k, v, g, beta, B_DEC, HV, HK, DK, DV,
+                                     1 / math.sqrt(DK))
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 240:
+            break
+    per_layer = el / n
+    return {"value": round(B_DEC / (per_layer * LAYERS), 2), "unit": "tokens/s",
+            "cores": orc.num_threads(), "kind": "port",
+            "sample": f"{n} layer-steps of B=64 x 32 heads x 128x128 fp32 "
+                      f"({n / LAYERS:.1f} full 24-layer steps), {el:.1f} s"}
+
+
+def bench_prefill(L, ob, torch, timer, reps=5):
+    from tests.gdn_inputs import bf16_bits, prefill_inputs
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    q, k, v, g, beta, S = prefill_inputs(7, 1, PF_T, HV, HK)
+    dq, dk_, dv_ = (torch.from_numpy(bf16_bits(x).view(np.int16)).cuda() for x in (q, k, v))
+    dg, db, dS = (torch.from_numpy(x).cuda() for x in (g, beta, S))
+    do = torch.empty((1, PF_T, HV, 128), dtype=torch.int16, device="cuda")
+    fn = L.kai_run_gdn_chunk_delta_rule_bf16_f32_hip
+
+    def run():
+        rc = fn(dq.data_ptr(), dk_.data_ptr(), dv_.data_ptr(), dg.data_ptr(), db.data_ptr(),
+                do.data_ptr(), dS.data_ptr(), 1, PF_T, HV, HK, 1 / math.sqrt(128), stream)
+        if rc:
+            ob.check(rc, "prefill")
+
+    run()
+    ms = timer.time_ms(run, reps)
+    flop = PF_FLOP_PER_CHUNK_HEAD * (PF_T // 64) * HV
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {"workload": "chunked WY prefill, B=1 T=16384 Hv=32 Hk=16 d=128 bf16 in, fp32 state",
+            "tokens_per_s": round(PF_T / (ms * 1e-3), 1), "ms": round(ms, 4),
+            "achieved_tflops": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+
+
+def cpu_prefill_baseline(budget_s=10.0):
+    from oracle import oracle as orc
+    from tests.gdn_inputs import prefill_inputs
+    T = 256
+    q, k, v, g, beta, S = prefill_inputs(7, 1, T, HV, HK)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        orc.chunk_gdr(q, k, v, g, beta, S, 1, T, HV, HK, 128, 128, 64)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s:
+            break
+    return {"value": round(n * T / el, 1), "unit": "tokens/s", "cores": orc.num_threads(),
+            "kind": "port", "sample": f"{n} x T={T} (32 heads), {el:.1f} s"}
+
+
+def bench_stream(L, ob, torch, timer, reps=20):
+    from tests.gdn_inputs import conv_inputs
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    x, w, h = conv_inputs(1, CONV_T, CONV_C)
+    dx, dw, dh = (torch.from_numpy(a).cuda() for a in (x, w, h))
+    do = torch.empty(CONV_T * CONV_C, dtype=torch.float32, device="cuda")
+
+    def conv():
+        rc = L.kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip(dx.data_ptr(), dw.data_ptr(),
+                                                          do.data_ptr(), dh.data_ptr(), CONV_T,
+                                                          CONV_C, stream)
+        if rc:
+            ob.check(rc, "conv")
+
+    conv()
+    conv_ms = float(np.mean(timer.per_launch_ms([conv] * reps)))
+    rs = np.random.RandomState(2)
+    gl = -np.log1p(np.exp(rs.randn(DEC_T * DEC_C))) * np.exp(rs.uniform(-2, 0, DEC_T * DEC_C))
+    da = torch.from_numpy(np.exp(gl).astype(np.float32)).cuda()
+    dd = torch.empty(DEC_T * DEC_C, dtype=torch.float32, device="cuda")
+
+    def decay():
+        rc = L.kai_run_gdn_cumdecay_f32_hip(da.data_ptr(), dd.data_ptr(), DEC_T, DEC_C, stream)
+        if rc:
+            ob.check(rc, "cumdecay")
+
+    decay()
+    dec_ms = float(np.mean(timer.per_launch_ms([decay] * reps)))
+    if L.kai_gdn_hip_check_device_error() != 0:
+        raise RuntimeError("cumdecay look-back watchdog fired")
+    conv_gbs = CONV_BYTES / (conv_ms * 1e-3) / 1e9
+    dec_gbs = DECAY_BYTES / (dec_ms * 1e-3) / 1e9
+    return (
+        {"workload": "causal dwconv1d K=4 + SiLU, T=4096 C=8192 fp32", "us": round(conv_ms * 1e3, 2),
+         "tokens_per_s": round(CONV_T / (conv_ms * 1e-3), 1), "achieved_gbs": round(conv_gbs, 1),
+         "hbm_frac": round(conv_gbs / HBM_PEAK_GBS, 4)},
+        {"workload": "cumulative decay [4096][8192] fp32", "us": round(dec_ms * 1e3, 2),
+         "achieved_gbs": round(dec_gbs, 1), "hbm_frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
+    )
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="skip prefill/conv/decay lines")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the GDN path has no cross-GPU "
+              f"communication; --gpus {args.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import orionsbelt_amd as ob
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    L = ob.lib()
+    ob.check(L.kai_gdn_hip_init(), "init")
+    timer = Timer(torch)
+
+    log("decode: 24 layers x B=64 ...")
+    ms_step, kern_ms, _ = bench_decode(L, ob, torch, args.steps, args.warmup, timer)
+    achieved = DEC_BYTES / (kern_ms * 1e-3) / 1e9
+    log(f"decode: {ms_step:.3f} ms/step, kernel {kern_ms * 1e3:.1f} us ({achieved:.0f} GB/s)")
+
+    secondary = {}
+    if not args.no_secondary:
+        log("prefill T=16K ...")
+        secondary["prefill"] = bench_prefill(L, ob, torch, timer)
+        log(f"prefill: {secondary['prefill']}")
+        log("conv / decay ...")
+        secondary["conv"], secondary["cumdecay"] = bench_stream(L, ob, torch, timer)
+        log(f"conv: {secondary['conv']}\ncumdecay: {secondary['cumdecay']}")
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle) ...")
+        cpu = cpu_decode_baseline()
+        log(f"cpu: {cpu}")
+        if not args.no_secondary:
+            secondary["prefill"]["cpu_baseline"] = cpu_prefill_baseline()
+
+    line = {
+        "metric": "GDN decode tok/s (B=64, 24 layers, 1 GPU) + % of HBM roofline",
+        "value": round(B_DEC / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (BASELINE distributions, random state)",
+        "config": {"workload": "gated delta-rule decode step: 24 GDN layers, batch 64, "
+                               "Hv=32 Hk=16 d_k=d_v=128, fp32 state (BASELINE configs[1])",
+                   "batch": B_DEC, "layers": LAYERS, "num_v_heads": HV, "num_k_heads": HK,
+                   "head_dim": DK},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profile_traffic("delta_decode_kernel"),
+                     "kernel": "delta_decode_kernel<128,128,f32>",
+                     "bytes_per_launch": DEC_BYTES, "launch_us": round(kern_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,150 @@
+/*
+ * kai_gdn_hip.h -- device-pointer entry points of libkai_gdn_hip.so (gfx950).
+ *
+ * The four kai_run_gdn_* symbols of include/kai/ukernels/gdn/ are the
+ * drop-in boundary (host or device pointers, synchronous).  The functions
+ * below are the stream-ordered forms a GPU caller uses: every pointer is
+ * device memory, work is enqueued on `stream` (a hipStream_t; NULL = the
+ * null stream) and the call returns without waiting.  They return 0 on
+ * success or a hipError_t code; kai_gdn_hip_error_string() names it.
+ * Argument checks happen before anything is enqueued: on an error nothing
+ * is written.
+ *
+ * Names keep the kai pattern kai_run_<op>_<types>_<isa>
+ * (kleidiai_submission/README.md:122-142) with isa = hip.
+ */
+#ifndef KAI_GDN_HIP_H
+#define KAI_GDN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- kai ukernels, device pointers -------------------------------------- */
+
+/* Replaces kai_run_gdn_cumdecay_f32_sve
+ * (kleidiai_submission/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.h:33-34). */
+int kai_run_gdn_cumdecay_f32_hip(const float *a, float *decay, size_t seq,
+                                 size_t channels, void *stream);
+
+/* Replaces kai_run_gdn_gated_scan_f32_sve (kai_gdn_gated_scan_f32_sve.h:35-36). */
+int kai_run_gdn_gated_scan_f32_hip(const float *g, const float *x, float *s,
+                                   float *state, size_t seq, size_t channels,
+                                   void *stream);
+
+/* Replaces kai_run_gdn_causal_dwconv1d_f32_k4_sve
+ * (kai_gdn_causal_dwconv1d_f32_k4_sve.h:39-41). */
+int kai_run_gdn_causal_dwconv1d_f32_k4_hip(const float *in, const float *w,
+                                           float *out, float *hist, size_t seq,
+                                           size_t channels, void *stream);
+
+/* The same conv with the SiLU epilogue out = y / (1 + exp(-y)) fused, as HF
+ * Qwen3.5 applies after the depthwise conv (transformers
+ * modeling_qwen3_5.py:222-239, activation="silu").  No reference kai symbol. */
+int kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip(const float *in, const float *w,
+                                                float *out, float *hist, size_t seq,
+                                                size_t channels, void *stream);
+
+/* Replaces kai_run_gdn_gemv_f32_f32_f32_1x4_neon
+ * (kai_gdn_gemv_f32_f32_f32_1x4_neon.h:40-42). */
+int kai_run_gdn_gemv_f32_f32_f32_hip(const float *a, const float *b, float *c,
+                                     size_t k, size_t n, void *stream);
+
+/* ---- mixed-precision diagonal kernels (gdn_sve.h:56-72) ------------------
+ * fp16 values are IEEE binary16 bit patterns, bf16 values the upper half of a
+ * binary32 (round to nearest even), both passed as uint16_t.  fp32
+ * accumulation; only the narrow array is narrowed (gdn_sve.c:433-441). */
+int kai_run_gdn_cumdecay_f16_hip(const float *a, uint16_t *decay, size_t seq,
+                                 size_t channels, void *stream);
+int kai_run_gdn_cumdecay_bf16_hip(const float *a, uint16_t *decay, size_t seq,
+                                  size_t channels, void *stream);
+int kai_run_gdn_gated_scan_f16_hip(const float *g, const float *x, float *s,
+                                   uint16_t *state, size_t seq, size_t channels,
+                                   void *stream);
+int kai_run_gdn_gated_scan_bf16_hip(const float *g, const float *x, float *s,
+                                    uint16_t *state, size_t seq, size_t channels,
+                                    void *stream);
+
+/* ---- matrix-state gated delta rule, single-token decode ------------------
+ * Replaces the OpenCL gdn_delta_rule_decode (gpu/gdn_gpu_kernels.cl:158-206)
+ * and its host oracle ref_delta_rule (gpu/gdn_gpu_validate.c:100-118), with
+ * per-(sequence, value-head) gates as HF torch_recurrent_gated_delta_rule
+ * uses them (modeling_qwen3_5.py:331-380).  For every sequence b and value
+ * head h (key head kh = h / (num_v_heads / num_k_heads)):
+ *     S *= exp(g[b][h]);  kv = S^T k;  delta = (v - kv) * beta[b][h];
+ *     S += k (x) delta;   o = S^T (q * q_scale)
+ * Layouts: S [batch][num_v_heads][head_k_dim][head_v_dim] (in/out),
+ * q,k [batch][num_k_heads][head_k_dim], v,o [batch][num_v_heads][head_v_dim],
+ * g,beta [batch][num_v_heads].  q and k are used as given (L2-normalise
+ * them beforehand, as HF does with use_qk_l2norm_in_kernel).
+ * head_k_dim, head_v_dim in {32, 64, 128}; num_v_heads % num_k_heads == 0. */
+int kai_run_gdn_delta_rule_decode_f32_hip(float *S, const float *q, const float *k,
+                                          const float *v, const float *g,
+                                          const float *beta, float *o, int batch,
+                                          int num_v_heads, int num_k_heads,
+                                          int head_k_dim, int head_v_dim,
+                                          float q_scale, void *stream);
+
+/* Same step with S stored as IEEE fp16 (bit patterns): widened to fp32 on
+ * load, narrowed (round to nearest even) on store.  Halves the state
+ * footprint and the bytes the step moves. */
+int kai_run_gdn_delta_rule_decode_f16state_hip(uint16_t *S, const float *q,
+                                               const float *k, const float *v,
+                                               const float *g, const float *beta,
+                                               float *o, int batch, int num_v_heads,
+                                               int num_k_heads, int head_k_dim,
+                                               int head_v_dim, float q_scale,
+                                               void *stream);
+
+/* ---- chunkwise (WY) gated delta rule, prefill ----------------------------
+ * The algorithm of HF torch_chunk_gated_delta_rule (modeling_qwen3_5.py:
+ * 248-328) with chunk size 64: per chunk, the UT transform
+ * T = (I + tril(beta K K^T * Gamma, -1))^-1, W = T (beta K e^G),
+ * U = T (beta V) and the masked Q K^T run in parallel over chunks; the state
+ * recurrence across chunks is sequential.  q,k,v bf16 (bit patterns),
+ * products on bf16 MFMA with fp32 accumulation, fp32 state.
+ * Layouts (token-major, HF's [B, T, H, D]):
+ *   q,k [batch][seq_len][num_k_heads][128]   v [batch][seq_len][num_v_heads][128]
+ *   g,beta [batch][seq_len][num_v_heads] fp32 (g = log-gate, beta = write gate)
+ *   o [batch][seq_len][num_v_heads][128] bf16
+ *   S [batch][num_v_heads][128][128] fp32: initial state in, final state out.
+ * seq_len need not be a multiple of 64.  head_k_dim = head_v_dim = 128. */
+int kai_run_gdn_chunk_delta_rule_bf16_f32_hip(const uint16_t *q, const uint16_t *k,
+                                              const uint16_t *v, const float *g,
+                                              const float *beta, uint16_t *o,
+                                              float *S, int batch, int seq_len,
+                                              int num_v_heads, int num_k_heads,
+                                              float q_scale, void *stream);
+
+/* Same prefill with S stored as IEEE fp16 bit patterns (widened on entry,
+ * fp32 across all chunks, narrowed once on exit). */
+int kai_run_gdn_chunk_delta_rule_bf16_f16state_hip(const uint16_t *q,
+                                                   const uint16_t *k,
+                                                   const uint16_t *v, const float *g,
+                                                   const float *beta, uint16_t *o,
+                                                   uint16_t *S, int batch,
+                                                   int seq_len, int num_v_heads,
+                                                   int num_k_heads, float q_scale,
+                                                   void *stream);
+
+/* ---- library ------------------------------------------------------------ */
+
+/* Initialise the HIP runtime state of the current device (optional; every
+ * entry point does it lazily).  Returns 0 or a hipError_t code. */
+int kai_gdn_hip_init(void);
+
+/* Text for a code returned by the functions above. */
+const char *kai_gdn_hip_error_string(int code);
+
+/* Non-zero when a scan kernel's bounded wait for a predecessor tile timed
+ * out on the current device since the last call (the result of that launch
+ * is invalid).  Synchronises the device, then clears the flag. */
+int kai_gdn_hip_check_device_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KAI_GDN_HIP_H */

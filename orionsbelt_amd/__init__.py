@@ -1,0 +1,111 @@
+"""orionsbelt_amd -- MI355X (gfx950) implementation of the OrionsBelt GDN hot path.
+
+The product is the C-ABI library ``orionsbelt_amd/lib/libkai_gdn_hip.so``
+(declared in ``include/kai/ukernels/gdn/*.h`` and ``include/kai_gdn_hip.h``).
+This module only loads it through ctypes so Python tests and the benchmark
+can call the same entry points a C caller would.  There is no fallback: if the
+library is missing, :func:`lib` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "libkai_gdn_hip.so")
+
+# Every symbol the headers in include/ declare.
+KAI_SYMBOLS = (
+    "kai_run_gdn_cumdecay_f32_sve",
+    "kai_run_gdn_gated_scan_f32_sve",
+    "kai_run_gdn_causal_dwconv1d_f32_k4_sve",
+    "kai_run_gdn_gemv_f32_f32_f32_1x4_neon",
+)
+HIP_SYMBOLS = (
+    "kai_run_gdn_cumdecay_f32_hip",
+    "kai_run_gdn_gated_scan_f32_hip",
+    "kai_run_gdn_causal_dwconv1d_f32_k4_hip",
+    "kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip",
+    "kai_run_gdn_gemv_f32_f32_f32_hip",
+    "kai_run_gdn_cumdecay_f16_hip",
+    "kai_run_gdn_cumdecay_bf16_hip",
+    "kai_run_gdn_gated_scan_f16_hip",
+    "kai_run_gdn_gated_scan_bf16_hip",
+    "kai_run_gdn_delta_rule_decode_f32_hip",
+    "kai_run_gdn_delta_rule_decode_f16state_hip",
+    "kai_run_gdn_chunk_delta_rule_bf16_f32_hip",
+    "kai_run_gdn_chunk_delta_rule_bf16_f16state_hip",
+    "kai_gdn_hip_init",
+    "kai_gdn_hip_error_string",
+    "kai_gdn_hip_check_device_error",
+)
+ALL_SYMBOLS = KAI_SYMBOLS + HIP_SYMBOLS
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_i = ctypes.c_int
+_f = ctypes.c_float
+
+_SIGS = {
+    "kai_run_gdn_cumdecay_f32_sve": (None, [_vp, _vp, _sz, _sz]),
+    "kai_run_gdn_gated_scan_f32_sve": (None, [_vp, _vp, _vp, _vp, _sz, _sz]),
+    "kai_run_gdn_causal_dwconv1d_f32_k4_sve": (None, [_vp, _vp, _vp, _vp, _sz, _sz]),
+    "kai_run_gdn_gemv_f32_f32_f32_1x4_neon": (None, [_vp, _vp, _vp, _sz, _sz]),
+    "kai_run_gdn_cumdecay_f32_hip": (_i, [_vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_cumdecay_f16_hip": (_i, [_vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_cumdecay_bf16_hip": (_i, [_vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_gated_scan_f32_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_gated_scan_f16_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_gated_scan_bf16_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_causal_dwconv1d_f32_k4_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_gemv_f32_f32_f32_hip": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_delta_rule_decode_f32_hip":
+        (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
+    "kai_run_gdn_delta_rule_decode_f16state_hip":
+        (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
+    "kai_run_gdn_chunk_delta_rule_bf16_f32_hip":
+        (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
+    "kai_run_gdn_chunk_delta_rule_bf16_f16state_hip":
+        (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
+    "kai_gdn_hip_init": (_i, []),
+    "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
+    "kai_gdn_hip_check_device_error": (_i, []),
+}
+
+_lib = None
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load libkai_gdn_hip.so (built by ``python -m orionsbelt_amd.build``).
+
+    torch is imported first when it is installed so that the library binds to
+    the same HIP runtime (libamdhip64.so.7) torch already loaded."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(
+            f"{LIB_PATH} not built: run `python -m orionsbelt_amd.build` (no CPU fallback exists)")
+    try:
+        import torch  # noqa: F401  (shares the HIP runtime)
+    except ImportError:
+        pass
+    L = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def check(rc: int, what: str = "") -> None:
+    """Raise HipError for a non-zero return code of a *_hip entry point."""
+    if rc != 0:
+        msg = lib().kai_gdn_hip_error_string(rc).decode()
+        raise HipError(f"{what}: {msg} ({rc})")

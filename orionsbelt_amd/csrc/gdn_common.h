@@ -1,0 +1,58 @@
+// gdn_common.h -- device helpers shared by the GDN kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define GDN_DEV __device__ __forceinline__
+
+// ---- narrow formats --------------------------------------------------------
+
+// float -> bfloat16 bits, round to nearest even by bias-and-truncate: the
+// same rule as the reference's f32_to_bf16_rne (gdn_sve.c:81-87).
+GDN_DEV uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+GDN_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// IEEE binary16 <-> binary32 with the hardware converts (v_cvt_f16_f32 rounds
+// to nearest even, keeps subnormals).
+GDN_DEV uint16_t f32_to_f16_rne(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+GDN_DEV float f16_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+
+// ---- MFMA: v_mfma_f32_16x16x32_bf16 -----------------------------------------
+// Operand layout (lane l, g = l >> 4, r = l & 15):
+//   A fragment: A[r][8g + 0..7]     (16 x 32, row r, 8 consecutive k)
+//   B fragment: B[8g + 0..7][r]     (32 x 16, column r, 8 consecutive k)
+//   C fragment: C[4g + 0..3][r]     (16 x 16, column r, 4 consecutive rows)
+// The k index inside a 32-wide step is a pure reduction index: any
+// permutation applied identically to A and B leaves the product unchanged.
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+GDN_DEV f32x4_t mfma_16x16x32_bf16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Pack 8 floats into a bf16x8 fragment (round to nearest even).
+GDN_DEV bf16x8_t pack_bf16x8(const float *f) {
+    u32x4_t w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16_rne(f[2 * i]) |
+               ((uint32_t)f32_to_bf16_rne(f[2 * i + 1]) << 16);
+    return __builtin_bit_cast(bf16x8_t, w);
+}
+
+GDN_DEV bf16x8_t as_bf16x8(u32x4_t w) { return __builtin_bit_cast(bf16x8_t, w); }
+
+GDN_DEV f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }

@@ -1,0 +1,68 @@
+// gdn_internal.h -- launchers shared between the kernel files and the C-ABI
+// layer (kai_shim.hip).  Not installed; callers use include/kai_gdn_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gdn {
+
+// Narrow storage formats of the mixed-precision variants.
+enum Narrow : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// ---- streaming kernels (gdn_stream.hip) ------------------------------------
+
+hipError_t launch_conv_k4(const float *in, const float *w, float *out, float *hist,
+                          size_t seq, size_t ch, bool silu, hipStream_t st);
+
+hipError_t launch_gemv(const float *a, const float *b, float *c, size_t k, size_t n,
+                       hipStream_t st);
+
+// Scratch of the decoupled look-back scan: a monotonically increasing tile
+// counter, three status arrays of n_row_tiles * channels 64-bit words and an
+// error word.  Owned per device by the C-ABI layer, which serialises scan
+// launches and advances `counter_base` and `epoch` itself.
+struct ScanScratch {
+    unsigned long long *counter;
+    unsigned long long *incl;
+    unsigned long long *aggG;
+    unsigned long long *aggX;
+    uint32_t *err;
+    size_t words;  // capacity of each status array
+};
+
+constexpr int kScanTileT = 64;      // rows per tile
+constexpr int kScanThreads = 256;   // channels per tile (one per thread)
+
+inline size_t scan_row_tiles(size_t seq) { return (seq + kScanTileT - 1) / kScanTileT; }
+inline size_t scan_col_tiles(size_t ch) { return (ch + kScanThreads - 1) / kScanThreads; }
+
+// mode 0: cumdecay (out = prefix product of g; `narrow` applies to out)
+// mode 1: gated scan (s fp32; `narrow` applies to state)
+hipError_t launch_lookback_scan(int mode, int narrow, const float *g, const float *x,
+                                void *out, void *state, size_t seq, size_t ch,
+                                const ScanScratch &scr, unsigned long long counter_base,
+                                uint32_t epoch, hipStream_t st);
+
+// ---- decode (gdn_decode.hip) ------------------------------------------------
+
+hipError_t launch_delta_decode(int narrow_state, void *S, const float *q, const float *k,
+                               const float *v, const float *g, const float *beta, float *o,
+                               int B, int Hv, int Hk, int dk, int dv, float q_scale,
+                               hipStream_t st);
+
+// ---- chunked prefill (gdn_chunk.hip) ----------------------------------------
+
+constexpr int kChunk = 64;
+constexpr int kHeadDim = 128;
+
+// Bytes of device workspace the prefill needs for one call.
+size_t chunk_workspace_bytes(int B, int T, int Hv);
+
+hipError_t launch_chunk_prefill(int narrow_state, const uint16_t *q, const uint16_t *k,
+                                const uint16_t *v, const float *g, const float *beta,
+                                uint16_t *o, void *S, int B, int T, int Hv, int Hk,
+                                float q_scale, void *workspace, hipStream_t st);
+
+}  // namespace gdn

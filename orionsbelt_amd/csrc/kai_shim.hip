@@ -1,0 +1,457 @@
+// kai_shim.hip -- the C ABI of libkai_gdn_hip.so.
+//
+// Two layers:
+//  * kai_run_gdn_*_sve / _neon: the reference kai symbols with identical
+//    prototypes (kleidiai_submission/kai/ukernels/gdn/*.h).  Synchronous;
+//    each pointer may be host or device memory (hipPointerGetAttributes):
+//    device pointers are used in place, host buffers are copied in/out.
+//    The reference has no error channel (void returns; fatal conditions
+//    print and exit(1), test_kai_gdn.c:38-42), so a HIP failure here prints
+//    the failing call and exits(1).  seq==0 / channels==0 return before any
+//    HIP call and write nothing (test_kai_gdn.c:520-637).
+//  * kai_run_gdn_*_hip: device pointers, stream-ordered, return hipError_t
+//    (include/kai_gdn_hip.h).
+//
+// Per-device state (created lazily under a mutex): an internal stream for
+// the synchronous symbols, staging buffers, the look-back scan scratch and
+// the prefill workspace.  Scan launches are serialised per device (host
+// mutex + an event the next scan waits on) because they share the tile
+// counter and status arrays; every other kernel is free of shared state.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "gdn_internal.h"
+#include "../../include/kai_gdn_hip.h"
+#include "../../include/kai/ukernels/gdn/kai_gdn_causal_dwconv1d_f32_k4_sve.h"
+#include "../../include/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.h"
+#include "../../include/kai/ukernels/gdn/kai_gdn_gated_scan_f32_sve.h"
+#include "../../include/kai/ukernels/gdn/kai_gdn_gemv_f32_f32_f32_1x4_neon.h"
+
+namespace {
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    // grow to at least n bytes; the old contents are not kept
+    hipError_t reserve(size_t n) {
+        if (n <= cap) return hipSuccess;
+        if (p) {
+            hipError_t e = hipFree(p);
+            if (e != hipSuccess) return e;
+            p = nullptr;
+            cap = 0;
+        }
+        size_t want = n < 4096 ? 4096 : n + n / 4;
+        hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) return e;
+        cap = want;
+        return hipSuccess;
+    }
+};
+
+struct DeviceCtx {
+    std::mutex mu;        // serialises scan launches and buffer growth
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    // synchronous-path staging (one buffer per argument slot)
+    DevBuf stage[6];
+    // look-back scan scratch
+    gdn::ScanScratch scan{};
+    size_t scan_words = 0;
+    unsigned long long counter_value = 0;
+    uint32_t epoch = 0;
+    hipEvent_t scan_done = nullptr;
+    bool scan_pending = false;
+    // prefill workspace
+    DevBuf chunk_ws;
+};
+
+std::mutex g_ctx_mu;
+std::vector<DeviceCtx *> g_ctx;
+
+hipError_t get_ctx(DeviceCtx **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    DeviceCtx *c;
+    {
+        std::lock_guard<std::mutex> lk(g_ctx_mu);
+        if ((int)g_ctx.size() <= dev) g_ctx.resize(dev + 1, nullptr);
+        if (!g_ctx[dev]) g_ctx[dev] = new DeviceCtx();
+        c = g_ctx[dev];
+    }
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (!c->ready) {
+        e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) return e;
+        e = hipEventCreateWithFlags(&c->scan_done, hipEventDisableTiming);
+        if (e != hipSuccess) return e;
+        e = hipMalloc(&c->scan.counter, 256);
+        if (e != hipSuccess) return e;
+        e = hipMemset(c->scan.counter, 0, 256);
+        if (e != hipSuccess) return e;
+        c->scan.err = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(c->scan.counter) + 64);
+        c->ready = true;
+    }
+    *out = c;
+    return hipSuccess;
+}
+
+// Grow the three scan status arrays to `words` entries each (zero-filled).
+// Called with c->mu held.  Waits for the previous scan before freeing.
+hipError_t scan_reserve(DeviceCtx *c, size_t words) {
+    if (words <= c->scan_words) return hipSuccess;
+    hipError_t e;
+    if (c->scan_pending) {
+        e = hipEventSynchronize(c->scan_done);
+        if (e != hipSuccess) return e;
+    }
+    if (c->scan.incl) {
+        (void)hipFree(c->scan.incl);
+        c->scan.incl = c->scan.aggG = c->scan.aggX = nullptr;
+        c->scan_words = 0;
+    }
+    size_t want = words < 65536 ? 65536 : words + words / 4;
+    void *p = nullptr;
+    e = hipMalloc(&p, 3 * want * sizeof(unsigned long long));
+    if (e != hipSuccess) return e;
+    e = hipMemset(p, 0, 3 * want * sizeof(unsigned long long));
+    if (e != hipSuccess) return e;
+    c->scan.incl = static_cast<unsigned long long *>(p);
+    c->scan.aggG = c->scan.incl + want;
+    c->scan.aggX = c->scan.aggG + want;
+    c->scan_words = want;
+    c->scan.words = want;
+    c->epoch = 0;  // fresh arrays: restart tags
+    return hipSuccess;
+}
+
+hipError_t run_scan(int mode, int narrow, const float *g, const float *x, void *out,
+                    void *state, size_t seq, size_t ch, hipStream_t st) {
+    if (seq == 0 || ch == 0) return hipSuccess;
+    DeviceCtx *c;
+    hipError_t e = get_ctx(&c);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(c->mu);
+    const size_t nr = gdn::scan_row_tiles(seq), nc = gdn::scan_col_tiles(ch);
+    e = scan_reserve(c, nr * ch);
+    if (e != hipSuccess) return e;
+    if (c->epoch == 0xFFFFFFFFu) {  // tag space exhausted: clear and restart
+        if (c->scan_pending && (e = hipEventSynchronize(c->scan_done)) != hipSuccess) return e;
+        e = hipMemset(c->scan.incl, 0, 3 * c->scan_words * sizeof(unsigned long long));
+        if (e != hipSuccess) return e;
+        c->epoch = 0;
+    }
+    const uint32_t epoch = ++c->epoch;
+    const unsigned long long base = c->counter_value;
+    if (c->scan_pending) {
+        e = hipStreamWaitEvent(st, c->scan_done, 0);
+        if (e != hipSuccess) return e;
+    }
+    e = gdn::launch_lookback_scan(mode, narrow, g, x, out, state, seq, ch, c->scan, base, epoch, st);
+    if (e != hipSuccess) return e;
+    c->counter_value += (unsigned long long)(nr * nc);
+    e = hipEventRecord(c->scan_done, st);
+    if (e != hipSuccess) return e;
+    c->scan_pending = true;
+    return hipSuccess;
+}
+
+// ---- synchronous (kai) path helpers ----------------------------------------
+
+bool is_device_ptr(const void *p) {
+    if (!p) return false;
+    hipPointerAttribute_t a;
+    hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+[[noreturn]] void fatal(const char *what, hipError_t e) {
+    std::fprintf(stderr, "libkai_gdn_hip: %s failed: %s (%d)\n", what, hipGetErrorString(e), (int)e);
+    std::exit(1);
+}
+
+void check(hipError_t e, const char *what) {
+    if (e != hipSuccess) fatal(what, e);
+}
+
+// One argument of a synchronous call: a device view of `bytes` at `host`.
+struct Arg {
+    void *dev = nullptr;
+    const void *src = nullptr;
+    void *dst = nullptr;  // copy back on exit (outputs / in-out)
+    size_t bytes = 0;
+};
+
+// in: copy to device before; out: copy back after.
+Arg stage_arg(DeviceCtx *c, int slot, const void *p, size_t bytes, bool in, bool out) {
+    Arg a;
+    a.bytes = bytes;
+    if (is_device_ptr(p)) {
+        a.dev = const_cast<void *>(p);
+        return a;
+    }
+    check(c->stage[slot].reserve(bytes), "hipMalloc (staging)");
+    a.dev = c->stage[slot].p;
+    if (in) check(hipMemcpyAsync(a.dev, p, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D");
+    if (out) a.dst = const_cast<void *>(p);
+    return a;
+}
+
+void finish(DeviceCtx *c, Arg *args, int n) {
+    for (int i = 0; i < n; ++i)
+        if (args[i].dst)
+            check(hipMemcpyAsync(args[i].dst, args[i].dev, args[i].bytes, hipMemcpyDeviceToHost, c->stream),
+                  "hipMemcpyAsync D2H");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+DeviceCtx *sync_ctx() {
+    DeviceCtx *c;
+    check(get_ctx(&c), "HIP initialisation");
+    return c;
+}
+
+// The synchronous symbols share the per-device staging buffers: one call at a
+// time per process.
+std::mutex g_sync_mu;
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+// ===========================================================================
+// Library
+// ===========================================================================
+
+extern "C" int kai_gdn_hip_init(void) {
+    DeviceCtx *c;
+    return (int)get_ctx(&c);
+}
+
+extern "C" const char *kai_gdn_hip_error_string(int code) {
+    return hipGetErrorString((hipError_t)code);
+}
+
+extern "C" int kai_gdn_hip_check_device_error(void) {
+    DeviceCtx *c;
+    if (get_ctx(&c) != hipSuccess) return -1;
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    uint32_t v = 0;
+    if (hipMemcpy(&v, c->scan.err, sizeof v, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if (v) (void)hipMemset(c->scan.err, 0, sizeof v);
+    return (int)v;
+}
+
+// ===========================================================================
+// Device-pointer entry points
+// ===========================================================================
+
+extern "C" int kai_run_gdn_cumdecay_f32_hip(const float *a, float *decay, size_t seq,
+                                            size_t channels, void *stream) {
+    return (int)run_scan(0, gdn::kF32, a, nullptr, decay, nullptr, seq, channels,
+                         (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_cumdecay_f16_hip(const float *a, uint16_t *decay, size_t seq,
+                                            size_t channels, void *stream) {
+    return (int)run_scan(0, gdn::kF16, a, nullptr, decay, nullptr, seq, channels,
+                         (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_cumdecay_bf16_hip(const float *a, uint16_t *decay, size_t seq,
+                                             size_t channels, void *stream) {
+    return (int)run_scan(0, gdn::kBF16, a, nullptr, decay, nullptr, seq, channels,
+                         (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_gated_scan_f32_hip(const float *g, const float *x, float *s,
+                                              float *state, size_t seq, size_t channels,
+                                              void *stream) {
+    return (int)run_scan(1, gdn::kF32, g, x, s, state, seq, channels, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_gated_scan_f16_hip(const float *g, const float *x, float *s,
+                                              uint16_t *state, size_t seq, size_t channels,
+                                              void *stream) {
+    return (int)run_scan(1, gdn::kF16, g, x, s, state, seq, channels, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_gated_scan_bf16_hip(const float *g, const float *x, float *s,
+                                               uint16_t *state, size_t seq, size_t channels,
+                                               void *stream) {
+    return (int)run_scan(1, gdn::kBF16, g, x, s, state, seq, channels, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_causal_dwconv1d_f32_k4_hip(const float *in, const float *w,
+                                                      float *out, float *hist, size_t seq,
+                                                      size_t channels, void *stream) {
+    return (int)gdn::launch_conv_k4(in, w, out, hist, seq, channels, false, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip(const float *in, const float *w,
+                                                           float *out, float *hist, size_t seq,
+                                                           size_t channels, void *stream) {
+    return (int)gdn::launch_conv_k4(in, w, out, hist, seq, channels, true, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_gemv_f32_f32_f32_hip(const float *a, const float *b, float *c,
+                                                size_t k, size_t n, void *stream) {
+    return (int)gdn::launch_gemv(a, b, c, k, n, (hipStream_t)stream);
+}
+
+static int check_decode_args(const void *S, const float *q, const float *k, const float *v,
+                             const float *g, const float *beta, const float *o, int B, int Hv,
+                             int Hk, int dk, int dv, size_t s_align) {
+    if (B < 0 || Hv < 0 || Hk <= 0 || (Hv > 0 && Hv % Hk != 0)) return (int)hipErrorInvalidValue;
+    const bool dims_ok = (dk == 32 || dk == 64 || dk == 128) && (dv == 32 || dv == 64 || dv == 128);
+    if (!dims_ok) return (int)hipErrorInvalidValue;
+    if (B == 0 || Hv == 0) return 0;
+    if (!S || !q || !k || !v || !g || !beta || !o) return (int)hipErrorInvalidValue;
+    if (!aligned(S, s_align) || !aligned(v, 16) || !aligned(o, 16)) return (int)hipErrorInvalidValue;
+    return 0;
+}
+
+extern "C" int kai_run_gdn_delta_rule_decode_f32_hip(float *S, const float *q, const float *k,
+                                                     const float *v, const float *g,
+                                                     const float *beta, float *o, int batch,
+                                                     int num_v_heads, int num_k_heads,
+                                                     int head_k_dim, int head_v_dim,
+                                                     float q_scale, void *stream) {
+    int rc = check_decode_args(S, q, k, v, g, beta, o, batch, num_v_heads, num_k_heads,
+                               head_k_dim, head_v_dim, 16);
+    if (rc) return rc;
+    return (int)gdn::launch_delta_decode(gdn::kF32, S, q, k, v, g, beta, o, batch, num_v_heads,
+                                         num_k_heads, head_k_dim, head_v_dim, q_scale,
+                                         (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_delta_rule_decode_f16state_hip(uint16_t *S, const float *q,
+                                                          const float *k, const float *v,
+                                                          const float *g, const float *beta,
+                                                          float *o, int batch, int num_v_heads,
+                                                          int num_k_heads, int head_k_dim,
+                                                          int head_v_dim, float q_scale,
+                                                          void *stream) {
+    int rc = check_decode_args(S, q, k, v, g, beta, o, batch, num_v_heads, num_k_heads,
+                               head_k_dim, head_v_dim, 8);
+    if (rc) return rc;
+    return (int)gdn::launch_delta_decode(gdn::kF16, S, q, k, v, g, beta, o, batch, num_v_heads,
+                                         num_k_heads, head_k_dim, head_v_dim, q_scale,
+                                         (hipStream_t)stream);
+}
+
+static int run_chunk(int narrow, const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                     const float *g, const float *beta, uint16_t *o, void *S, int B, int T,
+                     int Hv, int Hk, float q_scale, hipStream_t st) {
+    if (B < 0 || T < 0 || Hv < 0 || Hk <= 0 || (Hv > 0 && Hv % Hk != 0))
+        return (int)hipErrorInvalidValue;
+    if (B == 0 || T == 0 || Hv == 0) return 0;
+    if (!q || !k || !v || !g || !beta || !o || !S) return (int)hipErrorInvalidValue;
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16)) return (int)hipErrorInvalidValue;
+    DeviceCtx *c;
+    hipError_t e = get_ctx(&c);
+    if (e != hipSuccess) return (int)e;
+    std::lock_guard<std::mutex> lk(c->mu);
+    const size_t need = gdn::chunk_workspace_bytes(B, T, Hv);
+    if (need > c->chunk_ws.cap) {
+        // a previous prefill may still be using the old workspace
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) return (int)e;
+        e = c->chunk_ws.reserve(need);
+        if (e != hipSuccess) return (int)e;
+    }
+    return (int)gdn::launch_chunk_prefill(narrow, q, k, v, g, beta, o, S, B, T, Hv, Hk, q_scale,
+                                          c->chunk_ws.p, st);
+}
+
+extern "C" int kai_run_gdn_chunk_delta_rule_bf16_f32_hip(const uint16_t *q, const uint16_t *k,
+                                                         const uint16_t *v, const float *g,
+                                                         const float *beta, uint16_t *o,
+                                                         float *S, int batch, int seq_len,
+                                                         int num_v_heads, int num_k_heads,
+                                                         float q_scale, void *stream) {
+    return run_chunk(gdn::kF32, q, k, v, g, beta, o, S, batch, seq_len, num_v_heads, num_k_heads,
+                     q_scale, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_chunk_delta_rule_bf16_f16state_hip(
+    const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *g, const float *beta,
+    uint16_t *o, uint16_t *S, int batch, int seq_len, int num_v_heads, int num_k_heads,
+    float q_scale, void *stream) {
+    return run_chunk(gdn::kF16, q, k, v, g, beta, o, S, batch, seq_len, num_v_heads, num_k_heads,
+                     q_scale, (hipStream_t)stream);
+}
+
+// ===========================================================================
+// Reference kai symbols (synchronous, host or device pointers)
+// ===========================================================================
+
+extern "C" void kai_run_gdn_cumdecay_f32_sve(const float *a, float *decay, size_t seq,
+                                             size_t channels) {
+    if (seq == 0 || channels == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    const size_t n = seq * channels * sizeof(float);
+    Arg args[2] = {stage_arg(c, 0, a, n, true, false), stage_arg(c, 1, decay, n, false, true)};
+    check(run_scan(0, gdn::kF32, (const float *)args[0].dev, nullptr, args[1].dev, nullptr, seq,
+                   channels, c->stream),
+          "cumdecay launch");
+    finish(c, args, 2);
+}
+
+extern "C" void kai_run_gdn_gated_scan_f32_sve(const float *g, const float *x, float *s,
+                                               float *state, size_t seq, size_t channels) {
+    if (seq == 0 || channels == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    const size_t n = seq * channels * sizeof(float);
+    Arg args[4] = {stage_arg(c, 0, g, n, true, false), stage_arg(c, 1, x, n, true, false),
+                   stage_arg(c, 2, s, n, false, true),
+                   stage_arg(c, 3, state, channels * sizeof(float), true, true)};
+    check(run_scan(1, gdn::kF32, (const float *)args[0].dev, (const float *)args[1].dev,
+                   args[2].dev, args[3].dev, seq, channels, c->stream),
+          "gated_scan launch");
+    finish(c, args, 4);
+}
+
+extern "C" void kai_run_gdn_causal_dwconv1d_f32_k4_sve(const float *in, const float *w,
+                                                       float *out, float *hist, size_t seq,
+                                                       size_t channels) {
+    if (seq == 0 || channels == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    const size_t n = seq * channels * sizeof(float);
+    Arg args[4] = {stage_arg(c, 0, in, n, true, false),
+                   stage_arg(c, 1, w, 4 * channels * sizeof(float), true, false),
+                   stage_arg(c, 2, out, n, false, true),
+                   stage_arg(c, 3, hist, 3 * channels * sizeof(float), true, true)};
+    check(gdn::launch_conv_k4((const float *)args[0].dev, (const float *)args[1].dev,
+                              (float *)args[2].dev, (float *)args[3].dev, seq, channels, false,
+                              c->stream),
+          "dwconv1d launch");
+    finish(c, args, 4);
+}
+
+extern "C" void kai_run_gdn_gemv_f32_f32_f32_1x4_neon(const float *a, const float *b, float *c_,
+                                                      size_t k, size_t n) {
+    if (n == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    Arg args[3] = {stage_arg(c, 0, a, (k ? k : 1) * sizeof(float), k > 0, false),
+                   stage_arg(c, 1, b, (k ? k * n : 1) * sizeof(float), k > 0, false),
+                   stage_arg(c, 2, c_, n * sizeof(float), false, true)};
+    check(gdn::launch_gemv((const float *)args[0].dev, (const float *)args[1].dev,
+                           (float *)args[2].dev, k, n, c->stream),
+          "gemv launch");
+    finish(c, args, 3);
+}

@@ -1,0 +1,76 @@
+"""CPU checks of the drop-in boundary: the library exists, loads, and exports
+every symbol the headers in include/ declare, with the kai prototypes
+unchanged from the reference.  No compute calls (no GPU here)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(REPO, "include")
+
+
+def declared_symbols():
+    names = set()
+    for root, _, files in os.walk(INCLUDE):
+        for f in files:
+            if f.endswith(".h"):
+                txt = open(os.path.join(root, f)).read()
+                txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+                names.update(re.findall(r"\b(kai_[a-z0-9_]+)\s*\(", txt))
+    return names
+
+
+def test_headers_declare_expected_entry_points():
+    import orionsbelt_amd as ob
+    assert declared_symbols() == set(ob.ALL_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    import orionsbelt_amd as ob
+    assert os.path.exists(ob.LIB_PATH), "run python -m orionsbelt_amd.build"
+    out = subprocess.run(["nm", "-D", "--defined-only", ob.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    missing = declared_symbols() - exported
+    assert not missing, f"not exported: {sorted(missing)}"
+
+
+def test_library_loads_and_binds():
+    import orionsbelt_amd as ob
+    L = ob.lib()
+    for name in ob.ALL_SYMBOLS:
+        assert isinstance(getattr(L, name), ctypes._CFuncPtr)
+
+
+def _proto(path, name):
+    txt = re.sub(r"/\*.*?\*/|//[^\n]*", "", open(path).read(), flags=re.S)
+    m = re.search(r"void\s+" + name + r"\s*\(([^)]*)\)", txt)
+    return re.sub(r"\s+", " ", m.group(1)).strip() if m else None
+
+
+@pytest.mark.parametrize("hdr,name", [
+    ("kai_gdn_cumdecay_f32_sve.h", "kai_run_gdn_cumdecay_f32_sve"),
+    ("kai_gdn_gated_scan_f32_sve.h", "kai_run_gdn_gated_scan_f32_sve"),
+    ("kai_gdn_causal_dwconv1d_f32_k4_sve.h", "kai_run_gdn_causal_dwconv1d_f32_k4_sve"),
+    ("kai_gdn_gemv_f32_f32_f32_1x4_neon.h", "kai_run_gdn_gemv_f32_f32_f32_1x4_neon"),
+])
+def test_kai_prototypes_identical_to_reference(hdr, name):
+    ref = os.path.join("/root/reference/kleidiai_submission/kai/ukernels/gdn", hdr)
+    if not os.path.exists(ref):
+        pytest.skip("reference tree not present")
+    ours = os.path.join(INCLUDE, "kai", "ukernels", "gdn", hdr)
+    assert _proto(ours, name) == _proto(ref, name)
+
+
+def test_c_harnesses_built():
+    for b in ("test_kai_gdn", "bench_kai_gdn"):
+        assert os.access(os.path.join(REPO, "orionsbelt_amd", "bin", b), os.X_OK), b
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run(["python", os.path.join(REPO, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True)
+    assert r.returncode == 2 and "one GPU" in r.stderr

@@ -1,0 +1,162 @@
+"""GPU parity of the chunkwise (WY) prefill against the oracle's restatement
+of HF torch_chunk_gated_delta_rule (fp32), through the C-ABI.
+
+The kernel feeds bf16 operands to MFMA (q/k/v are bf16 inputs; T, W, the
+bf16 copy of S, v_new and the gated q/k are rounded to bf16 once each) and
+accumulates in fp32; the state stays fp32.  Stated bound, relative to the
+largest reference magnitude of the compared tensor:
+    max |got - ref| / max |ref|      <= 2e-2
+    ||got - ref||_2 / ||ref||_2      <= 1e-2
+for outputs and final state, scaled by 1.5^log2(T/4096) above T = 4096
+(docs/CORRECTNESS_TOLERANCES.md:34-49).  Exact identities (segmented calls)
+are checked bit for bit.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.gdn_inputs import bf16_bits, bf16_to_f32, prefill_inputs, rel_errors
+from tests.gpu_util import P, dev, empty, host, host_u16, stream, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL, L2_REL = 2e-2, 1e-2
+
+
+def drift(T):
+    return max(1.0, 1.5 ** math.log2(T / 4096)) if T > 4096 else 1.0
+
+
+@pytest.fixture(scope="module")
+def L():
+    torch = torch_mod()
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import orionsbelt_amd as ob
+    return ob.lib()
+
+
+def gpu_prefill(L, q, k, v, g, beta, S, f16=False, calls=None):
+    """Run the prefill; `calls` splits T into consecutive calls that carry S."""
+    import orionsbelt_amd as ob
+    torch = torch_mod()
+    B, T, Hk, d = q.shape
+    Hv = v.shape[2]
+    dq, dk_, dv_ = (dev(bf16_bits(x).view(np.int16)) for x in (q, k, v))
+    dg, db = dev(g), dev(beta)
+    do = empty((B, T, Hv, d), torch.int16)
+    if f16:
+        dS = dev(S.astype(np.float16).view(np.int16))
+        fn = L.kai_run_gdn_chunk_delta_rule_bf16_f16state_hip
+    else:
+        dS = dev(S)
+        fn = L.kai_run_gdn_chunk_delta_rule_bf16_f32_hip
+    bounds = calls or [T]
+    t0 = 0
+    for tlen in bounds:
+        sl = slice(t0, t0 + tlen)
+        if len(bounds) == 1:
+            args = (dq, dk_, dv_, dg, db, do)
+        else:
+            args = tuple(x[:, sl].contiguous() for x in (dq, dk_, dv_, dg, db)) + \
+                (empty((B, tlen, Hv, d), torch.int16),)
+        ob.check(fn(*(P(a) for a in args), P(dS), B, tlen, Hv, Hk, 1.0 / math.sqrt(d),
+                    stream()), "prefill")
+        if len(bounds) > 1:
+            do[:, sl] = args[-1]
+        t0 += tlen
+    o = bf16_to_f32(host_u16(do))
+    Sg = host_u16(dS).view(np.float16).astype(np.float32) if f16 else host(dS)
+    return o, Sg
+
+
+def check(got, ref, T, label):
+    mx, l2 = rel_errors(got, ref)
+    f = drift(T)
+    assert mx <= MAX_REL * f and l2 <= L2_REL * f, f"{label}: max_rel {mx:.3e} l2_rel {l2:.3e}"
+    return mx, l2
+
+
+@pytest.mark.parametrize("B,T,Hv,Hk", [(1, 64, 2, 1), (1, 200, 4, 2), (2, 130, 2, 2),
+                                      (1, 1, 2, 1), (1, 37, 2, 1), (1, 512, 32, 16)])
+def test_prefill_vs_oracle(L, B, T, Hv, Hk):
+    q, k, v, g, beta, S = prefill_inputs(T * 3 + Hv, B, T, Hv, Hk)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, B, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, "output")
+    check(Sg, S_ref, T, "state")
+
+
+def test_prefill_zero_initial_state(L):
+    q, k, v, g, beta, S = prefill_inputs(5, 1, 256, 4, 2, zero_state=True)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, 256, 4, 2, 128, 128, 64)
+    check(o, o_ref, 256, "output")
+    check(Sg, S_ref, 256, "state")
+
+
+def test_prefill_multi_segment_vs_oracle(L):
+    """T above one 4096-token segment: the state crosses segment launches."""
+    q, k, v, g, beta, S = prefill_inputs(9, 1, 4096 + 300, 2, 1)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, 4096 + 300, 2, 1, 128, 128, 64)
+    check(o, o_ref, 4396, "output")
+    check(Sg, S_ref, 4396, "state")
+
+
+def test_prefill_split_calls_bit_identical(L):
+    """Calls split at chunk boundaries carry the fp32 state exactly."""
+    q, k, v, g, beta, S = prefill_inputs(13, 1, 640, 4, 2)
+    o1, S1 = gpu_prefill(L, q, k, v, g, beta, S)
+    o2, S2 = gpu_prefill(L, q, k, v, g, beta, S, calls=[128, 64, 448])
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(S1.view(np.uint32), S2.view(np.uint32))
+
+
+def test_prefill_matches_decode_steps(L):
+    """A prefill of T tokens and T GPU decode steps run the same recurrence."""
+    import orionsbelt_amd as ob
+    torch = torch_mod()
+    B, T, Hv, Hk, d = 1, 48, 4, 2, 128
+    q, k, v, g, beta, S = prefill_inputs(21, B, T, Hv, Hk)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    dS = dev(S)
+    outs = []
+    for t in range(T):
+        dq, dk_, dv_ = dev(q[:, t]), dev(k[:, t]), dev(v[:, t])
+        dg, db = dev(g[:, t]), dev(beta[:, t])
+        do = empty((B, Hv, d), torch.float32)
+        ob.check(L.kai_run_gdn_delta_rule_decode_f32_hip(
+            P(dS), P(dq), P(dk_), P(dv_), P(dg), P(db), P(do), B, Hv, Hk, d, d,
+            1.0 / math.sqrt(d), stream()), "decode")
+        outs.append(host(do))
+    check(o, np.stack(outs, axis=1), T, "prefill vs decode output")
+    check(Sg, host(dS), T, "prefill vs decode state")
+
+
+def test_prefill_f16_state(L):
+    q, k, v, g, beta, S = prefill_inputs(17, 1, 300, 4, 2)
+    S16 = S.astype(np.float16).astype(np.float32)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S16, f16=True)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S16, 1, 300, 4, 2, 128, 128, 64)
+    check(o, o_ref, 300, "output")
+    check(Sg, S_ref, 300, "state (fp16)")
+
+
+def test_prefill_long_sequence_properties(L):
+    """T = 16K at the config-3 head shape: finite, and one call equals two
+    calls split at a chunk boundary (bit for bit)."""
+    B, T, Hv, Hk = 1, 16384, 32, 16
+    q, k, v, g, beta, S = prefill_inputs(3, B, T, Hv, Hk)
+    o1, S1 = gpu_prefill(L, q, k, v, g, beta, S)
+    assert np.isfinite(o1).all() and np.isfinite(S1).all()
+    o2, S2 = gpu_prefill(L, q, k, v, g, beta, S, calls=[8192, 8192])
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(S1.view(np.uint32), S2.view(np.uint32))
+
+
+def test_prefill_rejects_bad_args(L):
+    assert L.kai_run_gdn_chunk_delta_rule_bf16_f32_hip(None, None, None, None, None, None, None,
+                                                       1, 64, 3, 2, 1.0, None) != 0

@@ -1,0 +1,314 @@
+"""GPU parity of the streaming kernels (conv K=4, cumdecay, gated scan, GEMV,
+mixed-precision variants) against the CPU oracle, through the C-ABI.
+
+Bars: bit-identical where the kernel keeps the reference's operation order
+(conv without SiLU, GEMV, and cumdecay / scan inside one 64-row tile);
+otherwise the reference test's own tolerances (test_kai_gdn.c:190,222,434)
+and BASELINE's 1e-5 relative for fp32 decay and conv+SiLU.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.gdn_inputs import assert_kai_close, conv_inputs
+from tests.gpu_util import P, dev, empty, host, host_u16, np_ptr, stream, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+REF_SEQS = [1, 4, 16, 64]                           # test_kai_gdn.c:167
+REF_CHANS = [1, 3, 7, 8, 12, 16, 17, 32, 33, 128]   # test_kai_gdn.c:168
+
+
+@pytest.fixture(scope="module")
+def L():
+    torch = torch_mod()
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import orionsbelt_amd as ob
+    lib = ob.lib()
+    ob.check(lib.kai_gdn_hip_init(), "init")
+    return lib
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def lcg(seed=0x5EED1234):
+    """Fill helper with the reference test's LCG ranges (test_kai_gdn.c:45-55)."""
+    from tests.golden.gen_golden import LCG
+    return LCG(seed)
+
+
+# ---------------------------------------------------------------------------
+# conv
+# ---------------------------------------------------------------------------
+
+def run_conv(L, x, w, h, seq, ch, silu=False):
+    import orionsbelt_amd as ob
+    dx, dw, dh = dev(x), dev(w), dev(h)
+    dout = empty(seq * ch, torch_mod().float32)
+    fn = L.kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip if silu else \
+        L.kai_run_gdn_causal_dwconv1d_f32_k4_hip
+    ob.check(fn(P(dx), P(dw), P(dout), P(dh), seq, ch, stream()), "conv")
+    return host(dout), host(dh)
+
+
+def test_conv_reference_sweep_bit_exact(L):
+    rng = lcg()
+    for seq in REF_SEQS:
+        for ch in REF_CHANS + [129, 2051]:
+            x = rng.uniform(seq * ch, -1, 1)
+            w = rng.uniform(4 * ch, -1, 1)
+            h = rng.uniform(3 * ch, -1, 1)
+            out, hist = run_conv(L, x, w, h, seq, ch)
+            rout, rhist = orc.conv_f32(x, w, h, seq, ch)
+            assert np.array_equal(bits(out), bits(rout)), (seq, ch)
+            assert np.array_equal(bits(hist), bits(rhist)), (seq, ch)
+
+
+@pytest.mark.parametrize("seq,ch", [(1, 8192), (2, 8192), (3, 17), (37, 8192), (1000, 4096),
+                                    (4096, 8192)])
+def test_conv_config1_bit_exact_and_silu(L, seq, ch):
+    x, w, h = conv_inputs(seq + ch, seq, ch)
+    h = np.random.RandomState(5).randn(3 * ch).astype(np.float32)  # nonzero history
+    out, hist = run_conv(L, x, w, h, seq, ch)
+    rout, rhist = orc.conv_f32(x, w, h, seq, ch)
+    assert np.array_equal(bits(out), bits(rout))
+    assert np.array_equal(bits(hist), bits(rhist))
+    sout, shist = run_conv(L, x, w, h, seq, ch, silu=True)
+    rsout, _ = orc.conv_f32(x, w, h, seq, ch, silu=True)
+    assert np.array_equal(bits(shist), bits(rhist))
+    # BASELINE: <= 1e-5 relative for fp32 conv (SiLU uses the device expf)
+    assert_kai_close(sout, rsout, 1e-6, 1e-5, "conv+silu")
+
+
+def test_conv_continuity_two_calls(L):
+    """Two calls of 8 equal one call of 16 (test_kai_gdn.c:346-381)."""
+    seq1, seq2, ch = 8, 8, 17
+    x, w, _ = conv_inputs(11, seq1 + seq2, ch)
+    h = np.random.RandomState(6).randn(3 * ch).astype(np.float32)
+    full, hfull = orc.conv_f32(x, w, h, seq1 + seq2, ch)
+    o1, h1 = run_conv(L, x[:seq1 * ch], w, h, seq1, ch)
+    o2, h2 = run_conv(L, x[seq1 * ch:], w, h1, seq2, ch)
+    assert np.array_equal(bits(np.concatenate([o1, o2])), bits(full))
+    assert np.array_equal(bits(h2), bits(hfull))
+
+
+def test_conv_in_place(L):
+    import orionsbelt_amd as ob
+    seq, ch = 300, 256
+    x, w, _ = conv_inputs(12, seq, ch)
+    h = np.random.RandomState(7).randn(3 * ch).astype(np.float32)
+    rout, rhist = orc.conv_f32(x, w, h, seq, ch)
+    dx, dw, dh = dev(x), dev(w), dev(h)
+    ob.check(L.kai_run_gdn_causal_dwconv1d_f32_k4_hip(P(dx), P(dw), P(dx), P(dh), seq, ch,
+                                                      stream()), "conv in place")
+    assert np.array_equal(bits(host(dx)), bits(rout))
+    assert np.array_equal(bits(host(dh)), bits(rhist))
+
+
+# ---------------------------------------------------------------------------
+# cumdecay / gated scan
+# ---------------------------------------------------------------------------
+
+def run_cumdecay(L, a, seq, ch, fmt="f32"):
+    import orionsbelt_amd as ob
+    torch = torch_mod()
+    da = dev(a)
+    if fmt == "f32":
+        dout = empty(seq * ch, torch.float32)
+        ob.check(L.kai_run_gdn_cumdecay_f32_hip(P(da), P(dout), seq, ch, stream()), "cumdecay")
+        return host(dout)
+    dout = empty(seq * ch, torch.int16)
+    fn = L.kai_run_gdn_cumdecay_f16_hip if fmt == "f16" else L.kai_run_gdn_cumdecay_bf16_hip
+    ob.check(fn(P(da), P(dout), seq, ch, stream()), "cumdecay narrow")
+    return host_u16(dout)
+
+
+def run_scan(L, g, x, st, seq, ch, fmt="f32"):
+    import orionsbelt_amd as ob
+    torch = torch_mod()
+    dg, dx = dev(g), dev(x)
+    ds = empty(seq * ch, torch.float32)
+    if fmt == "f32":
+        dst = dev(np.asarray(st, np.float32))
+        ob.check(L.kai_run_gdn_gated_scan_f32_hip(P(dg), P(dx), P(ds), P(dst), seq, ch,
+                                                  stream()), "scan")
+        return host(ds), host(dst)
+    dst = dev(np.asarray(st, np.uint16).view(np.int16))
+    fn = L.kai_run_gdn_gated_scan_f16_hip if fmt == "f16" else L.kai_run_gdn_gated_scan_bf16_hip
+    ob.check(fn(P(dg), P(dx), P(ds), P(dst), seq, ch, stream()), "scan narrow")
+    return host(ds), host_u16(dst)
+
+
+def test_cumdecay_reference_sweep(L):
+    rng = lcg(0x1234)
+    for seq in REF_SEQS:
+        for ch in REF_CHANS + [129, 300]:
+            a = rng.uniform(seq * ch, 0.5, 1.5)
+            got = run_cumdecay(L, a, seq, ch)
+            ref = orc.cumdecay_f32(a, seq, ch)
+            # seq <= 64 is one row tile: the reference order exactly
+            assert np.array_equal(bits(got), bits(ref)), (seq, ch)
+
+
+@pytest.mark.parametrize("seq,ch", [(65, 7), (200, 300), (1000, 513), (4096, 8192)])
+def test_cumdecay_multi_tile(L, seq, ch):
+    rs = np.random.RandomState(seq)
+    g = (-np.log1p(np.exp(rs.randn(seq * ch))) * np.exp(rs.uniform(-2, 0, seq * ch)))
+    a = np.exp(g).astype(np.float32)  # config-2 gates
+    got = run_cumdecay(L, a, seq, ch)
+    ref = orc.cumdecay_f32(a, seq, ch)
+    assert_kai_close(got, ref, 1e-6, 1e-5, "cumdecay")   # test_kai_gdn.c:434, BASELINE 1e-5
+    # slow gates keep products O(1) over the whole sequence: relative bound
+    a2 = rs.uniform(0.9995, 1.0005, seq * ch).astype(np.float32)
+    got2 = run_cumdecay(L, a2, seq, ch)
+    ref2 = orc.cumdecay_f32(a2, seq, ch)
+    assert_kai_close(got2, ref2, 0.0, 1e-5 if seq <= 1000 else 3e-5, "cumdecay slow gates")
+
+
+def test_gated_scan_reference_sweep(L):
+    rng = lcg(0x777)
+    for seq in REF_SEQS:
+        for ch in REF_CHANS + [255]:
+            g = rng.uniform(seq * ch, -0.99, 0.99)
+            x = rng.uniform(seq * ch, -2, 2)
+            st = rng.uniform(ch, -1, 1)
+            s, st2 = run_scan(L, g, x, st, seq, ch)
+            rs_, rst = orc.gated_scan_f32(g, x, st, seq, ch)
+            assert np.array_equal(bits(s), bits(rs_)), (seq, ch)
+            assert np.array_equal(bits(st2), bits(rst)), (seq, ch)
+
+
+@pytest.mark.parametrize("seq,ch", [(65, 33), (1000, 2048), (4096, 8192)])
+def test_gated_scan_multi_tile(L, seq, ch):
+    rs = np.random.RandomState(seq + 1)
+    g = rs.uniform(-0.99, 0.99, seq * ch).astype(np.float32)
+    x = rs.uniform(-2, 2, seq * ch).astype(np.float32)
+    st = rs.uniform(-1, 1, ch).astype(np.float32)
+    s, st2 = run_scan(L, g, x, st, seq, ch)
+    rs_, rst = orc.gated_scan_f32(g, x, st, seq, ch)
+    assert_kai_close(s, rs_, 1e-4, 5e-4, "scan")          # test_kai_gdn.c:222
+    assert_kai_close(st2, rst, 1e-4, 5e-4, "scan state")
+
+
+def test_gated_scan_continuity(L):
+    """Two calls of 8 equal one call of 16 (test_kai_gdn.c:308-342), and the
+    state carry of the GPU validator (gdn_gpu_validate.c:580-584)."""
+    rng = lcg(99)
+    for seq1, seq2, ch in [(8, 8, 16), (64, 65, 2048), (1, 1, 2048)]:
+        n = (seq1 + seq2) * ch
+        g = rng.uniform(n, -0.99, 0.99)
+        x = rng.uniform(n, -2, 2)
+        st = rng.uniform(ch, -1, 1)
+        rs_, rst = orc.gated_scan_f32(g, x, st, seq1 + seq2, ch)
+        s1, st1 = run_scan(L, g[:seq1 * ch], x[:seq1 * ch], st, seq1, ch)
+        s2, st2 = run_scan(L, g[seq1 * ch:], x[seq1 * ch:], st1, seq2, ch)
+        assert_kai_close(np.concatenate([s1, s2]), rs_, 1e-4, 5e-4, "continuity")
+        assert_kai_close(st2, rst, 1e-4, 5e-4, "continuity state")
+
+
+@pytest.mark.parametrize("fmt", ["f16", "bf16"])
+def test_mixed_precision_variants(L, fmt, golden):
+    d = golden("sve_mixed.npz")
+    T, C = (int(x) for x in d["shape"])
+    for scen in ("warm", "cold"):
+        got = run_cumdecay(L, d[f"{scen}_a"], T, C, fmt)
+        assert np.array_equal(got, d[f"{scen}_cd_{fmt}"]), (scen, fmt)
+        s, st = run_scan(L, d[f"{scen}_g"], d[f"{scen}_x"], d[f"{scen}_st16_{fmt}"], T, C, fmt)
+        assert np.array_equal(bits(s), bits(d[f"{scen}_scan_s_{fmt}"])), (scen, fmt)
+        assert np.array_equal(st, d[f"{scen}_scan_st_{fmt}"]), (scen, fmt)
+
+
+# ---------------------------------------------------------------------------
+# GEMV
+# ---------------------------------------------------------------------------
+
+def test_gemv_bit_exact(L):
+    import orionsbelt_amd as ob
+    rng = lcg(0x4242)
+    for k in (1, 4, 16, 64, 128, 1024):
+        for n in (1, 3, 4, 7, 8, 17, 33, 130, 257, 2560):
+            a = rng.uniform(k, -1, 1)
+            b = rng.uniform(k * n, -1, 1)
+            da, db = dev(a), dev(b)
+            dc = empty(n, torch_mod().float32)
+            ob.check(L.kai_run_gdn_gemv_f32_f32_f32_hip(P(da), P(db), P(dc), k, n, stream()))
+            assert np.array_equal(bits(host(dc)), bits(orc.gemv_f32(a, b, k, n))), (k, n)
+
+
+# ---------------------------------------------------------------------------
+# Drop-in kai symbols with HOST pointers (the reference harness's usage)
+# ---------------------------------------------------------------------------
+
+def test_kai_symbols_host_pointers(L):
+    rng = lcg(5)
+    seq, ch = 16, 33
+    a = rng.uniform(seq * ch, 0.5, 1.5)
+    out = np.empty(seq * ch, np.float32)
+    L.kai_run_gdn_cumdecay_f32_sve(np_ptr(a), np_ptr(out), seq, ch)
+    assert np.array_equal(bits(out), bits(orc.cumdecay_f32(a, seq, ch)))
+
+    g, x = rng.uniform(seq * ch, -0.99, 0.99), rng.uniform(seq * ch, -2, 2)
+    st = rng.uniform(ch, -1, 1)
+    s = np.empty(seq * ch, np.float32)
+    st_got = st.copy()
+    L.kai_run_gdn_gated_scan_f32_sve(np_ptr(g), np_ptr(x), np_ptr(s), np_ptr(st_got), seq, ch)
+    rs_, rst = orc.gated_scan_f32(g, x, st, seq, ch)
+    assert np.array_equal(bits(s), bits(rs_)) and np.array_equal(bits(st_got), bits(rst))
+
+    w, h = rng.uniform(4 * ch, -1, 1), rng.uniform(3 * ch, -1, 1)
+    o = np.empty(seq * ch, np.float32)
+    h_got = h.copy()
+    L.kai_run_gdn_causal_dwconv1d_f32_k4_sve(np_ptr(x), np_ptr(w), np_ptr(o), np_ptr(h_got),
+                                             seq, ch)
+    ro, rh = orc.conv_f32(x, w, h, seq, ch)
+    assert np.array_equal(bits(o), bits(ro)) and np.array_equal(bits(h_got), bits(rh))
+
+    k, n = 128, 257
+    av, bm = rng.uniform(k, -1, 1), rng.uniform(k * n, -1, 1)
+    c = np.empty(n, np.float32)
+    L.kai_run_gdn_gemv_f32_f32_f32_1x4_neon(np_ptr(av), np_ptr(bm), np_ptr(c), k, n)
+    assert np.array_equal(bits(c), bits(orc.gemv_f32(av, bm, k, n)))
+
+
+def test_kai_symbols_device_pointers_in_place(L):
+    """The drop-in symbols also accept device pointers and run in place."""
+    seq, ch = 64, 128
+    rng = lcg(6)
+    a = rng.uniform(seq * ch, 0.5, 1.5)
+    da = dev(a)
+    dout = empty(seq * ch, torch_mod().float32)
+    L.kai_run_gdn_cumdecay_f32_sve(P(da), P(dout), seq, ch)
+    assert np.array_equal(bits(host(dout)), bits(orc.cumdecay_f32(a, seq, ch)))
+
+
+def test_kai_degenerate_no_writes(L):
+    """seq=0 / channels=0 write nothing; k=0 GEMV writes zeros
+    (test_kai_gdn.c:520-637)."""
+    sentinel = np.full(8, 42.0, np.float32)
+    out = sentinel.copy()
+    L.kai_run_gdn_cumdecay_f32_sve(np_ptr(sentinel), np_ptr(out), 0, 8)
+    L.kai_run_gdn_cumdecay_f32_sve(np_ptr(sentinel), np_ptr(out), 8, 0)
+    assert np.array_equal(out, sentinel)
+    st = np.array([1, -2, 3, -4], np.float32)
+    st2 = st.copy()
+    L.kai_run_gdn_gated_scan_f32_sve(np_ptr(sentinel), np_ptr(sentinel), np_ptr(out),
+                                     np_ptr(st2), 0, 4)
+    assert np.array_equal(st2, st)
+    hist = np.arange(6, dtype=np.float32)
+    h2 = hist.copy()
+    L.kai_run_gdn_causal_dwconv1d_f32_k4_sve(np_ptr(sentinel), np_ptr(sentinel), np_ptr(out),
+                                             np_ptr(h2), 0, 2)
+    assert np.array_equal(h2, hist)
+    c = np.full(8, np.nan, np.float32)
+    L.kai_run_gdn_gemv_f32_f32_f32_1x4_neon(np_ptr(sentinel), np_ptr(sentinel), np_ptr(c), 0, 8)
+    assert np.all(c == 0.0)
+    c1 = np.array([42.0], np.float32)
+    L.kai_run_gdn_gemv_f32_f32_f32_1x4_neon(np_ptr(sentinel), np_ptr(sentinel), np_ptr(c1), 4, 0)
+    assert c1[0] == 42.0
+
+
+def test_no_scan_watchdog_errors(L):
+    assert L.kai_gdn_hip_check_device_error() == 0
