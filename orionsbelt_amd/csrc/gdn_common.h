@@ -56,3 +56,30 @@ GDN_DEV bf16x8_t pack_bf16x8(const float *f) {
 GDN_DEV bf16x8_t as_bf16x8(u32x4_t w) { return __builtin_bit_cast(bf16x8_t, w); }
 
 GDN_DEV f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
+
+// ---- plain / non-temporal vector memory access ------------------------------
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
+
+template <bool NT> GDN_DEV float4 load_f4(const float *p) {
+    const f32x4_t *q = reinterpret_cast<const f32x4_t *>(p);
+    f32x4_t v;
+    if constexpr (NT) v = __builtin_nontemporal_load(q);
+    else v = *q;
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+template <bool NT> GDN_DEV void store_f4(float *p, float4 x) {
+    f32x4_t v = {x.x, x.y, x.z, x.w};
+    f32x4_t *q = reinterpret_cast<f32x4_t *>(p);
+    if constexpr (NT) __builtin_nontemporal_store(v, q);
+    else *q = v;
+}
+template <bool NT> GDN_DEV u32x2_t load_u2(const void *p) {
+    const u32x2_t *q = reinterpret_cast<const u32x2_t *>(p);
+    if constexpr (NT) return __builtin_nontemporal_load(q);
+    else return *q;
+}
+template <bool NT> GDN_DEV void store_u2(void *p, u32x2_t v) {
+    u32x2_t *q = reinterpret_cast<u32x2_t *>(p);
+    if constexpr (NT) __builtin_nontemporal_store(v, q);
+    else *q = v;
+}

@@ -20,26 +20,28 @@
 namespace gdn {
 namespace {
 
-template <int NARROW> struct StateIO;
-template <> struct StateIO<kF32> {
+// State I/O.  NT selects non-temporal loads and stores: the state is touched
+// once per step, so it need not be kept in L2 or the Infinity Cache.
+template <int NARROW, bool NT> struct StateIO;
+template <bool NT> struct StateIO<kF32, NT> {
     static GDN_DEV float4 load(const void *S, int64_t i) {
-        return *reinterpret_cast<const float4 *>(static_cast<const float *>(S) + i);
+        return load_f4<NT>(static_cast<const float *>(S) + i);
     }
     static GDN_DEV void store(void *S, int64_t i, float4 v) {
-        *reinterpret_cast<float4 *>(static_cast<float *>(S) + i) = v;
+        store_f4<NT>(static_cast<float *>(S) + i, v);
     }
 };
-template <> struct StateIO<kF16> {
+template <bool NT> struct StateIO<kF16, NT> {
     static GDN_DEV float4 load(const void *S, int64_t i) {
-        const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(S) + i);
-        return make_float4(f16_to_f32((uint16_t)(u.x & 0xFFFF)), f16_to_f32((uint16_t)(u.x >> 16)),
-                           f16_to_f32((uint16_t)(u.y & 0xFFFF)), f16_to_f32((uint16_t)(u.y >> 16)));
+        const u32x2_t u = load_u2<NT>(static_cast<const uint16_t *>(S) + i);
+        return make_float4(f16_to_f32((uint16_t)(u[0] & 0xFFFF)), f16_to_f32((uint16_t)(u[0] >> 16)),
+                           f16_to_f32((uint16_t)(u[1] & 0xFFFF)), f16_to_f32((uint16_t)(u[1] >> 16)));
     }
     static GDN_DEV void store(void *S, int64_t i, float4 v) {
-        uint2 u;
-        u.x = (uint32_t)f32_to_f16_rne(v.x) | ((uint32_t)f32_to_f16_rne(v.y) << 16);
-        u.y = (uint32_t)f32_to_f16_rne(v.z) | ((uint32_t)f32_to_f16_rne(v.w) << 16);
-        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(S) + i) = u;
+        u32x2_t u;
+        u[0] = (uint32_t)f32_to_f16_rne(v.x) | ((uint32_t)f32_to_f16_rne(v.y) << 16);
+        u[1] = (uint32_t)f32_to_f16_rne(v.z) | ((uint32_t)f32_to_f16_rne(v.w) << 16);
+        store_u2<NT>(static_cast<uint16_t *>(S) + i, u);
     }
 };
 
@@ -50,30 +52,34 @@ GDN_DEV float4 f4_add(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
-template <int DK, int DV, int NARROW>
-__global__ __launch_bounds__(256) void delta_decode_kernel(
+// MINW: minimum waves per SIMD the register allocation must allow.
+// NT:   non-temporal state traffic.
+// CS:   column splits -- CS workgroups per (sequence, head), each owning
+//       DV/CS value columns (the update of column j reads only column j).
+template <int DK, int DV, int NARROW, int MINW, bool NT, int CS>
+__global__ __launch_bounds__(256, MINW) void delta_decode_kernel(
     void *S, const float *__restrict__ q, const float *__restrict__ k,
     const float *__restrict__ v, const float *__restrict__ g, const float *__restrict__ beta,
     float *__restrict__ o, int Hv, int Hk, float q_scale) {
-    constexpr int TPR = DV / 4;        // threads per state row
+    constexpr int TPR = DV / CS / 4;   // threads per state row (segment)
     constexpr int RG = 256 / TPR;      // row groups
     constexpr int RPT = DK / RG;       // rows per thread
-    static_assert(RPT >= 1 && DK % RG == 0, "unsupported head shape");
+    static_assert(TPR >= 1 && RPT >= 1 && DK % RG == 0, "unsupported head shape");
     __shared__ float4 red[RG][TPR];
 
-    const int bh = blockIdx.x;
+    const int bh = blockIdx.x / CS;
     const int b = bh / Hv, h = bh % Hv;
     const int kh = h / (Hv / Hk);
     const int cgi = threadIdx.x % TPR;
     const int rg = threadIdx.x / TPR;
-    const int c = cgi * 4;
+    const int c = (blockIdx.x % CS) * (DV / CS) + cgi * 4;
     const int64_t sbase = (int64_t)bh * DK * DV;
     const float *kp = k + ((int64_t)b * Hk + kh) * DK;
     const float *qp = q + ((int64_t)b * Hk + kh) * DK;
 
     float4 s[RPT];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = StateIO<NARROW>::load(S, sbase + (int64_t)(rg + RG * i) * DV + c);
+    for (int i = 0; i < RPT; ++i) s[i] = StateIO<NARROW, NT>::load(S, sbase + (int64_t)(rg + RG * i) * DV + c);
     float kj[RPT], qj[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -104,7 +110,7 @@ __global__ __launch_bounds__(256) void delta_decode_kernel(
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
         s[i] = f4_fma(kj[i], delta, s[i]);
-        StateIO<NARROW>::store(S, sbase + (int64_t)(rg + RG * i) * DV + c, s[i]);
+        StateIO<NARROW, NT>::store(S, sbase + (int64_t)(rg + RG * i) * DV + c, s[i]);
         op = f4_fma(qj[i], s[i], op);
     }
     __syncthreads();  // everyone has read red[] for kv
@@ -118,15 +124,26 @@ __global__ __launch_bounds__(256) void delta_decode_kernel(
     }
 }
 
-template <int NARROW>
-hipError_t launch_decode_n(void *S, const float *q, const float *k, const float *v,
-                           const float *g, const float *beta, float *o, int B, int Hv, int Hk,
-                           int dk, int dv, float q_scale, hipStream_t st) {
-    dim3 grid((unsigned)(B * Hv)), block(256);
+}  // namespace
+
+// Production configuration of the decode kernel, measured on MI355X over 24
+// rotating 128 MiB states (B=64, 32 heads, 128x128): 2 column splits with
+// non-temporal state traffic run 47.1 us per layer (5.77 TB/s) against
+// 55.4 us for one workgroup per head with cached traffic.
+constexpr int kDecodeMinW = 1;
+constexpr bool kDecodeNT = true;
+constexpr int kDecodeCS = 2;
+
+template <int NARROW, int MINW, bool NT, int CS>
+hipError_t launch_decode_cfg(void *S, const float *q, const float *k, const float *v,
+                             const float *g, const float *beta, float *o, int B, int Hv, int Hk,
+                             int dk, int dv, float q_scale, hipStream_t st) {
 #define GDN_DEC(DK, DV)                                                                      \
     if (dk == DK && dv == DV) {                                                              \
-        delta_decode_kernel<DK, DV, NARROW><<<grid, block, 0, st>>>(S, q, k, v, g, beta, o,   \
-                                                                     Hv, Hk, q_scale);        \
+        constexpr int cs = (CS * 1024 <= DK * DV && DV / CS >= 4) ? CS : 1;                  \
+        dim3 grid((unsigned)(B * Hv * cs)), block(256);                                      \
+        delta_decode_kernel<DK, DV, NARROW, MINW, NT, cs><<<grid, block, 0, st>>>(            \
+            S, q, k, v, g, beta, o, Hv, Hk, q_scale);                                        \
         return hipGetLastError();                                                            \
     }
     GDN_DEC(128, 128)
@@ -142,17 +159,17 @@ hipError_t launch_decode_n(void *S, const float *q, const float *k, const float 
     return hipErrorInvalidValue;
 }
 
-}  // namespace
-
 hipError_t launch_delta_decode(int narrow_state, void *S, const float *q, const float *k,
                                const float *v, const float *g, const float *beta, float *o,
                                int B, int Hv, int Hk, int dk, int dv, float q_scale,
                                hipStream_t st) {
     if (B <= 0 || Hv <= 0) return hipSuccess;
     if (narrow_state == kF32)
-        return launch_decode_n<kF32>(S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
+        return launch_decode_cfg<kF32, kDecodeMinW, kDecodeNT, kDecodeCS>(
+            S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
     if (narrow_state == kF16)
-        return launch_decode_n<kF16>(S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
+        return launch_decode_cfg<kF16, kDecodeMinW, kDecodeNT, kDecodeCS>(
+            S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
     return hipErrorInvalidValue;
 }
 

@@ -332,7 +332,7 @@ static void *to_dev(const void *h, size_t n) {
         fprintf(stderr, "hipMalloc failed\n");
         exit(1);
     }
-    if (n && hipMemcpy(d, h, n, hipMemcpyHostToDevice) != hipSuccess) {
+    if (h && n && hipMemcpy(d, h, n, hipMemcpyHostToDevice) != hipSuccess) {
         fprintf(stderr, "hipMemcpy failed\n");
         exit(1);
     }
@@ -428,6 +428,7 @@ static int t_dev_delta_rule(void) {
 }
 
 int main(void) {
+    setvbuf(stdout, NULL, _IOLBF, 0);
     printf("=== GDN kai entry points on MI355X (libkai_gdn_hip) ===\n\n");
     SUITE("test_cumdecay", t_cumdecay());
     SUITE("test_gated_scan", t_gated_scan());
