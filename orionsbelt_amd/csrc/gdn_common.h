@@ -18,6 +18,16 @@ GDN_DEV uint16_t f32_to_bf16_rne(float f) {
 
 GDN_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// Two floats -> packed bf16 pair with the gfx950 hardware convert
+// (v_cvt_pk_bf16_f32, round to nearest even; equal to f32_to_bf16_rne for
+// every finite input).  Used for MFMA operands, where only the value matters.
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+GDN_DEV uint32_t pack2_bf16_hw(float a, float b) {
+    const bf16x2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+GDN_DEV uint16_t f32_to_bf16_hw(float a) { return __builtin_bit_cast(uint16_t, (__bf16)a); }
+
 // IEEE binary16 <-> binary32 with the hardware converts (v_cvt_f16_f32 rounds
 // to nearest even, keeps subnormals).
 GDN_DEV uint16_t f32_to_f16_rne(float f) {

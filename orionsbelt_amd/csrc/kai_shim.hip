@@ -67,8 +67,11 @@ struct DeviceCtx {
     uint32_t epoch = 0;
     hipEvent_t scan_done = nullptr;
     bool scan_pending = false;
-    // prefill workspace
+    // prefill workspace and the second stream its phases overlap on
     DevBuf chunk_ws;
+    gdn::PrefillStreams pf{};
+    hipEvent_t pf_done = nullptr;  // end of the last prefill (workspace free)
+    bool pf_pending = false;
 };
 
 std::mutex g_ctx_mu;
@@ -96,6 +99,12 @@ hipError_t get_ctx(DeviceCtx **out) {
         e = hipMemset(c->scan.counter, 0, 256);
         if (e != hipSuccess) return e;
         c->scan.err = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(c->scan.counter) + 64);
+        e = hipStreamCreateWithFlags(&c->pf.aux, hipStreamNonBlocking);
+        if (e != hipSuccess) return e;
+        hipEvent_t *evs[6] = {&c->pf.ready, &c->pf.a_done[0], &c->pf.a_done[1], &c->pf.b_done[0],
+                              &c->pf.b_done[1], &c->pf_done};
+        for (hipEvent_t *ev : evs)
+            if ((e = hipEventCreateWithFlags(ev, hipEventDisableTiming)) != hipSuccess) return e;
         c->ready = true;
     }
     *out = c;
@@ -370,8 +379,14 @@ static int run_chunk(int narrow, const uint16_t *q, const uint16_t *k, const uin
         e = c->chunk_ws.reserve(need);
         if (e != hipSuccess) return (int)e;
     }
-    return (int)gdn::launch_chunk_prefill(narrow, q, k, v, g, beta, o, S, B, T, Hv, Hk, q_scale,
-                                          c->chunk_ws.p, st);
+    // calls share the workspace: a call starts after the previous one ended
+    if (c->pf_pending && (e = hipStreamWaitEvent(st, c->pf_done, 0)) != hipSuccess) return (int)e;
+    e = gdn::launch_chunk_prefill(narrow, q, k, v, g, beta, o, S, B, T, Hv, Hk, q_scale,
+                                  c->chunk_ws.p, c->pf, st);
+    if (e != hipSuccess) return (int)e;
+    if ((e = hipEventRecord(c->pf_done, st)) != hipSuccess) return (int)e;
+    c->pf_pending = true;
+    return 0;
 }
 
 extern "C" int kai_run_gdn_chunk_delta_rule_bf16_f32_hip(const uint16_t *q, const uint16_t *k,
