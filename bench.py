@@ -242,6 +242,26 @@ def bench_stream(L, ob, torch, timer, reps=40, sets=4):
     )
 
 
+def run_profile(which, L, ob, torch, timer, steps, warmup):
+    """Workload for rocprofv3: `which`, then a plain copy kernel
+    (dst = src * 1 over 64M fp32: reads and writes exactly 268,435,456 bytes),
+    the reference for scaling FETCH_SIZE / WRITE_SIZE to bytes."""
+    if which == "decode":
+        ms, kern, _ = bench_decode(L, ob, torch, steps, warmup, timer)
+        log(f"decode: {ms:.4f} ms/step, {kern * 1e3:.2f} us/launch")
+    elif which == "prefill":
+        log(f"prefill: {bench_prefill(L, ob, torch, timer, reps=steps)}")
+    else:
+        conv, decay = bench_stream(L, ob, torch, timer, reps=steps)
+        log(f"{which}: {conv if which == 'conv' else decay}")
+    src = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    log("calibration copy: 3 x 268435456 bytes")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +269,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip prefill/conv/decay lines")
+    ap.add_argument("--profile", choices=["decode", "prefill", "conv", "cumdecay"],
+                    help="run only this workload (and a 256 MiB device copy that calibrates "
+                         "HBM byte counters) for rocprofv3; prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the GDN path has no cross-GPU "
@@ -263,6 +286,9 @@ def main():
     L = ob.lib()
     ob.check(L.kai_gdn_hip_init(), "init")
     timer = Timer(torch)
+    if args.profile:
+        run_profile(args.profile, L, ob, torch, timer, args.steps, args.warmup)
+        return
 
     log("decode: 24 layers x B=64 ...")
     ms_step, kern_ms, _ = bench_decode(L, ob, torch, args.steps, args.warmup, timer)
