@@ -146,8 +146,9 @@ def test_prefill_f16_state(L):
 
 
 def test_prefill_long_sequence_properties(L):
-    """T = 16K at the config-3 head shape: finite, and one call equals two
-    calls split at a chunk boundary (bit for bit)."""
+    """T = 16K at the config-3 head shape: finite, one call equals two calls
+    split at a chunk boundary (bit for bit), and the value heads of the last
+    key head agree with the oracle over the whole sequence."""
     B, T, Hv, Hk = 1, 16384, 32, 16
     q, k, v, g, beta, S = prefill_inputs(3, B, T, Hv, Hk)
     o1, S1 = gpu_prefill(L, q, k, v, g, beta, S)
@@ -155,6 +156,12 @@ def test_prefill_long_sequence_properties(L):
     o2, S2 = gpu_prefill(L, q, k, v, g, beta, S, calls=[8192, 8192])
     assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
     assert np.array_equal(S1.view(np.uint32), S2.view(np.uint32))
+    hv = slice(Hv - 2, Hv)  # value heads 30, 31 read key head 15
+    sub = [np.ascontiguousarray(x) for x in (q[:, :, Hk - 1:], k[:, :, Hk - 1:], v[:, :, hv],
+                                             g[:, :, hv], beta[:, :, hv], S[:, hv])]
+    o_ref, S_ref = orc.chunk_gdr(*sub, B, T, 2, 1, 128, 128, 64)
+    check(o1[:, :, hv], o_ref, T, "output, heads 30-31")
+    check(S1[:, hv], S_ref, T, "state, heads 30-31")
 
 
 def test_prefill_rejects_bad_args(L):

@@ -323,6 +323,24 @@ def test_decode_unscaled_equals_reference_loop():
             assert bits_equal(Sh, S[b, h].ravel()) and bits_equal(oh, o[b, h])
 
 
+def test_decode_f16state_is_widen_step_narrow():
+    """The fp16-state step is the fp32 step (pinned above against HF) on the
+    widened state, narrowed once by round-to-nearest-even; numpy's float16
+    conversion is the independent check of both conversions."""
+    rs = np.random.RandomState(9)
+    B, Hv, Hk, dk, dv = 2, 4, 2, 16, 8
+    S16 = (rs.randn(B, Hv, dk, dv) * 0.3).astype(np.float16).view(np.uint16)
+    q, k = rs.randn(B, Hk, dk).astype(np.float32), rs.randn(B, Hk, dk).astype(np.float32)
+    v = rs.randn(B, Hv, dv).astype(np.float32)
+    g, beta = -rs.rand(B, Hv).astype(np.float32), rs.rand(B, Hv).astype(np.float32)
+    S16n, o16 = orc.delta_rule_decode_f16state(S16, q, k, v, g, beta, B, Hv, Hk, dk, dv, 0.25)
+    S32 = S16.view(np.float16).astype(np.float32)
+    S32n, o32 = orc.delta_rule_decode(S32, q, k, v, g, beta, B, Hv, Hk, dk, dv, 0.25)
+    assert bits_equal(o16, o32)
+    assert np.array_equal(S16n, S32n.astype(np.float16).view(np.uint16))
+    assert not np.array_equal(S16n, S16)  # the step changed the state
+
+
 # --------------------------------------------------------------------------
 # Chunkwise prefill
 # --------------------------------------------------------------------------
