@@ -29,21 +29,30 @@ struct ScanScratch {
     unsigned long long *aggG;
     unsigned long long *aggX;
     uint32_t *err;
-    size_t words;  // capacity of each status array
+    size_t words;   // capacity of each status array
+    int cu_count;   // compute units of the device (sizes the persistent grid)
 };
 
-constexpr int kScanTileT = 64;      // rows per tile
-constexpr int kScanThreads = 256;   // channels per tile (one per thread)
+constexpr int kScanThreads = 256;   // channels per tile (one per thread of a row group)
+// Rows per tile: cumulative decay (one input stream) and gated scan (two).
+constexpr int kScanRowsDecay = 128;
+constexpr int kScanRowsGated = 64;
 
-inline size_t scan_row_tiles(size_t seq) { return (seq + kScanTileT - 1) / kScanTileT; }
+inline size_t scan_tile_rows(int mode) { return mode == 0 ? kScanRowsDecay : kScanRowsGated; }
+inline size_t scan_row_tiles(size_t seq, int mode) {
+    return (seq + scan_tile_rows(mode) - 1) / scan_tile_rows(mode);
+}
 inline size_t scan_col_tiles(size_t ch) { return (ch + kScanThreads - 1) / kScanThreads; }
 
 // mode 0: cumdecay (out = prefix product of g; `narrow` applies to out)
 // mode 1: gated scan (s fp32; `narrow` applies to state)
+// On success *ids_used is the number of tile ids the launch takes from the
+// counter (the caller's next counter_base is counter_base + *ids_used).
 hipError_t launch_lookback_scan(int mode, int narrow, const float *g, const float *x,
                                 void *out, void *state, size_t seq, size_t ch,
                                 const ScanScratch &scr, unsigned long long counter_base,
-                                uint32_t epoch, hipStream_t st);
+                                uint32_t epoch, unsigned long long *ids_used,
+                                hipStream_t st);
 
 // ---- decode (gdn_decode.hip) ------------------------------------------------
 

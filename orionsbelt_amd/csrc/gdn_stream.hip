@@ -19,10 +19,14 @@ namespace {
 // Thread = VEC consecutive channels x one segment of seg_len timesteps.  The
 // three history inputs of a segment are read from `in` (rows t0-3..t0-1), or
 // from hist for segment 0, so segments are independent and the grid is
-// (channels / VEC / 256) x (seq / seg_len) blocks.  Only segment-0 threads
-// touch hist: they read it first and write the new history last, so no two
-// threads race on it.  FP contraction is off, making the K=4 dot product
-// ((h0*w0 + h1*w1) + h2*w2) + cur*w3 bit-identical to the portable scalar C.
+// (channels / VEC / 256) x (seq / seg_len) blocks.  Short segments (8 rows:
+// one group of row loads per thread, issued together) keep thousands of
+// workgroups streaming; the halo rows re-read from `in` were just read by
+// the neighbouring segment's workgroup on the same XCD and hit in L2.  Only
+// segment-0 threads touch hist: they read it first and write the new
+// history last, so no two threads race on it.  FP contraction is off, making
+// the K=4 dot product ((h0*w0 + h1*w1) + h2*w2) + cur*w3 bit-identical to the
+// portable scalar C.
 
 template <int VEC> struct Vec;
 template <> struct Vec<1> { using T = float; };
@@ -88,14 +92,14 @@ __global__ __launch_bounds__(256) void conv_k4_kernel(const float *__restrict__ 
     }
 
     for (int64_t t = t0; t < t1; t += U) {
+        // Row loads are unconditional (rows past the end clamp to the last
+        // row and are not used), so the U loads issue back to back.
         V cur[U];
-        const int n = (int)min((int64_t)U, t1 - t);
 #pragma unroll
-        for (int i = 0; i < U; ++i)
-            if (i < n) cur[i] = vload<VEC, NT>(in + (t + i) * ch + c);
+        for (int i = 0; i < U; ++i) cur[i] = vload<VEC, NT>(in + min(t + i, seq - 1) * ch + c);
 #pragma unroll
         for (int i = 0; i < U; ++i) {
-            if (i < n) {
+            if (t + i < t1) {
                 vstore<VEC, NT>(out + (t + i) * ch + c,
                                 conv_tap(h0, h1, h2, cur[i], w0, w1, w2, w3, SILU));
                 h0 = h1;
@@ -131,24 +135,34 @@ __global__ __launch_bounds__(256) void conv_k4_kernel(const float *__restrict__ 
 // scan, kai_gdn_gated_scan_f32_sve.c:86-95) or s_t = s_{t-1} * a_t from
 // s_{-1} = 1 (mode 0, kai cumdecay, kai_gdn_cumdecay_f32_sve.c:122-129).
 //
-// A tile is kScanTileT rows x 256 channels (one channel per thread, the tile
-// held in registers).  Tiles take ids from a device counter in order, row
-// tiles of a column strip in sequence order, so every tile a workgroup waits
-// for was started earlier by a running workgroup and never waits on a later
-// one: the wait always ends.  Per tile:
-//   1. load the tile; fold it into its aggregate map s -> AG*s + AX, in the
-//      reference's own order starting from the identity;
-//   2. publish the aggregate (row tile > 0);
-//   3. look back over predecessor tiles, composing aggregates until one
-//      publishes its inclusive state;
-//   4. re-run the reference recurrence over the tile from that carry,
-//      publish the inclusive state, store the tile.
-// Only the carry into a tile is re-associated; inside a tile the arithmetic
-// is the reference's, and row tile 0 is bit-identical to it.
+// A tile is RH * TS rows x 256 channels, held in registers by a workgroup of
+// RH row groups x 256 threads: thread (row group q, lane l) owns channel l
+// of rows q*TS .. q*TS+TS-1.  The kernel is persistent: a grid of as many
+// workgroups as fit on the device takes tile ids from a device counter in
+// order (row tiles of a column strip in sequence order), so every tile a
+// workgroup waits for is held by a running workgroup and was taken earlier.
+// Per tile:
+//   1. each row group folds its rows into a map s -> AG*s + AX, in the
+//      reference's order starting from the identity; the maps of the row
+//      groups are composed in LDS into the tile's aggregate;
+//   2. the tile publishes its aggregate (row tile > 0);
+//   3. row group 0 looks back over predecessor tiles, composing their
+//      aggregates until one has published its inclusive state;
+//   4. the row groups re-run the reference recurrence over their rows one
+//      after another from that carry (the carry passes between them in LDS),
+//      the last publishes the tile's inclusive state, and all store.
+// With PF the next tile id is taken and its rows are loaded before step 3,
+// so the look-back waits overlap the next tile's reads.  Only the carry into
+// a tile is re-associated; inside a tile the arithmetic is the reference's,
+// and row tile 0 is bit-identical to it.  Every tile a waiting workgroup
+// depends on has a smaller id; the smallest unfinished id is always some
+// workgroup's current tile, whose predecessors are all finished, so the
+// wait always ends.
+//
 // Status words are 64-bit: (epoch << 32) | float bits.  A word belongs to
 // the current launch iff its tag equals `epoch`, so each word validates
 // itself and no fences are needed; the arrays are never cleared between
-// launches.  The wait is bounded: past spin_limit polls the tile records an
+// launches.  The wait is bounded: past kSpinLimit polls the tile records an
 // error in *err and carries 0, so every wave exits.
 
 GDN_DEV unsigned long long pack_status(uint32_t epoch, float v) {
@@ -177,123 +191,215 @@ template <int NARROW> GDN_DEV void narrow_store(void *p, int64_t i, float v) {
 
 constexpr uint32_t kSpinLimit = 1u << 22;
 
-template <int MODE, int NARROW, int TT, bool NT>
-__global__ __launch_bounds__(kScanThreads) void lookback_scan_kernel(
+// Rows of one row group, loaded unconditionally.  WHOLE: the launch has only
+// whole tiles (seq and channels multiples of the tile), so plain addressing;
+// otherwise rows past the sequence end and lanes past the channel end clamp
+// to the last valid row / channel (their values are never used).
+template <int MODE, int TS, bool NT, bool WHOLE>
+GDN_DEV void scan_load_rows(const float *g, const float *x, int64_t seq, int64_t ch,
+                            int64_t row0, int64_t c, float (&gv)[TS], float (&xv)[TS]) {
+    const int64_t cc = WHOLE ? c : min(c, ch - 1);
+#pragma unroll
+    for (int i = 0; i < TS; ++i) {
+        const int64_t at = (WHOLE ? row0 + i : min(row0 + i, seq - 1)) * ch + cc;
+        if constexpr (NT) {
+            gv[i] = __builtin_nontemporal_load(g + at);
+            if constexpr (MODE == 1) xv[i] = __builtin_nontemporal_load(x + at);
+        } else {
+            gv[i] = g[at];
+            if constexpr (MODE == 1) xv[i] = x[at];
+        }
+    }
+}
+
+template <int MODE, int NARROW, bool NT>
+GDN_DEV void scan_store(void *out, int64_t at, float gvi, float xvi) {
+    float *o32 = static_cast<float *>(out) + at;
+    if constexpr (MODE == 1) {
+        if constexpr (NT) __builtin_nontemporal_store(xvi, o32);
+        else *o32 = xvi;
+    } else if constexpr (NARROW == kF32 && NT) {
+        __builtin_nontemporal_store(gvi, o32);
+    } else {
+        narrow_store<NARROW>(out, at, gvi);
+    }
+}
+
+template <int MODE, int NARROW, int TS, int RH, bool PF, bool NT, bool WHOLE>
+__global__ __launch_bounds__(kScanThreads *RH) void lookback_scan_kernel(
     const float *__restrict__ g, const float *__restrict__ x, void *out, void *state,
     int64_t seq, int64_t ch, int n_row_tiles, int n_col_tiles,
     unsigned long long *__restrict__ incl, unsigned long long *__restrict__ aggG,
     unsigned long long *__restrict__ aggX, unsigned long long *counter,
     unsigned long long counter_base, uint32_t epoch, uint32_t *err) {
 #pragma clang fp contract(off)
-    __shared__ long long s_tile;
-    if (threadIdx.x == 0) s_tile = (long long)(atomicAdd(counter, 1ull) - counter_base);
-    __syncthreads();
-    const long long tile = s_tile;
+    constexpr int TT = TS * RH;
+    __shared__ long long s_tile[2];
+    __shared__ float s_ag[RH][kScanThreads];
+    __shared__ float s_ax[RH][kScanThreads];
+    __shared__ float s_carry[RH][kScanThreads];
     const long long n_tiles = (long long)n_row_tiles * n_col_tiles;
-    if (tile < 0 || tile >= n_tiles) {  // only if launches were not serialised
+    const int sub = (int)threadIdx.x / kScanThreads;
+    const int lc = (int)threadIdx.x % kScanThreads;
+    auto take = [&]() { return (long long)(atomicAdd(counter, 1ull) - counter_base); };
+
+    if (threadIdx.x == 0) s_tile[0] = take();
+    __syncthreads();
+    long long tile = s_tile[0];
+    if (tile < 0) {  // only if launches were not serialised
         if (threadIdx.x == 0) atomicOr(err, 2u);
         return;
     }
-    const int r = (int)(tile / n_col_tiles);
-    const int cb = (int)(tile % n_col_tiles);
-    const int64_t c = (int64_t)cb * kScanThreads + threadIdx.x;
-    const bool live = c < ch;
-    const int64_t t0 = (int64_t)r * TT;
-    const int nt = (int)min((int64_t)TT, seq - t0);
-
-    float gv[TT], xv[TT];
-#pragma unroll
-    for (int i = 0; i < TT; ++i) {
-        if (live && i < nt) {
-            if constexpr (NT) {
-                gv[i] = __builtin_nontemporal_load(g + (t0 + i) * ch + c);
-                if constexpr (MODE == 1) xv[i] = __builtin_nontemporal_load(x + (t0 + i) * ch + c);
-            } else {
-                gv[i] = g[(t0 + i) * ch + c];
-                if constexpr (MODE == 1) xv[i] = x[(t0 + i) * ch + c];
-            }
-        }
+    float gv[TS], xv[TS], gn[PF ? TS : 1], xn[PF ? TS : 1];
+    // tile t: row tile r, first row of this row group, this thread's channel
+    auto tile_rows = [&](long long t, int64_t &row0, int64_t &c) {
+        const int r = (int)(t / n_col_tiles), cb = (int)(t % n_col_tiles);
+        row0 = (int64_t)r * TT + (int64_t)sub * TS;
+        c = (int64_t)cb * kScanThreads + lc;
+        return r;
+    };
+    if (tile < n_tiles) {
+        int64_t row0, c;
+        tile_rows(tile, row0, c);
+        scan_load_rows<MODE, TS, NT, WHOLE>(g, x, seq, ch, row0, c, gv, xv);
     }
+    for (int it = 0; tile < n_tiles; ++it) {
+        int64_t row0, c;
+        const int r = tile_rows(tile, row0, c);
+        const bool live = WHOLE || c < ch;
+        const int nrows = WHOLE ? TS : (int)max((int64_t)0, min((int64_t)TS, seq - row0));
+        long long next = n_tiles;
+        if constexpr (PF)
+            if (threadIdx.x == 0) s_tile[(it + 1) & 1] = take();
 
-    float carry = 0.f;
-    if (r == 0) {
-        if (live) carry = (MODE == 0) ? 1.0f : narrow_load<NARROW>(state, c);
-    } else if (live) {
-        // 1. aggregate of this tile, identity start, reference order
-        float AG = 1.0f, AX = 0.0f;
+        // 1. this row group's map, identity start, reference order
+        {
+            float AG = 1.0f, AX = 0.0f;
 #pragma unroll
-        for (int i = 0; i < TT; ++i) {
-            if (i < nt) {
-                if constexpr (MODE == 1) AX = xv[i] + AX * gv[i];
-                AG = AG * gv[i];
-            }
-        }
-        // 2. publish it
-        const int64_t me = (int64_t)r * ch + c;
-        store_status(aggG + me, pack_status(epoch, AG));
-        if constexpr (MODE == 1) store_status(aggX + me, pack_status(epoch, AX));
-        // 3. look back
-        float GA = 1.0f, XA = 0.0f;
-        int p = r - 1;
-        uint32_t spins = 0;
-        for (;;) {
-            const int64_t at = (int64_t)p * ch + c;
-            const unsigned long long wi = load_status(incl + at);
-            if (status_tag(wi) == epoch) {
-                const float sp = status_val(wi);
-                carry = (MODE == 0) ? GA * sp : GA * sp + XA;
-                break;
-            }
-            const unsigned long long wg = load_status(aggG + at);
-            const unsigned long long wx = (MODE == 1) ? load_status(aggX + at) : wg;
-            if (p > 0 && status_tag(wg) == epoch && status_tag(wx) == epoch) {
-                if constexpr (MODE == 1) XA = GA * status_val(wx) + XA;
-                GA = GA * status_val(wg);
-                --p;
-                spins = 0;
-                continue;
-            }
-            if (++spins > kSpinLimit) {
-                atomicOr(err, 1u);
-                carry = 0.f;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
-
-    // 4. the reference recurrence from the carry, in registers
-    float run = carry;
-#pragma unroll
-    for (int i = 0; i < TT; ++i) {
-        if (i < nt) {
-            if constexpr (MODE == 1) {
-                run = xv[i] + run * gv[i];
-                xv[i] = run;
-            } else {
-                run = run * gv[i];
-                gv[i] = run;
-            }
-        }
-    }
-    if (live) {
-        if (r + 1 < n_row_tiles) store_status(incl + (int64_t)r * ch + c, pack_status(epoch, run));
-#pragma unroll
-        for (int i = 0; i < TT; ++i) {
-            if (i < nt) {
-                float *o32 = static_cast<float *>(out) + (t0 + i) * ch + c;
-                if constexpr (MODE == 1) {
-                    if constexpr (NT) __builtin_nontemporal_store(xv[i], o32);
-                    else *o32 = xv[i];
-                } else if constexpr (NARROW == kF32 && NT) {
-                    __builtin_nontemporal_store(gv[i], o32);
-                } else {
-                    narrow_store<NARROW>(out, (t0 + i) * ch + c, gv[i]);
+            for (int i = 0; i < TS; ++i) {
+                if (i < nrows) {
+                    if constexpr (MODE == 1) AX = xv[i] + AX * gv[i];
+                    AG = AG * gv[i];
                 }
             }
+            s_ag[sub][lc] = AG;
+            if constexpr (MODE == 1) s_ax[sub][lc] = AX;
         }
-        if constexpr (MODE == 1)
-            if (r == n_row_tiles - 1) narrow_store<NARROW>(state, c, run);
+        __syncthreads();
+        if constexpr (PF) {
+            next = s_tile[(it + 1) & 1];
+            if (next < n_tiles) {
+                int64_t nrow0, nc_;
+                tile_rows(next, nrow0, nc_);
+                scan_load_rows<MODE, TS, NT, WHOLE>(g, x, seq, ch, nrow0, nc_, gn, xn);
+            }
+        }
+
+        if (sub == 0) {
+            float carry = 0.f;
+            if (r == 0) {
+                if (live) carry = (MODE == 0) ? 1.0f : narrow_load<NARROW>(state, c);
+            } else if (live) {
+                // the tile's map: row-group maps composed in row order
+                float AG = s_ag[0][lc], AX = (MODE == 1) ? s_ax[0][lc] : 0.f;
+#pragma unroll
+                for (int q = 1; q < RH; ++q) {
+                    if constexpr (MODE == 1) AX = s_ax[q][lc] + AX * s_ag[q][lc];
+                    AG = AG * s_ag[q][lc];
+                }
+                // 2. publish it
+                const int64_t me = (int64_t)r * ch + c;
+                store_status(aggG + me, pack_status(epoch, AG));
+                if constexpr (MODE == 1) store_status(aggX + me, pack_status(epoch, AX));
+                // 3. look back
+                float GA = 1.0f, XA = 0.0f;
+                int p = r - 1;
+                uint32_t spins = 0;
+                for (;;) {
+                    const int64_t at = (int64_t)p * ch + c;
+                    const unsigned long long wi = load_status(incl + at);
+                    if (status_tag(wi) == epoch) {
+                        const float sp = status_val(wi);
+                        carry = (MODE == 0) ? GA * sp : GA * sp + XA;
+                        break;
+                    }
+                    const unsigned long long wg = load_status(aggG + at);
+                    const unsigned long long wx = (MODE == 1) ? load_status(aggX + at) : wg;
+                    if (p > 0 && status_tag(wg) == epoch && status_tag(wx) == epoch) {
+                        if constexpr (MODE == 1) XA = GA * status_val(wx) + XA;
+                        GA = GA * status_val(wg);
+                        --p;
+                        spins = 0;
+                        continue;
+                    }
+                    if (++spins > kSpinLimit) {
+                        atomicOr(err, 1u);
+                        carry = 0.f;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            s_carry[0][lc] = carry;
+        }
+
+        // 4. the reference recurrence from the carry, row group by row group
+        float run = 0.f;
+#pragma unroll
+        for (int q = 0; q < RH; ++q) {
+            __syncthreads();
+            if (sub == q) {
+                run = s_carry[q][lc];
+#pragma unroll
+                for (int i = 0; i < TS; ++i) {
+                    if (i < nrows) {
+                        if constexpr (MODE == 1) {
+                            run = xv[i] + run * gv[i];
+                            xv[i] = run;
+                        } else {
+                            run = run * gv[i];
+                            gv[i] = run;
+                        }
+                    }
+                }
+                if (q + 1 < RH) s_carry[q + 1][lc] = run;
+            }
+        }
+        if (live && sub == RH - 1) {
+            if (r + 1 < n_row_tiles)
+                store_status(incl + (int64_t)r * ch + c, pack_status(epoch, run));
+            if constexpr (MODE == 1)
+                if (r == n_row_tiles - 1) narrow_store<NARROW>(state, c, run);
+        }
+        // Whole tiles store unpredicated: per-row predicates split the stores
+        // into separate blocks and cost about 15% of the bandwidth.
+        if constexpr (WHOLE) {
+#pragma unroll
+            for (int i = 0; i < TS; ++i) scan_store<MODE, NARROW, NT>(out, (row0 + i) * ch + c, gv[i], xv[i]);
+        } else if (live) {
+#pragma unroll
+            for (int i = 0; i < TS; ++i)
+                if (i < nrows) scan_store<MODE, NARROW, NT>(out, (row0 + i) * ch + c, gv[i], xv[i]);
+        }
+
+        if constexpr (PF) {
+#pragma unroll
+            for (int i = 0; i < TS; ++i) {
+                gv[i] = gn[i];
+                if constexpr (MODE == 1) xv[i] = xn[i];
+            }
+        } else {
+            __syncthreads();
+            if (threadIdx.x == 0) s_tile[(it + 1) & 1] = take();
+            __syncthreads();
+            next = s_tile[(it + 1) & 1];
+            if (next < n_tiles) {
+                int64_t nrow0, nc_;
+                tile_rows(next, nrow0, nc_);
+                scan_load_rows<MODE, TS, NT, WHOLE>(g, x, seq, ch, nrow0, nc_, gv, xv);
+            }
+        }
+        tile = next;
     }
 }
 
@@ -328,12 +434,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ a,
 
 // Production configuration of the streaming kernels, measured on MI355X at
 // [4096][8192] with buffers rotated so every launch streams from HBM:
-// non-temporal traffic and 64-row conv segments (55.4 us vs 59.7 us cached
-// with 32-row segments); 64-row scan tiles (59.4 us; 32 rows: 76 us).
+// non-temporal traffic and 8-row conv segments, 4096 workgroups (46.9 us;
+// 64-row segments 57.1 us, cached loads 52.2 us).
 constexpr bool kConvNT = true;
 constexpr int64_t kConvTargetBlocks = 4096;
-constexpr int64_t kConvMinSeg = 64;
-constexpr bool kScanNT = true;
+constexpr int64_t kConvMinSeg = 8;
 
 // ---------------------------------------------------------------------------
 // Launchers
@@ -381,29 +486,60 @@ hipError_t launch_gemv(const float *a, const float *b, float *c, size_t k, size_
     return hipGetLastError();
 }
 
-template <int MODE, int NARROW, int TT = kScanTileT, bool NT = kScanNT>
-static void launch_scan_t(const float *g, const float *x, void *out, void *state, size_t seq,
-                          size_t ch, int nr, int nc, const ScanScratch &s,
-                          unsigned long long base, uint32_t epoch, hipStream_t st) {
-    dim3 grid((unsigned)((size_t)nr * nc)), block(kScanThreads);
-    lookback_scan_kernel<MODE, NARROW, TT, NT><<<grid, block, 0, st>>>(
-        g, x, out, state, (int64_t)seq, (int64_t)ch, nr, nc, s.incl, s.aggG, s.aggX, s.counter,
-        base, epoch, s.err);
+// Scan tiles: cumdecay 2 row groups x 64 rows, gated scan 2 x 32 (two input
+// streams), both prefetching the next tile.  Measured at [4096][8192]
+// cumdecay: 45.7 us (one-shot 64-row tiles without look-ahead: 59.7 us).
+template <int MODE> struct ScanCfg;
+template <> struct ScanCfg<0> { static constexpr int TS = kScanRowsDecay / 2, RH = 2; };
+template <> struct ScanCfg<1> { static constexpr int TS = kScanRowsGated / 2, RH = 2; };
+constexpr bool kScanNT = true;
+
+template <int MODE, int NARROW, bool WHOLE>
+static hipError_t launch_scan_t(const float *g, const float *x, void *out, void *state,
+                                size_t seq, size_t ch, int nr, int nc, const ScanScratch &s,
+                                unsigned long long base, uint32_t epoch,
+                                unsigned long long *ids_used, hipStream_t st) {
+    using Cfg = ScanCfg<MODE>;
+    auto kern = lookback_scan_kernel<MODE, NARROW, Cfg::TS, Cfg::RH, true, kScanNT, WHOLE>;
+    constexpr int threads = kScanThreads * Cfg::RH;
+    // Persistent grid: as many workgroups as are resident at once.
+    static int cached = -1;  // same code object on every device
+    int per_cu = __atomic_load_n(&cached, __ATOMIC_RELAXED);
+    if (per_cu < 0) {
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0);
+        if (e != hipSuccess) return e;
+        __atomic_store_n(&cached, per_cu, __ATOMIC_RELAXED);
+    }
+    if (per_cu < 1) return hipErrorLaunchOutOfResources;
+    const long long n_tiles = (long long)nr * nc;
+    const long long slots = (long long)per_cu * (s.cu_count > 0 ? s.cu_count : 1);
+    const unsigned grid = (unsigned)(n_tiles < slots ? n_tiles : slots);
+    kern<<<dim3(grid), dim3(threads), 0, st>>>(g, x, out, state, (int64_t)seq, (int64_t)ch, nr,
+                                               nc, s.incl, s.aggG, s.aggX, s.counter, base,
+                                               epoch, s.err);
+    // every workgroup takes one id past the last tile before it exits
+    *ids_used = (unsigned long long)n_tiles + grid;
+    return hipGetLastError();
 }
 
 hipError_t launch_lookback_scan(int mode, int narrow, const float *g, const float *x, void *out,
                                 void *state, size_t seq, size_t ch, const ScanScratch &scr,
                                 unsigned long long counter_base, uint32_t epoch,
-                                hipStream_t st) {
+                                unsigned long long *ids_used, hipStream_t st) {
+    *ids_used = 0;
     if (seq == 0 || ch == 0) return hipSuccess;
-    const int nr = (int)scan_row_tiles(seq);
+    if (mode != 0 && mode != 1) return hipErrorInvalidValue;
+    const int nr = (int)scan_row_tiles(seq, mode);
     const int nc = (int)scan_col_tiles(ch);
     if ((size_t)nr * ch > scr.words) return hipErrorInvalidValue;
-#define GDN_SCAN_CASE(M, N)                                                                  \
-    if (mode == M && narrow == N) {                                                          \
-        launch_scan_t<M, N>(g, x, out, state, seq, ch, nr, nc, scr, counter_base, epoch, st); \
-        return hipGetLastError();                                                            \
-    }
+    // Shapes made of whole tiles take the unpredicated kernel.
+    const bool whole = seq % scan_tile_rows(mode) == 0 && ch % kScanThreads == 0;
+#define GDN_SCAN_CASE(M, N)                                                                     \
+    if (mode == M && narrow == N)                                                               \
+        return whole ? launch_scan_t<M, N, true>(g, x, out, state, seq, ch, nr, nc, scr,        \
+                                                 counter_base, epoch, ids_used, st)             \
+                     : launch_scan_t<M, N, false>(g, x, out, state, seq, ch, nr, nc, scr,       \
+                                                  counter_base, epoch, ids_used, st);
     GDN_SCAN_CASE(0, kF32)
     GDN_SCAN_CASE(0, kF16)
     GDN_SCAN_CASE(0, kBF16)

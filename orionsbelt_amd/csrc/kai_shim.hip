@@ -15,8 +15,9 @@
 // Per-device state (created lazily under a mutex): an internal stream for
 // the synchronous symbols, staging buffers, the look-back scan scratch and
 // the prefill workspace.  Scan launches are serialised per device (host
-// mutex + an event the next scan waits on) because they share the tile
-// counter and status arrays; every other kernel is free of shared state.
+// mutex; stream order, or a device synchronisation when the stream changes)
+// because they share the tile counter and status arrays; every other kernel
+// is free of shared state.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -65,7 +66,8 @@ struct DeviceCtx {
     size_t scan_words = 0;
     unsigned long long counter_value = 0;
     uint32_t epoch = 0;
-    hipEvent_t scan_done = nullptr;
+    // the last scan launch: its stream, and whether it may still be running
+    hipStream_t scan_stream = nullptr;
     bool scan_pending = false;
     // prefill workspace and the second stream its phases overlap on
     DevBuf chunk_ws;
@@ -92,19 +94,23 @@ hipError_t get_ctx(DeviceCtx **out) {
     if (!c->ready) {
         e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
         if (e != hipSuccess) return e;
-        e = hipEventCreateWithFlags(&c->scan_done, hipEventDisableTiming);
-        if (e != hipSuccess) return e;
         e = hipMalloc(&c->scan.counter, 256);
         if (e != hipSuccess) return e;
         e = hipMemset(c->scan.counter, 0, 256);
         if (e != hipSuccess) return e;
         c->scan.err = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(c->scan.counter) + 64);
+        e = hipDeviceGetAttribute(&c->scan.cu_count, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
         e = hipStreamCreateWithFlags(&c->pf.aux, hipStreamNonBlocking);
         if (e != hipSuccess) return e;
         hipEvent_t *evs[6] = {&c->pf.ready, &c->pf.a_done[0], &c->pf.a_done[1], &c->pf.b_done[0],
                               &c->pf.b_done[1], &c->pf_done};
         for (hipEvent_t *ev : evs)
-            if ((e = hipEventCreateWithFlags(ev, hipEventDisableTiming)) != hipSuccess) return e;
+            // Device-scope release: these events only order work on this
+            // device (cheaper than the default system-scope release).
+            if ((e = hipEventCreateWithFlags(ev, hipEventDisableTiming | hipEventReleaseToDevice)) !=
+                hipSuccess)
+                return e;
         c->ready = true;
     }
     *out = c;
@@ -117,8 +123,9 @@ hipError_t scan_reserve(DeviceCtx *c, size_t words) {
     if (words <= c->scan_words) return hipSuccess;
     hipError_t e;
     if (c->scan_pending) {
-        e = hipEventSynchronize(c->scan_done);
+        e = hipDeviceSynchronize();
         if (e != hipSuccess) return e;
+        c->scan_pending = false;
     }
     if (c->scan.incl) {
         (void)hipFree(c->scan.incl);
@@ -147,26 +154,34 @@ hipError_t run_scan(int mode, int narrow, const float *g, const float *x, void *
     hipError_t e = get_ctx(&c);
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lk(c->mu);
-    const size_t nr = gdn::scan_row_tiles(seq), nc = gdn::scan_col_tiles(ch);
+    const size_t nr = gdn::scan_row_tiles(seq, mode);
     e = scan_reserve(c, nr * ch);
     if (e != hipSuccess) return e;
     if (c->epoch == 0xFFFFFFFFu) {  // tag space exhausted: clear and restart
-        if (c->scan_pending && (e = hipEventSynchronize(c->scan_done)) != hipSuccess) return e;
+        if (c->scan_pending && (e = hipDeviceSynchronize()) != hipSuccess) return e;
+        c->scan_pending = false;
         e = hipMemset(c->scan.incl, 0, 3 * c->scan_words * sizeof(unsigned long long));
         if (e != hipSuccess) return e;
         c->epoch = 0;
     }
     const uint32_t epoch = ++c->epoch;
     const unsigned long long base = c->counter_value;
-    if (c->scan_pending) {
-        e = hipStreamWaitEvent(st, c->scan_done, 0);
+    // Scans share the counter and status words, so a scan must not start
+    // before the previous one ends.  On the same stream, stream order does
+    // that at no cost (an event after every launch costs about 5 us here).
+    // On another stream, the previous stream may no longer exist, so wait
+    // for the device.
+    if (c->scan_pending && st != c->scan_stream) {
+        e = hipDeviceSynchronize();
         if (e != hipSuccess) return e;
+        c->scan_pending = false;
     }
-    e = gdn::launch_lookback_scan(mode, narrow, g, x, out, state, seq, ch, c->scan, base, epoch, st);
+    unsigned long long used = 0;
+    e = gdn::launch_lookback_scan(mode, narrow, g, x, out, state, seq, ch, c->scan, base, epoch,
+                                  &used, st);
     if (e != hipSuccess) return e;
-    c->counter_value += (unsigned long long)(nr * nc);
-    e = hipEventRecord(c->scan_done, st);
-    if (e != hipSuccess) return e;
+    c->counter_value += used;
+    c->scan_stream = st;
     c->scan_pending = true;
     return hipSuccess;
 }
@@ -222,6 +237,13 @@ void finish(DeviceCtx *c, Arg *args, int n) {
             check(hipMemcpyAsync(args[i].dst, args[i].dev, args[i].bytes, hipMemcpyDeviceToHost, c->stream),
                   "hipMemcpyAsync D2H");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+// After a synchronous call has drained the internal stream: a scan launched
+// there has ended.
+void scan_settled(DeviceCtx *c) {
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (c->scan_stream == c->stream) c->scan_pending = false;
 }
 
 DeviceCtx *sync_ctx() {
@@ -422,6 +444,7 @@ extern "C" void kai_run_gdn_cumdecay_f32_sve(const float *a, float *decay, size_
                    channels, c->stream),
           "cumdecay launch");
     finish(c, args, 2);
+    scan_settled(c);
 }
 
 extern "C" void kai_run_gdn_gated_scan_f32_sve(const float *g, const float *x, float *s,
@@ -437,6 +460,7 @@ extern "C" void kai_run_gdn_gated_scan_f32_sve(const float *g, const float *x, f
                    args[2].dev, args[3].dev, seq, channels, c->stream),
           "gated_scan launch");
     finish(c, args, 4);
+    scan_settled(c);
 }
 
 extern "C" void kai_run_gdn_causal_dwconv1d_f32_k4_sve(const float *in, const float *w,

@@ -2,7 +2,9 @@
 mixed-precision variants) against the CPU oracle, through the C-ABI.
 
 Bars: bit-identical where the kernel keeps the reference's operation order
-(conv without SiLU, GEMV, and cumdecay / scan inside one 64-row tile);
+(conv without SiLU, GEMV, cumdecay inside one 128-row tile and the gated
+scan inside one 64-row tile, including tiles whose second row group is
+partly or wholly past the end);
 otherwise the reference test's own tolerances (test_kai_gdn.c:190,222,434)
 and BASELINE's 1e-5 relative for fp32 decay and conv+SiLU.
 """
@@ -144,16 +146,16 @@ def run_scan(L, g, x, st, seq, ch, fmt="f32"):
 
 def test_cumdecay_reference_sweep(L):
     rng = lcg(0x1234)
-    for seq in REF_SEQS:
-        for ch in REF_CHANS + [129, 300]:
+    for seq in REF_SEQS + [65, 100, 128]:
+        for ch in REF_CHANS + [129, 256, 300, 512]:  # 256, 512: whole-tile kernel at 128 rows
             a = rng.uniform(seq * ch, 0.5, 1.5)
             got = run_cumdecay(L, a, seq, ch)
             ref = orc.cumdecay_f32(a, seq, ch)
-            # seq <= 64 is one row tile: the reference order exactly
+            # seq <= 128 is one row tile: the reference order exactly
             assert np.array_equal(bits(got), bits(ref)), (seq, ch)
 
 
-@pytest.mark.parametrize("seq,ch", [(65, 7), (200, 300), (1000, 513), (4096, 8192)])
+@pytest.mark.parametrize("seq,ch", [(129, 7), (200, 300), (1000, 513), (4096, 8192)])
 def test_cumdecay_multi_tile(L, seq, ch):
     rs = np.random.RandomState(seq)
     g = (-np.log1p(np.exp(rs.randn(seq * ch))) * np.exp(rs.uniform(-2, 0, seq * ch)))
@@ -170,8 +172,8 @@ def test_cumdecay_multi_tile(L, seq, ch):
 
 def test_gated_scan_reference_sweep(L):
     rng = lcg(0x777)
-    for seq in REF_SEQS:
-        for ch in REF_CHANS + [255]:
+    for seq in REF_SEQS + [33, 40]:
+        for ch in REF_CHANS + [255, 256]:  # 256: whole-tile kernel at 64 rows
             g = rng.uniform(seq * ch, -0.99, 0.99)
             x = rng.uniform(seq * ch, -2, 2)
             st = rng.uniform(ch, -1, 1)
