@@ -103,15 +103,20 @@ int kai_run_gdn_delta_rule_decode_f16state_hip(uint16_t *S, const float *q,
  * The algorithm of HF torch_chunk_gated_delta_rule (modeling_qwen3_5.py:
  * 248-328) with chunk size 64: per chunk, the UT transform
  * T = (I + tril(beta K K^T * Gamma, -1))^-1, W = T (beta K e^G),
- * U = T (beta V) and the masked Q K^T run in parallel over chunks; the state
- * recurrence across chunks is sequential.  q,k,v bf16 (bit patterns),
- * products on bf16 MFMA with fp32 accumulation, fp32 state.
+ * U = T (beta V) and the masked Q K^T, then the state recurrence.  The
+ * recurrence is affine in the state, so long sequences are cut into segments
+ * that run in parallel (each segment's transition is composed with its
+ * predecessors'), then rerun from their true start states.  q,k,v bf16 (bit
+ * patterns), products on bf16 MFMA with fp32 accumulation, fp32 state.
  * Layouts (token-major, HF's [B, T, H, D]):
  *   q,k [batch][seq_len][num_k_heads][128]   v [batch][seq_len][num_v_heads][128]
  *   g,beta [batch][seq_len][num_v_heads] fp32 (g = log-gate, beta = write gate)
  *   o [batch][seq_len][num_v_heads][128] bf16
  *   S [batch][num_v_heads][128][128] fp32: initial state in, final state out.
- * seq_len need not be a multiple of 64.  head_k_dim = head_v_dim = 128. */
+ * seq_len need not be a multiple of 64.  head_k_dim = head_v_dim = 128.
+ * Results depend on where a sequence is cut into segments only within the
+ * bf16 rounding bound; calls on one device must not overlap (they share a
+ * carry buffer; calls on one stream never do). */
 int kai_run_gdn_chunk_delta_rule_bf16_f32_hip(const uint16_t *q, const uint16_t *k,
                                               const uint16_t *v, const float *g,
                                               const float *beta, uint16_t *o,

@@ -61,28 +61,18 @@ hipError_t launch_delta_decode(int narrow_state, void *S, const float *q, const 
                                int B, int Hv, int Hk, int dk, int dv, float q_scale,
                                hipStream_t st);
 
-// ---- chunked prefill (gdn_chunk.hip) ----------------------------------------
+// ---- chunked prefill (gdn_prefill.hip) --------------------------------------
 
 constexpr int kChunk = 64;
 constexpr int kHeadDim = 128;
 
-// Bytes of device workspace the prefill needs for one call.
-size_t chunk_workspace_bytes(int B, int T, int Hv);
-
-// A second stream and events that let phase A of segment s+1 run while
-// phase B of segment s runs on the caller's stream.  aux == nullptr runs
-// everything on the caller's stream.
-struct PrefillStreams {
-    hipStream_t aux;
-    hipEvent_t ready;       // the caller's stream reached the prefill
-    hipEvent_t a_done[2];   // phase A finished filling workspace buffer i
-    hipEvent_t b_done[2];   // phase B finished reading workspace buffer i
-};
-
-hipError_t launch_chunk_prefill(int narrow_state, const uint16_t *q, const uint16_t *k,
-                                const uint16_t *v, const float *g, const float *beta,
-                                uint16_t *o, void *S, int B, int T, int Hv, int Hk,
-                                float q_scale, void *workspace, const PrefillStreams &ps,
-                                hipStream_t st);
+// Chunkwise prefill, parallel over the sequence.  `carry` holds
+// prefill_carry_bytes(B, T, Hv) bytes of device memory (segment transitions
+// and start states); calls that share it must not overlap.
+size_t prefill_carry_bytes(int B, int T, int Hv);
+hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_t *k,
+                              const uint16_t *v, const float *g, const float *beta, uint16_t *o,
+                              void *S, int B, int T, int Hv, int Hk, float q_scale, void *carry,
+                              hipStream_t st);
 
 }  // namespace gdn

@@ -1,0 +1,910 @@
+// gdn_prefill.hip -- chunkwise (WY) gated delta rule prefill for gfx950,
+// parallel over the sequence.
+//
+// Algorithm: HF torch_chunk_gated_delta_rule (transformers
+// modeling_qwen3_5.py:248-328), chunk size 64, head dims 128.  Per (sequence
+// b, value head h, chunk n) with G = cumsum(g) inside the chunk and
+// Gamma_ij = exp(G_i - G_j) (i >= j):
+//   M = tril(beta_i (k_i . k_j) Gamma_ij, -1)       T = (I + M)^-1
+//   U = T diag(beta) V        W = T diag(beta e^G) K
+//   A = tril(Gamma_ij (q_i . k_j)) * scale
+// and, sequentially over chunks, with S the [128 x 128] state:
+//   v_new = U - W S ;  o = e^G scale (q S) + A v_new ;
+//   S' = e^{G_last} S + K^T diag(e^{G_last - G}) v_new
+//
+// Parallel over the sequence.  The step is affine in S:
+//   S' = Phi_n S + C_n,  Phi_n = e^{G_last} I - K^T diag(e^{G_last-G}) W,
+//   C_n = K^T diag(e^{G_last-G}) U,
+// so the chunks are cut into P segments and
+//   pass 1: segment 0 runs the recurrence from the initial state (with o);
+//           every middle segment p runs it from S = 0 and, alongside, on
+//           128 more state columns started at I with U = 0, which yields its
+//           local result C_p and its transition Phi_p;
+//   combine: S_start(p+1) = Phi_p S_start(p) + C_p, p = 1 .. P-2;
+//   pass 2: segments 1 .. P-1 rerun the recurrence from S_start(p), with o.
+// The work is twice that of one sequential pass, spread over (P-1) x heads
+// workgroups instead of heads.
+//
+// Each workgroup (4 waves) owns one (sequence, head, segment) and walks its
+// chunks.  Per chunk, stage A (all waves, LDS) loads the chunk's k, q, v
+// rows, forms K K^T and Q K^T on bf16 MFMA, solves for T in fp32 and
+// computes W on MFMA.  Stage B (each wave, its own state columns) runs the
+// recurrence: the state and v_new never leave registers.  That works
+// because the 32 k-indices of one 16x16x32 MFMA may be assigned to lanes in
+// any order as long as both operands use the same order: with lane group g
+// holding k = {4g..4g+3, 16+4g..16+4g+3} of each 32-block, the accumulator
+// layout of two stacked 16x16 tiles (lane group g holds rows 4g..4g+3 of
+// each) is exactly the B operand of the next product.  Operands that live in
+// LDS are read in that order with 8-byte reads, or with the gfx950 LDS
+// transpose read (ds_read_b64_tr_b16) where the stored orientation is the
+// other one.
+#include "gdn_common.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+namespace {
+
+constexpr int C = kChunk;     // 64
+constexpr int D = kHeadDim;   // 128
+constexpr int PD = D + 8;     // bf16 row pitch of [.][D] tiles (272 B)
+constexpr int PC = C + 8;     // bf16 row pitch of [.][C] tiles (144 B)
+constexpr int PF = C + 1;     // fp32 row pitch of the solve's [.][C] tiles
+
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
+
+// ---------------------------------------------------------------------------
+// Operand fragments of mfma_f32_16x16x32_bf16 in the permuted k order.
+// Lane (g, r), g = lane / 16, r = lane % 16, holds k-slots s = 0..7 of a
+// 32-block as k = 4g + s (s < 4) and k = 16 + 4g + (s - 4) (s >= 4).
+// ---------------------------------------------------------------------------
+
+GDN_DEV u32x4_t join(u32x2_t a, u32x2_t b) {
+    u32x4_t v;
+    v[0] = a[0];
+    v[1] = a[1];
+    v[2] = b[0];
+    v[3] = b[1];
+    return v;
+}
+
+// A operand from a row-major tile: A[m][k] = base[(row0 + m) * pitch + k0 + k].
+GDN_DEV bf16x8_t frag_rows(const uint16_t *base, int pitch, int row0, int k0, int g, int r) {
+    const uint16_t *p = base + (row0 + r) * pitch + k0 + 4 * g;
+    return as_bf16x8(join(*reinterpret_cast<const u32x2_t *>(p),
+                          *reinterpret_cast<const u32x2_t *>(p + 16)));
+}
+
+// Transposing LDS read: within each group of 16 lanes, output lane 4m+e gets
+// element e of the 8-byte rows addressed by lanes m, m+4, m+8, m+12.
+GDN_DEV u32x2_t lds_tr(const uint16_t *p) {
+    const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(p));
+    u32x2_t u;
+    u[0] = (uint32_t)(uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16);
+    u[1] = (uint32_t)(uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16);
+    return u;
+}
+
+// Operand whose k runs down the rows of a stored tile:
+// element (k, n) = base[(k0 + k) * pitch + col0 + n], n = r.  As an A operand
+// that is A[m][k] = base[k][col0 + m], i.e. the transpose of the stored tile.
+GDN_DEV bf16x8_t frag_tr(const uint16_t *base, int pitch, int k0, int col0, int g, int r) {
+    const uint16_t *p = base + (k0 + 4 * g + (r >> 2)) * pitch + col0 + 4 * (r & 3);
+    return as_bf16x8(join(lds_tr(p), lds_tr(p + 16 * pitch)));
+}
+
+// B operand from two stacked accumulator tiles (rows 0..15 and 16..31 of
+// the 32-block), optionally scaled per row.
+GDN_DEV bf16x8_t frag_acc(const f32x4_t &lo, const f32x4_t &hi) {
+    u32x4_t u;
+    u[0] = pack2_bf16_hw(lo[0], lo[1]);
+    u[1] = pack2_bf16_hw(lo[2], lo[3]);
+    u[2] = pack2_bf16_hw(hi[0], hi[1]);
+    u[3] = pack2_bf16_hw(hi[2], hi[3]);
+    return as_bf16x8(u);
+}
+GDN_DEV bf16x8_t frag_acc_scaled(const f32x4_t &lo, const f32x4_t &hi, const float *slo,
+                                 const float *shi) {
+    u32x4_t u;
+    u[0] = pack2_bf16_hw(lo[0] * slo[0], lo[1] * slo[1]);
+    u[1] = pack2_bf16_hw(lo[2] * slo[2], lo[3] * slo[3]);
+    u[2] = pack2_bf16_hw(hi[0] * shi[0], hi[1] * shi[1]);
+    u[3] = pack2_bf16_hw(hi[2] * shi[2], hi[3] * shi[3]);
+    return as_bf16x8(u);
+}
+
+// Natural-order A/B operand of a row-major tile (used where both operands
+// come from LDS): element k = 8g + s of row row0 + r.
+GDN_DEV bf16x8_t frag_nat(const uint16_t *base, int pitch, int row0, int k0, int g, int r) {
+    return as_bf16x8(*reinterpret_cast<const u32x4_t *>(base + (row0 + r) * pitch + k0 + 8 * g));
+}
+
+// ---------------------------------------------------------------------------
+// 16x16x16 MFMA helpers.  Layout: A lane (g, r) = A[r][4g..4g+3],
+// B lane (g, r) = B[4g..4g+3][r], C lane (g, r) = C[4g..4g+3][r].  So the
+// accumulator of a 16x16 tile is the B operand of the next product, and the
+// accumulator of X^T is the A operand of X: X Y = mfma(C(X^T), C(Y)).
+// ---------------------------------------------------------------------------
+
+typedef short s4_t __attribute__((ext_vector_type(4)));
+
+GDN_DEV f32x4_t mfma16(s4_t a, s4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+GDN_DEV s4_t bf4(const f32x4_t &x) {
+    u32x2_t u;
+    u[0] = pack2_bf16_hw(x[0], x[1]);
+    u[1] = pack2_bf16_hw(x[2], x[3]);
+    return __builtin_bit_cast(s4_t, u);
+}
+GDN_DEV f32x4_t unbf4(s4_t v) {
+    f32x4_t x;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = bf16_to_f32((uint16_t)v[e]);
+    return x;
+}
+// c + A B with fp32 fragments split into bf16 hi + lo parts (the lo*lo term
+// dropped): about 16 bits of precision.
+GDN_DEV f32x4_t mfma16x3(const f32x4_t &a, const f32x4_t &b, f32x4_t c) {
+    const s4_t ah = bf4(a), bh = bf4(b);
+    const f32x4_t ar = a - unbf4(ah), br = b - unbf4(bh);
+    c = mfma16(ah, bh, c);
+    c = mfma16(ah, bf4(br), c);
+    c = mfma16(bf4(ar), bh, c);
+    return c;
+}
+
+// ---------------------------------------------------------------------------
+// Shared memory and stage A
+// ---------------------------------------------------------------------------
+
+// Chunk tiles (k, q, v rows: [64][128] bf16) are written by direct
+// global -> LDS loads, 1 KiB (4 rows) per wave instruction, unpadded.  To
+// keep every read pattern free of bank conflicts, the 16-byte chunk c of row
+// i is stored in slot c ^ (i & 15) of the row's 256 bytes.
+GDN_DEV int sw(int row, int col) { return row * D + ((((col >> 3) ^ (row & 15)) << 3) | (col & 7)); }
+
+struct Smem {
+    uint16_t Kb[2][C * D];   // k rows, two buffers (chunk n and n+1)
+    uint16_t Qb[2][C * D];   // q rows (output passes)
+    uint16_t Vb[2][C * D];   // v rows
+    float grb[2][C], btb[2][C];  // log-gates, beta
+    uint16_t Wt[D][PC];   // -W^T  [d][i]
+    uint16_t At[C][PC];   // A^T   [j][i]
+    uint16_t O[C][PD];    // o rows of the chunk, staged for row stores
+    u32x2_t Mf[6][64];    // A fragments of -M_ab (a > b), 16x16x16 layout
+    u32x2_t Lf[4][64];    // A fragments of T_aa - I
+    float G[C], eG[C], eGl[C], bt[C], bg[C];
+};
+
+// The rows of one chunk in LDS.
+struct ChunkView {
+    const uint16_t *K, *Q, *V;
+    const float *gr, *bt;
+};
+GDN_DEV ChunkView chunk_view(const Smem &sm, int buf) {
+    return ChunkView{sm.Kb[buf], sm.Qb[buf], sm.Vb[buf], sm.grb[buf], sm.btb[buf]};
+}
+
+GDN_DEV int mf_index(int a, int b) { return a * (a - 1) / 2 + b; }  // a > b
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Issue the direct loads of chunk n into buffer `buf` (completion: vmcnt).
+// Wave w fills rows 16w .. 16w+15 of each tile, 4 rows per instruction: lane
+// L takes row i0 + L/16, slot L%16, i.e. chunk (L%16) ^ (row & 15) of the
+// row in HBM.  Rows past the sequence end read row T-1 and are zeroed later.
+// Waves 0 and 1 also load the 64 log-gates and betas (4 bytes per lane).
+template <bool WITH_Q>
+GDN_DEV void load_chunk(Smem &sm, int buf, const uint16_t *q, const uint16_t *k,
+                        const uint16_t *v, const float *g, const float *beta, int b, int h,
+                        int kh, int n, int T, int Hv, int Hk, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i0 = 16 * wave + 4 * j;
+        const int i = i0 + (lane >> 4);
+        const int c = (lane & 15) ^ (i & 15);
+        const int tc = min(n * C + i, T - 1);
+        const uint16_t *kp = k + (((size_t)b * T + tc) * Hk + kh) * D + 8 * c;
+        const uint16_t *vp = v + (((size_t)b * T + tc) * Hv + h) * D + 8 * c;
+        __builtin_amdgcn_global_load_lds(kp, (lds_void_t *)&sm.Kb[buf][i0 * D], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vp, (lds_void_t *)&sm.Vb[buf][i0 * D], 16, 0, 0);
+        if constexpr (WITH_Q) {
+            const uint16_t *qp = q + (((size_t)b * T + tc) * Hk + kh) * D + 8 * c;
+            __builtin_amdgcn_global_load_lds(qp, (lds_void_t *)&sm.Qb[buf][i0 * D], 16, 0, 0);
+        }
+    }
+    if (wave < 2) {
+        const int tc = min(n * C + lane, T - 1);
+        const float *src = (wave == 0 ? g : beta) + ((size_t)b * T + tc) * Hv + h;
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(wave == 0 ? sm.grb[buf] : sm.btb[buf]),
+                                         4, 0, 0);
+    }
+}
+
+// Wait for this thread's outstanding global loads and stores (including the
+// direct LDS loads).
+GDN_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Workgroup barrier for LDS traffic only.  __syncthreads() is also a release
+// fence for global memory, which would wait for the next chunk's direct loads
+// at every barrier; here the waves only exchange data through LDS, so the
+// barrier waits for this wave's LDS operations and nothing else.  Global
+// visibility of the direct loads is established by wait_vmem() before the
+// barrier that ends a chunk.
+GDN_DEV void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Rows of chunk n past the sequence end read as zero (HF pads with zeros).
+// Call between barriers, after the chunk's loads have landed.
+template <bool WITH_Q>
+GDN_DEV void zero_tail(Smem &sm, int buf, int n, int T, int tid) {
+    const int valid = T - n * C;  // 1 .. 63
+    for (int e = tid; e < (C - valid) * (D / 8); e += 256) {
+        const int i = valid + e / (D / 8), c = e % (D / 8);
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4 *>(&sm.Kb[buf][i * D + 8 * c]) = z;
+        *reinterpret_cast<uint4 *>(&sm.Vb[buf][i * D + 8 * c]) = z;
+        if constexpr (WITH_Q) *reinterpret_cast<uint4 *>(&sm.Qb[buf][i * D + 8 * c]) = z;
+    }
+    if (tid >= valid && tid < C) {
+        sm.grb[buf][tid] = 0.f;
+        sm.btb[buf][tid] = 0.f;
+    }
+}
+
+// Operand reads of the swizzled chunk tiles (same fragments as above).
+GDN_DEV bf16x8_t sfrag_nat(const uint16_t *base, int row0, int k0, int g, int r) {
+    return as_bf16x8(*reinterpret_cast<const u32x4_t *>(base + sw(row0 + r, k0 + 8 * g)));
+}
+GDN_DEV bf16x8_t sfrag_rows(const uint16_t *base, int row0, int k0, int g, int r) {
+    return as_bf16x8(join(*reinterpret_cast<const u32x2_t *>(base + sw(row0 + r, k0 + 4 * g)),
+                          *reinterpret_cast<const u32x2_t *>(base + sw(row0 + r, k0 + 16 + 4 * g))));
+}
+GDN_DEV bf16x8_t sfrag_tr(const uint16_t *base, int k0, int col0, int g, int r) {
+    const int row = k0 + 4 * g + (r >> 2), col = col0 + 4 * (r & 3);
+    return as_bf16x8(join(lds_tr(base + sw(row, col)), lds_tr(base + sw(row + 16, col))));
+}
+
+// Accumulator tile (rows row0 .. row0+15, columns col .. col+15) of a chunk
+// tile, scaled per row by sc (rows row0 + 4g .. +3): one transposing read.
+GDN_DEV f32x4_t rhs_tile(const uint16_t *base, int row0, int col, const f32x4_t &sc, int g, int r) {
+    const u32x2_t w = lds_tr(base + sw(row0 + 4 * g + (r >> 2), col + 4 * (r & 3)));
+    f32x4_t x;
+    x[0] = __uint_as_float(w[0] << 16) * sc[0];
+    x[1] = __uint_as_float(w[0] & 0xFFFF0000u) * sc[1];
+    x[2] = __uint_as_float(w[1] << 16) * sc[2];
+    x[3] = __uint_as_float(w[1] & 0xFFFF0000u) * sc[3];
+    return x;
+}
+
+GDN_DEV f32x4_t lds_f4(const float *p) { return *reinterpret_cast<const f32x4_t *>(p); }
+
+// Stage A for the chunk in view cv (landed and visible to all threads).
+//  - gates: G = cumsum(g), e^G, e^{G_last - G};
+//  - wave w: row tile w of K K^T and Q K^T.  K K^T is symmetric, so its
+//    upper tiles give the A operands of the lower blocks of M directly and
+//    the diagonal tile gives both Z = -M_ww and Z^T;
+//  - wave w inverts its diagonal block, T_ww = (I + Z)(I + Z^2)(I + Z^4)
+//    (I + Z^8) (Z is nilpotent), on MFMA with hi/lo bf16 operands;
+//  - each wave solves (I + M) X = R by block rows for its right-hand sides:
+//    W columns 32w .. 32w+31 (R = diag(beta e^G) K) and U columns
+//    ucol0 .. ucol0+16 NUT-1 (R = diag(beta) V), kept in registers;
+//  - -W^T and A^T go to LDS.
+template <bool WITH_Q, int NUT, bool DO_U>
+GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int ucol0,
+                     f32x4_t (&U)[4][NUT]) {
+    constexpr bool do_u = DO_U;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15;
+
+    if (wave == 0) {
+        float x = cv.gr[lane];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        const float glast = __shfl(x, 63, 64);
+        const float eg = expf(x);
+        sm.G[lane] = x;
+        sm.eG[lane] = eg;
+        sm.eGl[lane] = expf(glast - x);
+        const float bv = cv.bt[lane];
+        sm.bt[lane] = bv;
+        sm.bg[lane] = bv * eg;
+    }
+    lds_barrier();
+
+    {
+        f32x4_t kk[4], qk[4];
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            kk[ct] = zero4();
+            qk[ct] = zero4();
+        }
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            const bf16x8_t ak = sfrag_nat(cv.K, 16 * wave, 32 * kb, g, r);
+            bf16x8_t aq;
+            if constexpr (WITH_Q) aq = sfrag_nat(cv.Q, 16 * wave, 32 * kb, g, r);
+            // all four column tiles: branch-free code lets the LDS reads run
+            // ahead of the MFMAs (tiles outside the triangle are discarded)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                const bf16x8_t bk = sfrag_nat(cv.K, 16 * ct, 32 * kb, g, r);
+                kk[ct] = mfma_16x16x32_bf16(ak, bk, kk[ct]);
+                if constexpr (WITH_Q) qk[ct] = mfma_16x16x32_bf16(aq, bk, qk[ct]);
+            }
+        }
+        // Gates of this lane's rows (16 wave + 4g + e) and columns (16 ct + r),
+        // read once; Gamma factors exp(G_i - G_j) <= 1 for i >= j.
+        const f32x4_t Gw = lds_f4(&sm.G[16 * wave + 4 * g]);
+        const f32x4_t Bw = lds_f4(&sm.bt[16 * wave + 4 * g]);
+        float Gc[4], Bc[4];
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            Gc[ct] = sm.G[16 * ct + r];
+            Bc[ct] = sm.bt[16 * ct + r];
+        }
+        // A^T [j][i] = scale Gamma_ij (q_i . k_j), j <= i; zero tiles above
+        if constexpr (WITH_Q) {
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                const int j = 16 * ct + r;
+                float av[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 16 * wave + 4 * g + e;
+                    const float ga = __expf(fminf(Gw[e] - Gc[ct], 0.f));
+                    av[e] = (ct <= wave && j <= i) ? q_scale * qk[ct][e] * ga : 0.f;
+                }
+                u32x2_t w2;
+                w2[0] = pack2_bf16_hw(av[0], av[1]);
+                w2[1] = pack2_bf16_hw(av[2], av[3]);
+                *reinterpret_cast<u32x2_t *>(&sm.At[j][16 * wave + 4 * g]) = w2;
+            }
+        }
+        // A fragments of -M_{a,wave}, a > wave: element e of lane (g, r) is
+        // -M[16a + r][16 wave + 4g + e] = -beta Gamma (k.k) from tile (wave, a)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            if (ct > wave) {
+                f32x4_t m;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    m[e] = -Bc[ct] * __expf(fminf(Gc[ct] - Gw[e], 0.f)) * kk[ct][e];
+                sm.Mf[mf_index(ct, wave)][lane] = __builtin_bit_cast(u32x2_t, bf4(m));
+            }
+        }
+        // diagonal block: Z = -M_ww and Z^T as accumulator tiles (tile ct =
+        // wave, selected without indexing registers by a runtime value)
+        f32x4_t Z = zero4(), Zt = zero4(), I4;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            if (ct == wave) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 4 * g + e, j = r;
+                    const float d = Gw[e] - Gc[ct];      // G_i - G_j
+                    const float zij = -Bw[e] * __expf(fminf(d, 0.f)) * kk[ct][e];
+                    const float zji = -Bc[ct] * __expf(fminf(-d, 0.f)) * kk[ct][e];
+                    Z[e] = (i > j) ? zij : 0.f;
+                    Zt[e] = (j > i) ? zji : 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) I4[e] = (4 * g + e == r) ? 1.f : 0.f;
+        const f32x4_t Z2 = mfma16x3(Zt, Z, zero4());
+        const f32x4_t Z2t = mfma16x3(Z, Zt, zero4());
+        const f32x4_t Z4 = mfma16x3(Z2t, Z2, zero4());
+        const f32x4_t Z4t = mfma16x3(Z2, Z2t, zero4());
+        const f32x4_t Z8 = mfma16x3(Z4t, Z4, zero4());
+        // T^T = (I + Z^8)^T (I + Z^4)^T (I + Z^2)^T (I + Z)^T, built up as
+        // P^T <- P^T + (Z^k)^T P^T = P^T + mfma(C(Z^k), C(P^T))
+        f32x4_t Pt = I4 + Zt;
+        Pt = mfma16x3(Z2, Pt, Pt);
+        Pt = mfma16x3(Z4, Pt, Pt);
+        Pt = mfma16x3(Z8, Pt, Pt);
+        sm.Lf[wave][lane] = __builtin_bit_cast(u32x2_t, bf4(Pt - I4));  // A fragment of T - I
+    }
+    lds_barrier();
+
+    // block forward substitution: X_a = T_aa (R_a - sum_{b<a} M_ab X_b)
+    f32x4_t Wx[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        const f32x4_t swt = lds_f4(&sm.bg[16 * a + 4 * g]);   // beta e^G
+#pragma unroll
+        for (int t = 0; t < 2; ++t) Wx[a][t] = rhs_tile(cv.K, 16 * a, 32 * wave + 16 * t, swt, g, r);
+        if constexpr (do_u) {
+            const f32x4_t su = lds_f4(&sm.bt[16 * a + 4 * g]);  // beta
+#pragma unroll
+            for (int t = 0; t < NUT; ++t) U[a][t] = rhs_tile(cv.V, 16 * a, ucol0 + 16 * t, su, g, r);
+        }
+#pragma unroll
+        for (int b = 0; b < a; ++b) {
+            const s4_t am = __builtin_bit_cast(s4_t, sm.Mf[mf_index(a, b)][lane]);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) Wx[a][t] = mfma16(am, bf4(Wx[b][t]), Wx[a][t]);
+            if constexpr (do_u) {
+#pragma unroll
+                for (int t = 0; t < NUT; ++t) U[a][t] = mfma16(am, bf4(U[b][t]), U[a][t]);
+            }
+        }
+        const s4_t al = __builtin_bit_cast(s4_t, sm.Lf[a][lane]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) Wx[a][t] = mfma16(al, bf4(Wx[a][t]), Wx[a][t]);
+        if constexpr (do_u) {
+#pragma unroll
+            for (int t = 0; t < NUT; ++t) U[a][t] = mfma16(al, bf4(U[a][t]), U[a][t]);
+        }
+    }
+    // -W^T [d][i]
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            u32x2_t w2;
+            w2[0] = pack2_bf16_hw(-Wx[a][t][0], -Wx[a][t][1]);
+            w2[1] = pack2_bf16_hw(-Wx[a][t][2], -Wx[a][t][3]);
+            *reinterpret_cast<u32x2_t *>(&sm.Wt[32 * wave + 16 * t + r][16 * a + 4 * g]) = w2;
+        }
+    lds_barrier();
+}
+
+// ---------------------------------------------------------------------------
+// State I/O
+// ---------------------------------------------------------------------------
+
+template <int FMT> GDN_DEV float state_ld(const void *S, size_t i) {
+    if constexpr (FMT == kF16) return f16_to_f32(static_cast<const uint16_t *>(S)[i]);
+    else return static_cast<const float *>(S)[i];
+}
+template <int FMT> GDN_DEV void state_st(void *S, size_t i, float x) {
+    if constexpr (FMT == kF16) static_cast<uint16_t *>(S)[i] = f32_to_f16_rne(x);
+    else static_cast<float *>(S)[i] = x;
+}
+
+// Accumulator tiles of a [128][NCT*16] column block of a row-major [128][128]
+// matrix at column c0: tile (rt, ct), lane (g, r), element e is row
+// 16 rt + 4 g + e, column c0 + 16 ct + r.
+template <int FMT, int NCT>
+GDN_DEV void tiles_load(f32x4_t (&S)[8][NCT], const void *src, int c0, int g, int r) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                S[rt][ct][e] = state_ld<FMT>(src, (size_t)(16 * rt + 4 * g + e) * D + c0 + 16 * ct + r);
+}
+template <int FMT, int NCT>
+GDN_DEV void tiles_store(const f32x4_t (&S)[8][NCT], void *dst, int c0, int g, int r) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                state_st<FMT>(dst, (size_t)(16 * rt + 4 * g + e) * D + c0 + 16 * ct + r, S[rt][ct][e]);
+}
+
+// Per (sequence, head): slot p of the carry buffer holds, for segment p,
+// S_start (p >= 1), Phi and C (1 <= p <= P-2), each [128][128] fp32.
+GDN_DEV float *carry_slot(float *carry, int b, int h, int Hv, int P, int p, int which) {
+    return carry + ((((size_t)b * Hv + h) * P + p) * 3 + which) * (size_t)(D * D);
+}
+constexpr int kSst = 0, kPhi = 1, kCst = 2;
+
+// ---------------------------------------------------------------------------
+// Segment kernels
+// ---------------------------------------------------------------------------
+
+struct SegArgs {
+    const uint16_t *q, *k, *v;
+    const float *g, *beta;
+    uint16_t *o;
+    void *S;          // initial state in, final state out
+    float *carry;
+    int T, Hv, Hk, NC, L, P;
+    float q_scale;
+};
+
+// The recurrence with output over chunks [n0, n1) of one (b, h), from the
+// state `S` in registers (wave w owns columns 32w .. 32w+31).
+GDN_DEV void run_output_segment(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h,
+                                int n0, int n1) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int kh = h / (a.Hv / a.Hk);
+    const int c0 = 32 * wave;
+    load_chunk<true>(sm, 0, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
+    wait_vmem();
+    lds_barrier();
+    for (int n = n0; n < n1; ++n) {
+        const int buf = (n - n0) & 1;
+        if (n * C + C > a.T) {  // last, partial chunk
+            zero_tail<true>(sm, buf, n, a.T, tid);
+            lds_barrier();
+        }
+        if (n + 1 < n1)  // next chunk's rows stream into the other buffer
+            load_chunk<true>(sm, buf ^ 1, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
+                             a.Hk, tid);
+        const ChunkView cv = chunk_view(sm, buf);
+        // v starts as U = T diag(beta) V (this wave's columns), o as 0
+        f32x4_t vacc[4][2], oacc[4][2];
+        stage_a<true, 2, true>(sm, cv, a.q_scale, tid, c0, vacc);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) oacc[rt][ct] = zero4();
+        // v -= W S ;  o = q S
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            bf16x8_t sb[2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) sb[ct] = frag_acc(S[2 * kb][ct], S[2 * kb + 1][ct]);
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const bf16x8_t aw = frag_tr(&sm.Wt[0][0], PC, 32 * kb, 16 * rt, g, r);
+                const bf16x8_t aq = sfrag_rows(cv.Q, 16 * rt, 32 * kb, g, r);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    vacc[rt][ct] = mfma_16x16x32_bf16(aw, sb[ct], vacc[rt][ct]);
+                    oacc[rt][ct] = mfma_16x16x32_bf16(aq, sb[ct], oacc[rt][ct]);
+                }
+            }
+        }
+        // o = e^G scale (q S) + A v
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float f = a.q_scale * sm.eG[16 * rt + 4 * g + e];
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) oacc[rt][ct][e] *= f;
+            }
+#pragma unroll
+        for (int kb = 0; kb < C / 32; ++kb) {
+            bf16x8_t vb[2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) vb[ct] = frag_acc(vacc[2 * kb][ct], vacc[2 * kb + 1][ct]);
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const bf16x8_t aa = frag_tr(&sm.At[0][0], PC, 32 * kb, 16 * rt, g, r);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) oacc[rt][ct] = mfma_16x16x32_bf16(aa, vb[ct], oacc[rt][ct]);
+            }
+        }
+        // o -> LDS (row-major); the whole workgroup stores rows after the barrier
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    sm.O[16 * rt + 4 * g + e][c0 + 16 * ct + r] = f32_to_bf16_hw(oacc[rt][ct][e]);
+        // S = e^{G_last} S + K^T diag(e^{G_last - G}) v
+        {
+            const float gam = expf(sm.G[C - 1]);
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) S[rt][ct][e] *= gam;
+#pragma unroll
+            for (int kb = 0; kb < C / 32; ++kb) {
+                float slo[4], shi[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    slo[e] = sm.eGl[32 * kb + 4 * g + e];
+                    shi[e] = sm.eGl[32 * kb + 16 + 4 * g + e];
+                }
+                bf16x8_t vg[2];
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+                    vg[ct] = frag_acc_scaled(vacc[2 * kb][ct], vacc[2 * kb + 1][ct], slo, shi);
+#pragma unroll
+                for (int rt = 0; rt < 8; ++rt) {
+                    const bf16x8_t ak = sfrag_tr(cv.K, 32 * kb, 16 * rt, g, r);
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) S[rt][ct] = mfma_16x16x32_bf16(ak, vg[ct], S[rt][ct]);
+                }
+            }
+        }
+        wait_vmem();      // the next chunk's rows have landed
+        lds_barrier();  // and this chunk's buffer may be refilled
+        // o rows inside the sequence -> HBM, 16 B per thread
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int it = tid + 256 * j;
+            const int i = it >> 4, d0 = (it & 15) * 8;
+            const int t = n * C + i;
+            if (t < a.T)
+                *reinterpret_cast<uint4 *>(a.o + (((size_t)b * a.T + t) * a.Hv + h) * D + d0) =
+                    *reinterpret_cast<const uint4 *>(&sm.O[i][d0]);
+        }
+    }
+}
+
+// Middle segment of pass 1: the recurrence from S = 0 on state columns
+// 0..127 (waves 0, 1) and from Phi = I with U = 0 on 128 more columns
+// (waves 2, 3), without output.  Wave w owns augmented columns 64w..64w+63.
+GDN_DEV void run_transition_segment(Smem &sm, const SegArgs &a, int b, int h, int p, int n0,
+                                    int n1) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int kh = h / (a.Hv / a.Hk);
+    const bool is_phi = wave >= 2;
+    const int c0 = 64 * (wave & 1);   // column of the S or Phi block
+    f32x4_t X[8][4];
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                X[rt][ct][e] = (is_phi && 16 * rt + 4 * g + e == c0 + 16 * ct + r) ? 1.f : 0.f;
+
+    load_chunk<false>(sm, 0, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
+    wait_vmem();
+    lds_barrier();
+    for (int n = n0; n < n1; ++n) {
+        const int buf = (n - n0) & 1;
+        if (n * C + C > a.T) {
+            zero_tail<false>(sm, buf, n, a.T, tid);
+            lds_barrier();
+        }
+        if (n + 1 < n1)
+            load_chunk<false>(sm, buf ^ 1, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
+                              a.Hk, tid);
+        const ChunkView cv = chunk_view(sm, buf);
+        // v starts as U (state waves) or 0 (transition waves)
+        f32x4_t vacc[4][4];
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) vacc[rt][ct] = zero4();
+        if (is_phi)
+            stage_a<false, 4, false>(sm, cv, a.q_scale, tid, c0, vacc);
+        else
+            stage_a<false, 4, true>(sm, cv, a.q_scale, tid, c0, vacc);
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            bf16x8_t xb[4];
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) xb[ct] = frag_acc(X[2 * kb][ct], X[2 * kb + 1][ct]);
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const bf16x8_t aw = frag_tr(&sm.Wt[0][0], PC, 32 * kb, 16 * rt, g, r);
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) vacc[rt][ct] = mfma_16x16x32_bf16(aw, xb[ct], vacc[rt][ct]);
+            }
+        }
+        {
+            const float gam = expf(sm.G[C - 1]);
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) X[rt][ct][e] *= gam;
+#pragma unroll
+            for (int kb = 0; kb < C / 32; ++kb) {
+                float slo[4], shi[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    slo[e] = sm.eGl[32 * kb + 4 * g + e];
+                    shi[e] = sm.eGl[32 * kb + 16 + 4 * g + e];
+                }
+                bf16x8_t vg[4];
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+                    vg[ct] = frag_acc_scaled(vacc[2 * kb][ct], vacc[2 * kb + 1][ct], slo, shi);
+#pragma unroll
+                for (int rt = 0; rt < 8; ++rt) {
+                    const bf16x8_t ak = sfrag_tr(cv.K, 32 * kb, 16 * rt, g, r);
+#pragma unroll
+                    for (int ct = 0; ct < 4; ++ct) X[rt][ct] = mfma_16x16x32_bf16(ak, vg[ct], X[rt][ct]);
+                }
+            }
+        }
+        wait_vmem();
+        lds_barrier();
+    }
+    tiles_store<kF32, 4>(X, carry_slot(a.carry, b, h, a.Hv, a.P, p, is_phi ? kPhi : kCst), c0, g, r);
+}
+
+// Pass 1: slot p = blockIdx.y < P-1.  Segment 0 runs the output recurrence
+// from the initial state; segments 1 .. P-2 their transition.
+template <int IN_FMT, int OUT_FMT>
+__global__ __launch_bounds__(256) void prefill_pass1_kernel(SegArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
+    const int h = blockIdx.x, p = blockIdx.y, b = blockIdx.z;
+    const int n0 = p * a.L, n1 = min(a.NC, n0 + a.L);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    if (p == 0) {
+        f32x4_t S[8][2];
+        void *Sg = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (IN_FMT == kF16 ? 2 : 4);
+        tiles_load<IN_FMT, 2>(S, Sg, 32 * wave, g, r);
+        run_output_segment(sm, S, a, b, h, n0, n1);
+        if (a.P == 1) {
+            void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
+            tiles_store<OUT_FMT, 2>(S, So, 32 * wave, g, r);
+        } else {
+            tiles_store<kF32, 2>(S, carry_slot(a.carry, b, h, a.Hv, a.P, 1, kSst), 32 * wave, g, r);
+        }
+    } else {
+        run_transition_segment(sm, a, b, h, p, n0, n1);
+    }
+}
+
+// Pass 2: slot blockIdx.y -> segment p = blockIdx.y + 1, from S_start(p).
+template <int OUT_FMT>
+__global__ __launch_bounds__(256) void prefill_pass2_kernel(SegArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
+    const int h = blockIdx.x, p = blockIdx.y + 1, b = blockIdx.z;
+    const int n0 = p * a.L, n1 = min(a.NC, n0 + a.L);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    f32x4_t S[8][2];
+    tiles_load<kF32, 2>(S, carry_slot(a.carry, b, h, a.Hv, a.P, p, kSst), 32 * wave, g, r);
+    run_output_segment(sm, S, a, b, h, n0, n1);
+    if (p == a.P - 1) {
+        void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
+        tiles_store<OUT_FMT, 2>(S, So, 32 * wave, g, r);
+    }
+}
+
+// Combine: one wave per (head, 16-column tile, sequence).  S_start(1) is in
+// the carry; S_start(p+1) = Phi_p S_start(p) + C_p for p = 1 .. P-2, with the
+// product split as hi/lo bf16 pairs (hi*hi + hi*lo + lo*hi) for near-fp32
+// accuracy.
+__global__ __launch_bounds__(64) void prefill_combine_kernel(float *carry, int Hv, int P) {
+    const int h = blockIdx.x, ctile = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x, g = lane >> 4, r = lane & 15;
+    const int c0 = 16 * ctile;
+    f32x4_t S[8][1];
+    tiles_load<kF32, 1>(S, carry_slot(carry, b, h, Hv, P, 1, kSst), c0, g, r);
+    for (int p = 1; p + 1 < P; ++p) {
+        const float *Phi = carry_slot(carry, b, h, Hv, P, p, kPhi);
+        f32x4_t acc[8][1];
+        tiles_load<kF32, 1>(acc, carry_slot(carry, b, h, Hv, P, p, kCst), c0, g, r);
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            // B = S rows of this 32-block, split hi / lo
+            f32x4_t lo_hi[2], lo_lo[2];
+            u32x4_t bh, bl;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const f32x4_t s = S[2 * kb + half][0];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lo_hi[half][e] = bf16_to_f32(f32_to_bf16_rne(s[e]));
+                    lo_lo[half][e] = s[e] - lo_hi[half][e];
+                }
+            }
+            bh[0] = pack2_bf16_hw(lo_hi[0][0], lo_hi[0][1]);
+            bh[1] = pack2_bf16_hw(lo_hi[0][2], lo_hi[0][3]);
+            bh[2] = pack2_bf16_hw(lo_hi[1][0], lo_hi[1][1]);
+            bh[3] = pack2_bf16_hw(lo_hi[1][2], lo_hi[1][3]);
+            bl[0] = pack2_bf16_hw(lo_lo[0][0], lo_lo[0][1]);
+            bl[1] = pack2_bf16_hw(lo_lo[0][2], lo_lo[0][3]);
+            bl[2] = pack2_bf16_hw(lo_lo[1][0], lo_lo[1][1]);
+            bl[3] = pack2_bf16_hw(lo_lo[1][2], lo_lo[1][3]);
+            const bf16x8_t sbh = as_bf16x8(bh), sbl = as_bf16x8(bl);
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt) {
+                // A = Phi row 16 rt + r, k-slots of lane group g (permuted order)
+                const float *prow = Phi + (size_t)(16 * rt + r) * D + 32 * kb + 4 * g;
+                const float4 x0 = *reinterpret_cast<const float4 *>(prow);
+                const float4 x1 = *reinterpret_cast<const float4 *>(prow + 16);
+                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                u32x4_t ah, al;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float h0 = bf16_to_f32(f32_to_bf16_rne(xs[2 * e]));
+                    const float h1 = bf16_to_f32(f32_to_bf16_rne(xs[2 * e + 1]));
+                    ah[e] = pack2_bf16_hw(h0, h1);
+                    al[e] = pack2_bf16_hw(xs[2 * e] - h0, xs[2 * e + 1] - h1);
+                }
+                const bf16x8_t aph = as_bf16x8(ah), apl = as_bf16x8(al);
+                acc[rt][0] = mfma_16x16x32_bf16(aph, sbh, acc[rt][0]);
+                acc[rt][0] = mfma_16x16x32_bf16(aph, sbl, acc[rt][0]);
+                acc[rt][0] = mfma_16x16x32_bf16(apl, sbh, acc[rt][0]);
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt) S[rt][0] = acc[rt][0];
+        tiles_store<kF32, 1>(S, carry_slot(carry, b, h, Hv, P, p + 1, kSst), c0, g, r);
+    }
+}
+
+// Segments: enough middle segments that a pass fills the device (about 256
+// workgroups), at least kMinSegChunks chunks each; P = 2 would only
+// serialise, so it falls back to 1.
+constexpr int kMinSegChunks = 8;
+constexpr int kTargetWgs = 256;
+
+void plan_segments(int B, int Hv, int NC, int &P, int &L) {
+    const int bh = B * Hv;
+    int want = 1 + (kTargetWgs + bh - 1) / bh;
+    const int cap = NC / kMinSegChunks;
+    if (want > cap) want = cap;
+    if (want < 3) want = 1;
+    P = want;
+    L = (NC + P - 1) / P;
+    P = (NC + L - 1) / L;  // drop empty trailing segments
+    if (P < 3) {
+        P = 1;
+        L = NC;
+    }
+}
+
+}  // namespace
+
+size_t prefill_carry_bytes(int B, int T, int Hv) {
+    const int NC = (T + C - 1) / C;
+    int P, L;
+    plan_segments(B, Hv, NC, P, L);
+    return P > 1 ? (size_t)B * Hv * P * 3 * D * D * sizeof(float) : 0;
+}
+
+hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_t *k,
+                              const uint16_t *v, const float *g, const float *beta, uint16_t *o,
+                              void *S, int B, int T, int Hv, int Hk, float q_scale, void *carry,
+                              hipStream_t st) {
+    if (B <= 0 || T <= 0) return hipSuccess;
+    if (Hv <= 0 || Hk <= 0 || Hv % Hk) return hipErrorInvalidValue;
+    const int NC = (T + C - 1) / C;
+    SegArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.g = g;
+    a.beta = beta;
+    a.o = o;
+    a.S = S;
+    a.carry = static_cast<float *>(carry);
+    a.T = T;
+    a.Hv = Hv;
+    a.Hk = Hk;
+    a.NC = NC;
+    a.q_scale = q_scale;
+    plan_segments(B, Hv, NC, a.P, a.L);
+    if (a.P > 1 && !carry) return hipErrorInvalidValue;
+    const size_t smem = sizeof(Smem);
+    auto pass1 = narrow_state == kF16 ? prefill_pass1_kernel<kF16, kF16> : prefill_pass1_kernel<kF32, kF32>;
+    auto pass2 = narrow_state == kF16 ? prefill_pass2_kernel<kF16> : prefill_pass2_kernel<kF32>;
+    static bool attr_set = false;  // idempotent; races only repeat the same call
+    if (!attr_set) {
+        hipError_t e;
+        for (auto f : {prefill_pass1_kernel<kF32, kF32>, prefill_pass1_kernel<kF16, kF16>})
+            if ((e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)smem)) != hipSuccess)
+                return e;
+        for (auto f : {prefill_pass2_kernel<kF32>, prefill_pass2_kernel<kF16>})
+            if ((e = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)smem)) != hipSuccess)
+                return e;
+        attr_set = true;
+    }
+    const int slots = a.P > 1 ? a.P - 1 : 1;
+    pass1<<<dim3(Hv, slots, B), 256, smem, st>>>(a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.P == 1) return e;
+    if (a.P > 2) {
+        prefill_combine_kernel<<<dim3(Hv, D / 16, B), 64, 0, st>>>(a.carry, Hv, a.P);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    pass2<<<dim3(Hv, a.P - 1, B), 256, smem, st>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace gdn

@@ -14,7 +14,7 @@
 //
 // Per-device state (created lazily under a mutex): an internal stream for
 // the synchronous symbols, staging buffers, the look-back scan scratch and
-// the prefill workspace.  Scan launches are serialised per device (host
+// the prefill carry buffer.  Scan launches are serialised per device (host
 // mutex; stream order, or a device synchronisation when the stream changes)
 // because they share the tile counter and status arrays; every other kernel
 // is free of shared state.
@@ -69,10 +69,9 @@ struct DeviceCtx {
     // the last scan launch: its stream, and whether it may still be running
     hipStream_t scan_stream = nullptr;
     bool scan_pending = false;
-    // prefill workspace and the second stream its phases overlap on
+    // prefill carry buffer (segment transitions and start states)
     DevBuf chunk_ws;
-    gdn::PrefillStreams pf{};
-    hipEvent_t pf_done = nullptr;  // end of the last prefill (workspace free)
+    hipStream_t pf_stream = nullptr;  // stream of the last prefill
     bool pf_pending = false;
 };
 
@@ -101,16 +100,6 @@ hipError_t get_ctx(DeviceCtx **out) {
         c->scan.err = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(c->scan.counter) + 64);
         e = hipDeviceGetAttribute(&c->scan.cu_count, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
-        e = hipStreamCreateWithFlags(&c->pf.aux, hipStreamNonBlocking);
-        if (e != hipSuccess) return e;
-        hipEvent_t *evs[6] = {&c->pf.ready, &c->pf.a_done[0], &c->pf.a_done[1], &c->pf.b_done[0],
-                              &c->pf.b_done[1], &c->pf_done};
-        for (hipEvent_t *ev : evs)
-            // Device-scope release: these events only order work on this
-            // device (cheaper than the default system-scope release).
-            if ((e = hipEventCreateWithFlags(ev, hipEventDisableTiming | hipEventReleaseToDevice)) !=
-                hipSuccess)
-                return e;
         c->ready = true;
     }
     *out = c;
@@ -393,20 +382,28 @@ static int run_chunk(int narrow, const uint16_t *q, const uint16_t *k, const uin
     hipError_t e = get_ctx(&c);
     if (e != hipSuccess) return (int)e;
     std::lock_guard<std::mutex> lk(c->mu);
-    const size_t need = gdn::chunk_workspace_bytes(B, T, Hv);
+    const size_t need = gdn::prefill_carry_bytes(B, T, Hv);
     if (need > c->chunk_ws.cap) {
-        // a previous prefill may still be using the old workspace
+        // a previous prefill may still be using the old carry buffer
         e = hipDeviceSynchronize();
         if (e != hipSuccess) return (int)e;
+        c->pf_pending = false;
         e = c->chunk_ws.reserve(need);
         if (e != hipSuccess) return (int)e;
     }
-    // calls share the workspace: a call starts after the previous one ended
-    if (c->pf_pending && (e = hipStreamWaitEvent(st, c->pf_done, 0)) != hipSuccess) return (int)e;
-    e = gdn::launch_chunk_prefill(narrow, q, k, v, g, beta, o, S, B, T, Hv, Hk, q_scale,
-                                  c->chunk_ws.p, c->pf, st);
+    // Calls share the carry buffer, so a call must not start before the
+    // previous one ends: stream order does that on the same stream; on
+    // another stream (the previous one may no longer exist) wait for the
+    // device.
+    if (c->pf_pending && st != c->pf_stream) {
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) return (int)e;
+        c->pf_pending = false;
+    }
+    e = gdn::launch_prefill_seq(narrow, q, k, v, g, beta, o, S, B, T, Hv, Hk, q_scale,
+                                c->chunk_ws.p, st);
     if (e != hipSuccess) return (int)e;
-    if ((e = hipEventRecord(c->pf_done, st)) != hipSuccess) return (int)e;
+    c->pf_stream = st;
     c->pf_pending = true;
     return 0;
 }

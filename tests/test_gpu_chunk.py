@@ -8,8 +8,9 @@ largest reference magnitude of the compared tensor:
     max |got - ref| / max |ref|      <= 2e-2
     ||got - ref||_2 / ||ref||_2      <= 1e-2
 for outputs and final state, scaled by 1.5^log2(T/4096) above T = 4096
-(docs/CORRECTNESS_TOLERANCES.md:34-49).  Exact identities (segmented calls)
-are checked bit for bit.
+(docs/CORRECTNESS_TOLERANCES.md:34-49).  Long sequences are cut into
+segments that run in parallel (their results depend on the cut, within the
+bound); calls split inside one segment are checked bit for bit.
 """
 import math
 
@@ -106,6 +107,17 @@ def test_prefill_multi_segment_vs_oracle(L):
     check(Sg, S_ref, 4396, "state")
 
 
+def test_prefill_segments_vs_oracle(L):
+    """A sequence long enough to be cut into segments that run in parallel
+    (segment transitions, the combine and the output pass), vs the oracle."""
+    for T, Hv, Hk in [(2048 + 37, 4, 2), (64 * 40, 2, 1)]:
+        q, k, v, g, beta, S = prefill_inputs(T + Hv, 1, T, Hv, Hk)
+        o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+        o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, T, Hv, Hk, 128, 128, 64)
+        check(o, o_ref, T, f"output T={T}")
+        check(Sg, S_ref, T, f"state T={T}")
+
+
 def test_prefill_split_calls_bit_identical(L):
     """Calls split at chunk boundaries carry the fp32 state exactly."""
     q, k, v, g, beta, S = prefill_inputs(13, 1, 640, 4, 2)
@@ -146,16 +158,18 @@ def test_prefill_f16_state(L):
 
 
 def test_prefill_long_sequence_properties(L):
-    """T = 16K at the config-3 head shape: finite, one call equals two calls
-    split at a chunk boundary (bit for bit), and the value heads of the last
-    key head agree with the oracle over the whole sequence."""
+    """T = 16K at the config-3 head shape: finite, one call agrees with two
+    calls split at a chunk boundary (each call cuts its own sequence into
+    segments, so the agreement is to the stated bound, not bit for bit), and
+    the value heads of the last key head agree with the oracle over the whole
+    sequence."""
     B, T, Hv, Hk = 1, 16384, 32, 16
     q, k, v, g, beta, S = prefill_inputs(3, B, T, Hv, Hk)
     o1, S1 = gpu_prefill(L, q, k, v, g, beta, S)
     assert np.isfinite(o1).all() and np.isfinite(S1).all()
     o2, S2 = gpu_prefill(L, q, k, v, g, beta, S, calls=[8192, 8192])
-    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
-    assert np.array_equal(S1.view(np.uint32), S2.view(np.uint32))
+    check(o2, o1, T, "two calls vs one, output")
+    check(S2, S1, T, "two calls vs one, state")
     hv = slice(Hv - 2, Hv)  # value heads 30, 31 read key head 15
     sub = [np.ascontiguousarray(x) for x in (q[:, :, Hk - 1:], k[:, :, Hk - 1:], v[:, :, hv],
                                              g[:, :, hv], beta[:, :, hv], S[:, hv])]
