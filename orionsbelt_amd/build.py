@@ -37,6 +37,10 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-result", f"-I{INCLUDE}",
 ]
 LIB_NAME = "libkai_gdn_hip.so"
+# Per-file code generation options.  The prefill keeps its MFMA accumulators
+# in ordinary VGPRs: its state tiles are rescaled and converted by VALU every
+# chunk, and accumulators in AGPRs would cost a move each way.
+EXTRA_FLAGS = {"gdn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd):
@@ -56,7 +60,8 @@ def build_library(verbose: bool = False) -> str:
     for src in SOURCES:
         obj = os.path.join(OBJDIR, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src),
+                     "-o", obj])
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         for out in ex.map(_run, cmds):
             if verbose and out.strip():

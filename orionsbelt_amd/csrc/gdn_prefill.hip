@@ -20,8 +20,9 @@
 //           every middle segment p runs it from S = 0 and, alongside, on
 //           128 more state columns started at I with U = 0, which yields its
 //           local result C_p and its transition Phi_p;
-//   combine: S_start(p+1) = Phi_p S_start(p) + C_p, p = 1 .. P-2;
-//   pass 2: segments 1 .. P-1 rerun the recurrence from S_start(p), with o.
+//   pass 2: segment p = 1 .. P-1 first composes its start state,
+//           S_start(q+1) = Phi_q S_start(q) + C_q from S_start(1) = the end of
+//           segment 0, then reruns the recurrence from it, with o.
 // The work is twice that of one sequential pass, spread over (P-1) x heads
 // workgroups instead of heads.
 //
@@ -143,15 +144,31 @@ GDN_DEV f32x4_t unbf4(s4_t v) {
     for (int e = 0; e < 4; ++e) x[e] = bf16_to_f32((uint16_t)v[e]);
     return x;
 }
-// c + A B with fp32 fragments split into bf16 hi + lo parts (the lo*lo term
-// dropped): about 16 bits of precision.
-GDN_DEV f32x4_t mfma16x3(const f32x4_t &a, const f32x4_t &b, f32x4_t c) {
-    const s4_t ah = bf4(a), bh = bf4(b);
-    const f32x4_t ar = a - unbf4(ah), br = b - unbf4(bh);
-    c = mfma16(ah, bh, c);
-    c = mfma16(ah, bf4(br), c);
-    c = mfma16(bf4(ar), bh, c);
+// c + X Y in fp32 for 16x16 tiles given as accumulators xt = C(X^T) and
+// y = C(Y): four mfma_f32_16x16x4_f32 steps, step s taking k = 4g + s in lane
+// group g, which is element s of both accumulator tiles.
+GDN_DEV f32x4_t mfma_f32x16(const f32x4_t &xt, const f32x4_t &y, f32x4_t c) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(xt[s], y[s], c, 0, 0, 0);
     return c;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wavefront with DPP: shifts
+// within rows of 16 lanes, then the last lane of row 0 (row_bcast:15) and of
+// row 1 (row_bcast:31) carried into the rows after them.  Lanes whose source
+// is outside the row, or whose row is masked off, add 0.
+template <int CTRL, int ROW_MASK> GDN_DEV float dpp_src(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                                   ROW_MASK, 0xF, false));
+}
+GDN_DEV float wave_incl_scan(float x) {
+    x += dpp_src<0x111, 0xF>(x);  // row_shr:1
+    x += dpp_src<0x112, 0xF>(x);  // row_shr:2
+    x += dpp_src<0x114, 0xF>(x);  // row_shr:4
+    x += dpp_src<0x118, 0xF>(x);  // row_shr:8
+    x += dpp_src<0x142, 0xA>(x);  // row_bcast:15 into rows 1, 3
+    x += dpp_src<0x143, 0xC>(x);  // row_bcast:31 into rows 2, 3
+    return x;
 }
 
 // ---------------------------------------------------------------------------
@@ -171,7 +188,7 @@ struct Smem {
     float grb[2][C], btb[2][C];  // log-gates, beta
     uint16_t Wt[D][PC];   // -W^T  [d][i]
     uint16_t At[C][PC];   // A^T   [j][i]
-    uint16_t O[C][PD];    // o rows of the chunk, staged for row stores
+    uint16_t Ot[D][PC];   // o^T of the chunk, staged for row stores
     u32x2_t Mf[6][64];    // A fragments of -M_ab (a > b), 16x16x16 layout
     u32x2_t Lf[4][64];    // A fragments of T_aa - I
     float G[C], eG[C], eGl[C], bt[C], bg[C];
@@ -190,30 +207,55 @@ GDN_DEV int mf_index(int a, int b) { return a * (a - 1) / 2 + b; }  // a > b
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Issue the direct loads of chunk n into buffer `buf` (completion: vmcnt).
-// Wave w fills rows 16w .. 16w+15 of each tile, 4 rows per instruction: lane
-// L takes row i0 + L/16, slot L%16, i.e. chunk (L%16) ^ (row & 15) of the
-// row in HBM.  Rows past the sequence end read row T-1 and are zeroed later.
-// Waves 0 and 1 also load the 64 log-gates and betas (4 bytes per lane).
-template <bool WITH_Q>
-GDN_DEV void load_chunk(Smem &sm, int buf, const uint16_t *q, const uint16_t *k,
-                        const uint16_t *v, const float *g, const float *beta, int b, int h,
-                        int kh, int n, int T, int Hv, int Hk, int tid) {
+// Per-lane element offsets of the direct loads within one chunk (fixed for a
+// segment).  Wave w fills rows 16w .. 16w+15 of each tile, 4 rows per
+// instruction: lane L of instruction j takes row i = 16w + 4j + L/16 and LDS
+// slot L%16, i.e. chunk c = (L%16) ^ (i & 15) of the row in HBM.
+struct LoadPlan {
+    int kq[4], v[4];  // row offset * row stride + 8c, for k/q and for v
+    int row[4];       // i
+};
+GDN_DEV LoadPlan load_plan(int Hv, int Hk, int tid) {
     const int lane = tid & 63, wave = tid >> 6;
+    LoadPlan lp;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 16 * wave + 4 * j + (lane >> 4);
+        const int c = (lane & 15) ^ (i & 15);
+        lp.row[j] = i;
+        lp.kq[j] = i * Hk * D + 8 * c;
+        lp.v[j] = i * Hv * D + 8 * c;
+    }
+    return lp;
+}
+
+// Issue the direct loads of chunk n into buffer `buf` (completion: vmcnt).
+// Rows past the sequence end read row T-1 and are zeroed later.  Waves 0 and
+// 1 also load the 64 log-gates and betas (4 bytes per lane).
+template <bool WITH_Q>
+GDN_DEV void load_chunk(Smem &sm, int buf, const LoadPlan &lp, const uint16_t *q,
+                        const uint16_t *k, const uint16_t *v, const float *g, const float *beta,
+                        int b, int h, int kh, int n, int T, int Hv, int Hk, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const size_t t0 = (size_t)b * T + (size_t)n * C;   // first row of the chunk
+    const uint16_t *kb = k + (t0 * Hk + kh) * D;
+    const uint16_t *qb = q + (t0 * Hk + kh) * D;
+    const uint16_t *vb = v + (t0 * Hv + h) * D;
+    const bool tail = n * C + C > T;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i0 = 16 * wave + 4 * j;
-        const int i = i0 + (lane >> 4);
-        const int c = (lane & 15) ^ (i & 15);
-        const int tc = min(n * C + i, T - 1);
-        const uint16_t *kp = k + (((size_t)b * T + tc) * Hk + kh) * D + 8 * c;
-        const uint16_t *vp = v + (((size_t)b * T + tc) * Hv + h) * D + 8 * c;
-        __builtin_amdgcn_global_load_lds(kp, (lds_void_t *)&sm.Kb[buf][i0 * D], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vp, (lds_void_t *)&sm.Vb[buf][i0 * D], 16, 0, 0);
-        if constexpr (WITH_Q) {
-            const uint16_t *qp = q + (((size_t)b * T + tc) * Hk + kh) * D + 8 * c;
-            __builtin_amdgcn_global_load_lds(qp, (lds_void_t *)&sm.Qb[buf][i0 * D], 16, 0, 0);
+        int okq = lp.kq[j], ov = lp.v[j];
+        if (tail) {
+            const int last = T - 1 - n * C;  // last row inside the sequence
+            const int dr = min(lp.row[j], last) - lp.row[j];
+            okq += dr * Hk * D;
+            ov += dr * Hv * D;
         }
+        __builtin_amdgcn_global_load_lds(kb + okq, (lds_void_t *)&sm.Kb[buf][i0 * D], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vb + ov, (lds_void_t *)&sm.Vb[buf][i0 * D], 16, 0, 0);
+        if constexpr (WITH_Q)
+            __builtin_amdgcn_global_load_lds(qb + okq, (lds_void_t *)&sm.Qb[buf][i0 * D], 16, 0, 0);
     }
     if (wave < 2) {
         const int tc = min(n * C + lane, T - 1);
@@ -286,7 +328,7 @@ GDN_DEV f32x4_t lds_f4(const float *p) { return *reinterpret_cast<const f32x4_t 
 //    upper tiles give the A operands of the lower blocks of M directly and
 //    the diagonal tile gives both Z = -M_ww and Z^T;
 //  - wave w inverts its diagonal block, T_ww = (I + Z)(I + Z^2)(I + Z^4)
-//    (I + Z^8) (Z is nilpotent), on MFMA with hi/lo bf16 operands;
+//    (I + Z^8) (Z is nilpotent), on fp32 MFMA;
 //  - each wave solves (I + M) X = R by block rows for its right-hand sides:
 //    W columns 32w .. 32w+31 (R = diag(beta e^G) K) and U columns
 //    ucol0 .. ucol0+16 NUT-1 (R = diag(beta) V), kept in registers;
@@ -299,13 +341,8 @@ GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int 
     const int g = lane >> 4, r = lane & 15;
 
     if (wave == 0) {
-        float x = cv.gr[lane];
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(x, off, 64);
-            if (lane >= off) x += y;
-        }
-        const float glast = __shfl(x, 63, 64);
+        const float x = wave_incl_scan(cv.gr[lane]);
+        const float glast = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
         const float eg = expf(x);
         sm.G[lane] = x;
         sm.eG[lane] = eg;
@@ -338,7 +375,10 @@ GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int 
             }
         }
         // Gates of this lane's rows (16 wave + 4g + e) and columns (16 ct + r),
-        // read once; Gamma factors exp(G_i - G_j) <= 1 for i >= j.
+        // read once.  Every element below uses exactly one Gamma factor:
+        // exp(G_i - G_j) where row i >= column j (A, Z) and exp(G_j - G_i)
+        // where j > i (the transposed entries of M); masked elements take the
+        // other direction and are discarded by the select.
         const f32x4_t Gw = lds_f4(&sm.G[16 * wave + 4 * g]);
         const f32x4_t Bw = lds_f4(&sm.bt[16 * wave + 4 * g]);
         float Gc[4], Bc[4];
@@ -347,6 +387,14 @@ GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int 
             Gc[ct] = sm.G[16 * ct + r];
             Bc[ct] = sm.bt[16 * ct + r];
         }
+        f32x4_t ga[4];  // ga[ct][e] = Gamma for row 16 wave + 4g + e, column 16 ct + r
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool lower = 16 * ct + r <= 16 * wave + 4 * g + e;
+                ga[ct][e] = __expf(lower ? Gw[e] - Gc[ct] : Gc[ct] - Gw[e]);
+            }
         // A^T [j][i] = scale Gamma_ij (q_i . k_j), j <= i; zero tiles above
         if constexpr (WITH_Q) {
 #pragma unroll
@@ -356,8 +404,7 @@ GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int i = 16 * wave + 4 * g + e;
-                    const float ga = __expf(fminf(Gw[e] - Gc[ct], 0.f));
-                    av[e] = (ct <= wave && j <= i) ? q_scale * qk[ct][e] * ga : 0.f;
+                    av[e] = (j <= i) ? q_scale * qk[ct][e] * ga[ct][e] : 0.f;
                 }
                 u32x2_t w2;
                 w2[0] = pack2_bf16_hw(av[0], av[1]);
@@ -372,8 +419,7 @@ GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int 
             if (ct > wave) {
                 f32x4_t m;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    m[e] = -Bc[ct] * __expf(fminf(Gc[ct] - Gw[e], 0.f)) * kk[ct][e];
+                for (int e = 0; e < 4; ++e) m[e] = -Bc[ct] * ga[ct][e] * kk[ct][e];
                 sm.Mf[mf_index(ct, wave)][lane] = __builtin_bit_cast(u32x2_t, bf4(m));
             }
         }
@@ -386,27 +432,24 @@ GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int i = 4 * g + e, j = r;
-                    const float d = Gw[e] - Gc[ct];      // G_i - G_j
-                    const float zij = -Bw[e] * __expf(fminf(d, 0.f)) * kk[ct][e];
-                    const float zji = -Bc[ct] * __expf(fminf(-d, 0.f)) * kk[ct][e];
-                    Z[e] = (i > j) ? zij : 0.f;
-                    Zt[e] = (j > i) ? zji : 0.f;
+                    Z[e] = (i > j) ? -Bw[e] * ga[ct][e] * kk[ct][e] : 0.f;
+                    Zt[e] = (j > i) ? -Bc[ct] * ga[ct][e] * kk[ct][e] : 0.f;
                 }
             }
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) I4[e] = (4 * g + e == r) ? 1.f : 0.f;
-        const f32x4_t Z2 = mfma16x3(Zt, Z, zero4());
-        const f32x4_t Z2t = mfma16x3(Z, Zt, zero4());
-        const f32x4_t Z4 = mfma16x3(Z2t, Z2, zero4());
-        const f32x4_t Z4t = mfma16x3(Z2, Z2t, zero4());
-        const f32x4_t Z8 = mfma16x3(Z4t, Z4, zero4());
+        const f32x4_t Z2 = mfma_f32x16(Zt, Z, zero4());
+        const f32x4_t Z2t = mfma_f32x16(Z, Zt, zero4());
+        const f32x4_t Z4 = mfma_f32x16(Z2t, Z2, zero4());
+        const f32x4_t Z4t = mfma_f32x16(Z2, Z2t, zero4());
+        const f32x4_t Z8 = mfma_f32x16(Z4t, Z4, zero4());
         // T^T = (I + Z^8)^T (I + Z^4)^T (I + Z^2)^T (I + Z)^T, built up as
         // P^T <- P^T + (Z^k)^T P^T = P^T + mfma(C(Z^k), C(P^T))
         f32x4_t Pt = I4 + Zt;
-        Pt = mfma16x3(Z2, Pt, Pt);
-        Pt = mfma16x3(Z4, Pt, Pt);
-        Pt = mfma16x3(Z8, Pt, Pt);
+        Pt = mfma_f32x16(Z2, Pt, Pt);
+        Pt = mfma_f32x16(Z4, Pt, Pt);
+        Pt = mfma_f32x16(Z8, Pt, Pt);
         sm.Lf[wave][lane] = __builtin_bit_cast(u32x2_t, bf4(Pt - I4));  // A fragment of T - I
     }
     lds_barrier();
@@ -496,6 +539,9 @@ GDN_DEV void tiles_store(const f32x4_t (&S)[8][NCT], void *dst, int c0, int g, i
 GDN_DEV float *carry_slot(float *carry, int b, int h, int Hv, int P, int p, int which) {
     return carry + ((((size_t)b * Hv + h) * P + p) * 3 + which) * (size_t)(D * D);
 }
+GDN_DEV const float *carry_slot(const float *carry, int b, int h, int Hv, int P, int p, int which) {
+    return carry + ((((size_t)b * Hv + h) * P + p) * 3 + which) * (size_t)(D * D);
+}
 constexpr int kSst = 0, kPhi = 1, kCst = 2;
 
 // ---------------------------------------------------------------------------
@@ -520,7 +566,8 @@ GDN_DEV void run_output_segment(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, 
     const int g = lane >> 4, r = lane & 15;
     const int kh = h / (a.Hv / a.Hk);
     const int c0 = 32 * wave;
-    load_chunk<true>(sm, 0, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
+    const LoadPlan lp = load_plan(a.Hv, a.Hk, tid);
+    load_chunk<true>(sm, 0, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
     wait_vmem();
     lds_barrier();
     for (int n = n0; n < n1; ++n) {
@@ -530,7 +577,7 @@ GDN_DEV void run_output_segment(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, 
             lds_barrier();
         }
         if (n + 1 < n1)  // next chunk's rows stream into the other buffer
-            load_chunk<true>(sm, buf ^ 1, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
+            load_chunk<true>(sm, buf ^ 1, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
                              a.Hk, tid);
         const ChunkView cv = chunk_view(sm, buf);
         // v starts as U = T diag(beta) V (this wave's columns), o as 0
@@ -578,14 +625,29 @@ GDN_DEV void run_output_segment(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, 
                 for (int ct = 0; ct < 2; ++ct) oacc[rt][ct] = mfma_16x16x32_bf16(aa, vb[ct], oacc[rt][ct]);
             }
         }
-        // o -> LDS (row-major); the whole workgroup stores rows after the barrier
+        // o -> HBM through LDS: each wave writes its columns of o^T (4 rows of
+        // one column per 8-byte write), reads them back transposed (row t,
+        // 8 consecutive columns per lane) and stores 16 B per lane.  Only this
+        // wave touches its columns, so no barrier is needed.
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
+            for (int ct = 0; ct < 2; ++ct) {
+                u32x2_t w2;
+                w2[0] = pack2_bf16_hw(oacc[rt][ct][0], oacc[rt][ct][1]);
+                w2[1] = pack2_bf16_hw(oacc[rt][ct][2], oacc[rt][ct][3]);
+                *reinterpret_cast<u32x2_t *>(&sm.Ot[c0 + 16 * ct + r][16 * rt + 4 * g]) = w2;
+            }
+        {
+            const int t = n * C + 16 * g + r;   // lane (g, r) stores row 16g + r
+            uint16_t *orow = a.o + (((size_t)b * a.T + t) * a.Hv + h) * D + c0;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    sm.O[16 * rt + 4 * g + e][c0 + 16 * ct + r] = f32_to_bf16_hw(oacc[rt][ct][e]);
+            for (int qd = 0; qd < 4; ++qd) {
+                const uint16_t *src = &sm.Ot[c0 + 8 * qd + (r >> 2)][16 * g + 4 * (r & 3)];
+                const u32x4_t w = join(lds_tr(src), lds_tr(src + 4 * PC));
+                if (t < a.T) *reinterpret_cast<u32x4_t *>(orow + 8 * qd) = w;
+            }
+        }
         // S = e^{G_last} S + K^T diag(e^{G_last - G}) v
         {
             const float gam = expf(sm.G[C - 1]);
@@ -617,16 +679,7 @@ GDN_DEV void run_output_segment(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, 
         }
         wait_vmem();      // the next chunk's rows have landed
         lds_barrier();  // and this chunk's buffer may be refilled
-        // o rows inside the sequence -> HBM, 16 B per thread
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int it = tid + 256 * j;
-            const int i = it >> 4, d0 = (it & 15) * 8;
-            const int t = n * C + i;
-            if (t < a.T)
-                *reinterpret_cast<uint4 *>(a.o + (((size_t)b * a.T + t) * a.Hv + h) * D + d0) =
-                    *reinterpret_cast<const uint4 *>(&sm.O[i][d0]);
-        }
+        (void)0;
     }
 }
 
@@ -638,6 +691,7 @@ GDN_DEV void run_transition_segment(Smem &sm, const SegArgs &a, int b, int h, in
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r = lane & 15;
     const int kh = h / (a.Hv / a.Hk);
+    const LoadPlan lp = load_plan(a.Hv, a.Hk, tid);
     const bool is_phi = wave >= 2;
     const int c0 = 64 * (wave & 1);   // column of the S or Phi block
     f32x4_t X[8][4];
@@ -649,7 +703,7 @@ GDN_DEV void run_transition_segment(Smem &sm, const SegArgs &a, int b, int h, in
             for (int e = 0; e < 4; ++e)
                 X[rt][ct][e] = (is_phi && 16 * rt + 4 * g + e == c0 + 16 * ct + r) ? 1.f : 0.f;
 
-    load_chunk<false>(sm, 0, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
+    load_chunk<false>(sm, 0, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
     wait_vmem();
     lds_barrier();
     for (int n = n0; n < n1; ++n) {
@@ -659,7 +713,7 @@ GDN_DEV void run_transition_segment(Smem &sm, const SegArgs &a, int b, int h, in
             lds_barrier();
         }
         if (n + 1 < n1)
-            load_chunk<false>(sm, buf ^ 1, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
+            load_chunk<false>(sm, buf ^ 1, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
                               a.Hk, tid);
         const ChunkView cv = chunk_view(sm, buf);
         // v starts as U (state waves) or 0 (transition waves)
@@ -718,6 +772,103 @@ GDN_DEV void run_transition_segment(Smem &sm, const SegArgs &a, int b, int h, in
     tiles_store<kF32, 4>(X, carry_slot(a.carry, b, h, a.Hv, a.P, p, is_phi ? kPhi : kCst), c0, g, r);
 }
 
+// Start state of segment p >= 1 of pass 2, composed by the workgroup itself:
+// S_start(1) = the end state of segment 0 (in the carry); for q = 1 .. p-1,
+// S_start(q+1) = Phi_q S_start(q) + C_q.  Phi_{q+1} streams from the carry
+// into an fp32 LDS buffer by direct loads (and C_{q+1} into registers) while
+// step q computes; at the start of a step the threads split the staged Phi
+// into bf16 hi and lo halves, so every wave reads MFMA-ready A fragments; the
+// product is hi*hi + hi*lo + lo*hi (near-fp32 accuracy).  Wave w keeps
+// columns 32w .. 32w+31, as the output pass does.
+constexpr int PH = D + 8;  // bf16 row pitch of the Phi halves
+
+struct CombSmem {
+    float raw[D * D];       // Phi as loaded, row-major fp32
+    uint16_t hi[D][PH];
+    uint16_t lo[D][PH];
+};
+
+// Direct loads of one 64 KiB Phi: wave w moves kilobytes 16w .. 16w+15.
+GDN_DEV void comb_fetch(CombSmem &sm, const float *phi, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int blk = 16 * wave + j;  // 1 KiB = 256 floats
+        __builtin_amdgcn_global_load_lds(phi + blk * 256 + 4 * lane, (lds_void_t *)&sm.raw[blk * 256],
+                                         16, 0, 0);
+    }
+}
+
+GDN_DEV void combine_prefix(CombSmem &sm, f32x4_t (&S)[8][2], const float *carry, int b, int h,
+                            int Hv, int P, int p, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int c0 = 32 * wave;
+    tiles_load<kF32, 2>(S, carry_slot(carry, b, h, Hv, P, 1, kSst), c0, g, r);
+    if (p < 2) return;
+    f32x4_t cn[8][2];
+    tiles_load<kF32, 2>(cn, carry_slot(carry, b, h, Hv, P, 1, kCst), c0, g, r);
+    comb_fetch(sm, carry_slot(carry, b, h, Hv, P, 1, kPhi), tid);
+    wait_vmem();
+    lds_barrier();
+    for (int q = 1; q < p; ++q) {
+#pragma unroll 4
+        for (int j = 0; j < 16; ++j) {
+            const int it = tid + 256 * j;
+            const int row = it >> 5, col = (it & 31) * 4;
+            const f32x4_t x = *reinterpret_cast<const f32x4_t *>(&sm.raw[row * D + col]);
+            f32x4_t hx;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hx[e] = bf16_to_f32(f32_to_bf16_rne(x[e]));
+            *reinterpret_cast<s4_t *>(&sm.hi[row][col]) = bf4(hx);
+            *reinterpret_cast<s4_t *>(&sm.lo[row][col]) = bf4(x - hx);
+        }
+        lds_barrier();  // halves ready, raw buffer free
+        f32x4_t acc[8][2];
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = cn[rt][ct];
+        if (q + 1 < p) {  // next step's operands stream in during this one
+            comb_fetch(sm, carry_slot(carry, b, h, Hv, P, q + 1, kPhi), tid);
+            tiles_load<kF32, 2>(cn, carry_slot(carry, b, h, Hv, P, q + 1, kCst), c0, g, r);
+        }
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            bf16x8_t sbh[2], sbl[2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const f32x4_t s0 = S[2 * kb][ct], s1 = S[2 * kb + 1][ct];
+                f32x4_t h0, h1;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    h0[e] = bf16_to_f32(f32_to_bf16_rne(s0[e]));
+                    h1[e] = bf16_to_f32(f32_to_bf16_rne(s1[e]));
+                }
+                sbh[ct] = frag_acc(h0, h1);
+                sbl[ct] = frag_acc(s0 - h0, s1 - h1);
+            }
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt) {
+                const bf16x8_t ah = frag_rows(&sm.hi[0][0], PH, 16 * rt, 32 * kb, g, r);
+                const bf16x8_t al = frag_rows(&sm.lo[0][0], PH, 16 * rt, 32 * kb, g, r);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    acc[rt][ct] = mfma_16x16x32_bf16(ah, sbh[ct], acc[rt][ct]);
+                    acc[rt][ct] = mfma_16x16x32_bf16(ah, sbl[ct], acc[rt][ct]);
+                    acc[rt][ct] = mfma_16x16x32_bf16(al, sbh[ct], acc[rt][ct]);
+                }
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) S[rt][ct] = acc[rt][ct];
+        wait_vmem();    // the next Phi has landed
+        lds_barrier();  // and every wave is done with the halves
+    }
+}
+
 // Pass 1: slot p = blockIdx.y < P-1.  Segment 0 runs the output recurrence
 // from the initial state; segments 1 .. P-2 their transition.
 template <int IN_FMT, int OUT_FMT>
@@ -744,7 +895,8 @@ __global__ __launch_bounds__(256) void prefill_pass1_kernel(SegArgs a) {
     }
 }
 
-// Pass 2: slot blockIdx.y -> segment p = blockIdx.y + 1, from S_start(p).
+// Pass 2: slot blockIdx.y -> segment p = blockIdx.y + 1, from S_start(p),
+// which the workgroup first composes from the pass-1 results.
 template <int OUT_FMT>
 __global__ __launch_bounds__(256) void prefill_pass2_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -754,75 +906,12 @@ __global__ __launch_bounds__(256) void prefill_pass2_kernel(SegArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, r = lane & 15;
     f32x4_t S[8][2];
-    tiles_load<kF32, 2>(S, carry_slot(a.carry, b, h, a.Hv, a.P, p, kSst), 32 * wave, g, r);
+    combine_prefix(*reinterpret_cast<CombSmem *>(smem_raw), S, a.carry, b, h, a.Hv, a.P, p,
+                   threadIdx.x);
     run_output_segment(sm, S, a, b, h, n0, n1);
     if (p == a.P - 1) {
         void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
         tiles_store<OUT_FMT, 2>(S, So, 32 * wave, g, r);
-    }
-}
-
-// Combine: one wave per (head, 16-column tile, sequence).  S_start(1) is in
-// the carry; S_start(p+1) = Phi_p S_start(p) + C_p for p = 1 .. P-2, with the
-// product split as hi/lo bf16 pairs (hi*hi + hi*lo + lo*hi) for near-fp32
-// accuracy.
-__global__ __launch_bounds__(64) void prefill_combine_kernel(float *carry, int Hv, int P) {
-    const int h = blockIdx.x, ctile = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x, g = lane >> 4, r = lane & 15;
-    const int c0 = 16 * ctile;
-    f32x4_t S[8][1];
-    tiles_load<kF32, 1>(S, carry_slot(carry, b, h, Hv, P, 1, kSst), c0, g, r);
-    for (int p = 1; p + 1 < P; ++p) {
-        const float *Phi = carry_slot(carry, b, h, Hv, P, p, kPhi);
-        f32x4_t acc[8][1];
-        tiles_load<kF32, 1>(acc, carry_slot(carry, b, h, Hv, P, p, kCst), c0, g, r);
-#pragma unroll
-        for (int kb = 0; kb < D / 32; ++kb) {
-            // B = S rows of this 32-block, split hi / lo
-            f32x4_t lo_hi[2], lo_lo[2];
-            u32x4_t bh, bl;
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const f32x4_t s = S[2 * kb + half][0];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    lo_hi[half][e] = bf16_to_f32(f32_to_bf16_rne(s[e]));
-                    lo_lo[half][e] = s[e] - lo_hi[half][e];
-                }
-            }
-            bh[0] = pack2_bf16_hw(lo_hi[0][0], lo_hi[0][1]);
-            bh[1] = pack2_bf16_hw(lo_hi[0][2], lo_hi[0][3]);
-            bh[2] = pack2_bf16_hw(lo_hi[1][0], lo_hi[1][1]);
-            bh[3] = pack2_bf16_hw(lo_hi[1][2], lo_hi[1][3]);
-            bl[0] = pack2_bf16_hw(lo_lo[0][0], lo_lo[0][1]);
-            bl[1] = pack2_bf16_hw(lo_lo[0][2], lo_lo[0][3]);
-            bl[2] = pack2_bf16_hw(lo_lo[1][0], lo_lo[1][1]);
-            bl[3] = pack2_bf16_hw(lo_lo[1][2], lo_lo[1][3]);
-            const bf16x8_t sbh = as_bf16x8(bh), sbl = as_bf16x8(bl);
-#pragma unroll
-            for (int rt = 0; rt < 8; ++rt) {
-                // A = Phi row 16 rt + r, k-slots of lane group g (permuted order)
-                const float *prow = Phi + (size_t)(16 * rt + r) * D + 32 * kb + 4 * g;
-                const float4 x0 = *reinterpret_cast<const float4 *>(prow);
-                const float4 x1 = *reinterpret_cast<const float4 *>(prow + 16);
-                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                u32x4_t ah, al;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float h0 = bf16_to_f32(f32_to_bf16_rne(xs[2 * e]));
-                    const float h1 = bf16_to_f32(f32_to_bf16_rne(xs[2 * e + 1]));
-                    ah[e] = pack2_bf16_hw(h0, h1);
-                    al[e] = pack2_bf16_hw(xs[2 * e] - h0, xs[2 * e + 1] - h1);
-                }
-                const bf16x8_t aph = as_bf16x8(ah), apl = as_bf16x8(al);
-                acc[rt][0] = mfma_16x16x32_bf16(aph, sbh, acc[rt][0]);
-                acc[rt][0] = mfma_16x16x32_bf16(aph, sbl, acc[rt][0]);
-                acc[rt][0] = mfma_16x16x32_bf16(apl, sbh, acc[rt][0]);
-            }
-        }
-#pragma unroll
-        for (int rt = 0; rt < 8; ++rt) S[rt][0] = acc[rt][0];
-        tiles_store<kF32, 1>(S, carry_slot(carry, b, h, Hv, P, p + 1, kSst), c0, g, r);
     }
 }
 
@@ -879,6 +968,7 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
     a.q_scale = q_scale;
     plan_segments(B, Hv, NC, a.P, a.L);
     if (a.P > 1 && !carry) return hipErrorInvalidValue;
+    static_assert(sizeof(CombSmem) <= sizeof(Smem), "the start-state staging reuses the chunk LDS");
     const size_t smem = sizeof(Smem);
     auto pass1 = narrow_state == kF16 ? prefill_pass1_kernel<kF16, kF16> : prefill_pass1_kernel<kF32, kF32>;
     auto pass2 = narrow_state == kF16 ? prefill_pass2_kernel<kF16> : prefill_pass2_kernel<kF32>;
@@ -899,10 +989,6 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
     pass1<<<dim3(Hv, slots, B), 256, smem, st>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.P == 1) return e;
-    if (a.P > 2) {
-        prefill_combine_kernel<<<dim3(Hv, D / 16, B), 64, 0, st>>>(a.carry, Hv, a.P);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
     pass2<<<dim3(Hv, a.P - 1, B), 256, smem, st>>>(a);
     return hipGetLastError();
 }

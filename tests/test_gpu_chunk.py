@@ -118,6 +118,17 @@ def test_prefill_segments_vs_oracle(L):
         check(Sg, S_ref, T, f"state T={T}")
 
 
+def test_prefill_positive_log_gates(L):
+    """Log-gates of either sign (the kernel must not assume g <= 0): the
+    Gamma factors exp(G_i - G_j) then exceed 1 inside a chunk."""
+    q, k, v, g, beta, S = prefill_inputs(31, 1, 200, 2, 1)
+    g = np.random.RandomState(32).uniform(-0.3, 0.05, g.shape).astype(np.float32)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, 200, 2, 1, 128, 128, 64)
+    check(o, o_ref, 200, "output")
+    check(Sg, S_ref, 200, "state")
+
+
 def test_prefill_split_calls_bit_identical(L):
     """Calls split at chunk boundaries carry the fp32 state exactly."""
     q, k, v, g, beta, S = prefill_inputs(13, 1, 640, 4, 2)
