@@ -6,11 +6,14 @@
 // b, value head h, chunk n) with G = cumsum(g) inside the chunk and
 // Gamma_ij = exp(G_i - G_j) (i >= j):
 //   M = tril(beta_i (k_i . k_j) Gamma_ij, -1)       T = (I + M)^-1
-//   U = T diag(beta) V        W = T diag(beta e^G) K
 //   A = tril(Gamma_ij (q_i . k_j)) * scale
 // and, sequentially over chunks, with S the [128 x 128] state:
-//   v_new = U - W S ;  o = e^G scale (q S) + A v_new ;
+//   v_new = U - W S = T diag(beta) (V - diag(e^G) K S)
+//   o = scale e^G (q S) + A v_new
 //   S' = e^{G_last} S + K^T diag(e^{G_last - G}) v_new
+// HF forms U = T diag(beta) V and W = T diag(beta e^G) K first
+// (modeling_qwen3_5.py:299-300); the product is regrouped here so that the
+// chunk's 64x64 T multiplies one right-hand side, after the K S product.
 //
 // Parallel over the sequence.  The step is affine in S:
 //   S' = Phi_n S + C_n,  Phi_n = e^{G_last} I - K^T diag(e^{G_last-G}) W,
@@ -18,33 +21,47 @@
 // so the chunks are cut into P segments and
 //   pass 1: segment 0 runs the recurrence from the initial state (with o);
 //           every middle segment p runs it from S = 0 and, alongside, on
-//           128 more state columns started at I with U = 0, which yields its
+//           128 more state columns started at I with V = 0, which yields its
 //           local result C_p and its transition Phi_p;
 //   pass 2: segment p = 1 .. P-1 first composes its start state,
 //           S_start(q+1) = Phi_q S_start(q) + C_q from S_start(1) = the end of
 //           segment 0, then reruns the recurrence from it, with o.
-// The work is twice that of one sequential pass, spread over (P-1) x heads
-// workgroups instead of heads.
 //
-// Each workgroup (8 waves, two per SIMD, so that one wave's LDS and MFMA
-// latencies overlap the other's work) owns one (sequence, head, segment)
-// and walks its chunks.  Per chunk, stage A loads the chunk's k, q, v rows
-// into LDS, forms K K^T and Q K^T on bf16 MFMA, inverts (I + M) by 16 x 16
-// blocks and solves for W and U.  Stage B (each wave, its own 16 state
-// columns) runs the recurrence: the state and v_new never leave registers.
+// Workgroup: 8 waves in two roles, one of each role per SIMD.
+//  - State waves 0..3 own 32 state columns each (64 in a transition
+//    segment) in VGPRs and run the S-dependent products of chunk n:
+//    P = K S and O = Q S (phase 1), then v = T diag(beta)(V - e^G P),
+//    o^T = e^G scale O^T + v^T A^T and the state update (phase 2).
+//  - Helper waves 4..7 prepare the S-independent operands one chunk ahead
+//    and stream the chunk tiles: in phase 1 of chunk n one helper builds T
+//    of chunk n (forward substitution of the 16x16 diagonal blocks of M on
+//    the VALU, then the off-diagonal blocks on MFMA); in phase 2 the helpers
+//    form K K^T and K Q^T of chunk n+1 and write M and the A fragments.
+//  Two LDS barriers per chunk separate the phases, so the MFMA-heavy state
+//  work of one role overlaps the latency-bound work of the other.
+//
+// Loads: the helpers move chunk tiles straight from HBM into LDS
+// (global_load_lds_dwordx4, 1 KiB per wave instruction): at the start of
+// chunk n the k rows, gates and betas of chunk n+2 and the v rows of n+1,
+// after the first barrier the q rows of chunk n+2.  Every load is issued,
+// with its chunk index clamped to the sequence, so that each helper has the
+// same count in flight and waits with a fixed vmcnt.
 //
 // Fragment orders.  The 32 k-indices of one 16x16x32 MFMA may be assigned
 // to lanes in any order as long as both operands use the same order.
 //  - k = t (a chunk row): lane group g holds t = {4g..4g+3, 16+4g..16+4g+3}
-//    of a 32-block, which is the accumulator layout of two stacked 16 x 16
-//    tiles (lane group g holds rows 4g..4g+3 of each), so v_new feeds the
-//    next products straight from registers.
+//    of a 32-block ("t order"), which is the accumulator layout of two
+//    stacked 16 x 16 tiles (lane group g holds rows 4g..4g+3 of each), so an
+//    accumulator feeds the next products straight from registers, as the
+//    B operand and, for its transpose, as the A operand.
 //  - k = d (a state row): lane group g holds d = 8g..8g+7 of a 32-block, the
-//    natural order, so q and Phi rows are read with one 16-byte LDS read per
+//    natural order, so q and k rows are read with one 16-byte LDS read per
 //    lane.  For that, state tile 2j + u holds, in lane group g, the state
 //    rows 32j + 8g + 4u + e (e = 0..3): the state's rows are permuted among
 //    the tiles (srow below), which the products that write the state follow
 //    by reading their A operand rows in the same order.
+#include <utility>
+
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -55,8 +72,8 @@ constexpr int C = kChunk;     // 64
 constexpr int D = kHeadDim;   // 128
 constexpr int NW = 8;         // waves per workgroup
 constexpr int NT = 64 * NW;   // threads per workgroup
-constexpr int PC = C + 8;     // bf16 row pitch of the [.][C] tiles Wt and Ot (144 B)
-constexpr int PA = C + 16;    // bf16 row pitch of At (160 B: conflict-free transposing reads)
+constexpr int NSW = 4;        // state waves (the first four)
+constexpr float kLog2e = 1.4426950408889634f;
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
@@ -109,7 +126,7 @@ GDN_DEV bf16x8_t frag_acc_scaled(const f32x4_t &lo, const f32x4_t &hi, const f32
 // 16x16x16 MFMA helpers.  Layout: A lane (g, r) = A[r][4g..4g+3],
 // B lane (g, r) = B[4g..4g+3][r], C lane (g, r) = C[4g..4g+3][r].  So the
 // accumulator of a 16x16 tile is the B operand of the next product, and the
-// accumulator of X^T is the A operand of X: X Y = mfma(C(X^T), C(Y)).
+// accumulator of X^T is the A operand of X.
 // ---------------------------------------------------------------------------
 
 GDN_DEV f32x4_t mfma16(s4_t a, s4_t b, f32x4_t c) {
@@ -134,16 +151,14 @@ GDN_DEV void split_bf(const f32x4_t &x, u32x2_t &hi, u32x2_t &lo) {
     lo = bf4u(r);
 }
 
-// c + X Y in fp32 for 16x16 tiles given as accumulators xt = C(X^T) and
-// y = C(Y): four mfma_f32_16x16x4_f32 steps, step s taking k = 4g + s in lane
-// group g, which is element s of both accumulator tiles.  The block inverse
-// needs the full fp32 significand: its partial products (I + Z)(I + Z^2)...
-// can exceed the final entries by several orders of magnitude (repeated
-// keys, beta near 1) and cancel.
-GDN_DEV f32x4_t mfma_f32x16(const f32x4_t &xt, const f32x4_t &y, f32x4_t c) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(xt[s], y[s], c, 0, 0, 0);
-    return c;
+// B operand pair (hi, lo) of two stacked accumulator tiles: hi + lo carries
+// 16 significant bits of each element.
+GDN_DEV void frag_acc_split(const f32x4_t &lo_tile, const f32x4_t &hi_tile, bf16x8_t &hi, bf16x8_t &lo) {
+    u32x2_t ah, al, bh, bl;
+    split_bf(lo_tile, ah, al);
+    split_bf(hi_tile, bh, bl);
+    hi = as_bf16x8(join(ah, bh));
+    lo = as_bf16x8(join(al, bl));
 }
 
 // Inclusive prefix sum over the 64 lanes of a wavefront with DPP: shifts
@@ -164,8 +179,54 @@ GDN_DEV float wave_incl_scan(float x) {
     return x;
 }
 
+// Index of this wave in the workgroup, as a wave-uniform (scalar) value, so
+// that branches on a wave's role compile to scalar branches.
+GDN_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// acc += (m in lane I of this lane's 16-lane row) * x: one DPP row_newbcast
+// FMA.  The compiler's update_dpp builtin merges row_newbcast moves of
+// different sources, so the instruction is written out; the s_nop covers
+// the VALU -> DPP read hazard on m.
+template <int I> GDN_DEV void fma_row_bcast(float &acc, float m, float x) {
+    __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc)
+                     : "v"(m), "v"(x), "n"(I));
+}
+
+// 4 x 4 transpose of (16-lane row, register): afterwards x[b] row g holds
+// what x[g] row b held.  v_permlane32_swap exchanges the upper two rows of
+// its first operand with the lower two of its second, v_permlane16_swap the
+// odd rows of the first with the even rows of the second.
+GDN_DEV void row_transpose4(uint32_t (&x)[4]) {
+    auto s02 = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
+    auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    x[0] = s01[0];
+    x[1] = s01[1];
+    x[2] = s23[0];
+    x[3] = s23[1];
+}
+
+// Wait for this wave's outstanding LDS operations and order the compiler's
+// LDS accesses around the wait (a wave reads back what it wrote itself).
+GDN_DEV void lds_fence() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Workgroup barrier for LDS traffic only.  __syncthreads() is also a release
+// fence for global memory, which would wait for outstanding direct loads at
+// every barrier; here the waves exchange data only through LDS, so the
+// barrier waits for this wave's LDS operations and nothing else.  Direct
+// loads become visible to other waves once their issuing wave has waited
+// for them (vmcnt) before a barrier.
+GDN_DEV void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// vmcnt(n): at most n of this wave's vector memory operations outstanding.
+GDN_DEV void wait_vmem0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+GDN_DEV void wait_vmem9() { __builtin_amdgcn_s_waitcnt(0x0F79); }  // 4 k, 4 v, 1 gate load
+GDN_DEV void wait_vmem4() { __builtin_amdgcn_s_waitcnt(0x0F74); }  // 4 q loads
+
 // ---------------------------------------------------------------------------
-// Shared memory and stage A
+// Shared memory
 // ---------------------------------------------------------------------------
 
 // Chunk tiles (k, q, v rows: [64][128] bf16) are written by direct
@@ -177,325 +238,386 @@ GDN_DEV float wave_incl_scan(float x) {
 GDN_DEV int fsw(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 GDN_DEV int sw(int row, int col) { return row * D + ((((col >> 3) ^ fsw(row)) << 3) | (col & 7)); }
 
+// Per-chunk gates for the state waves.
+struct Gates {
+    float bt[C];    // beta (0 past the sequence end)
+    float eg[C];    // e^{G}
+    float egl[C];   // e^{G_last - G}
+    float seg[C];   // scale e^{G}
+    float gam;      // e^{G_last}
+    float pad[3];
+};
+
+// Fragments of the lower block triangle of a 64x64 matrix X for 16x16x32
+// MFMA with k in t order: fragment (rt, kb) (rt = 0..3, kb <= rt/2), lane
+// (g, r), slots 4h + e hold X[16 rt + r][32 kb + 16 h + 4 g + e], i.e. half
+// h of the fragment is the 16x16x16 A layout of block (rt, 2 kb + h).  The
+// upper blocks (0, 1) and (2, 3) are zero and are never written after set-up.
+GDN_DEV constexpr int fidx(int rt, int kb) { return rt < 2 ? rt : 2 * rt - 2 + kb; }
+// M blocks (a >= b), fp32 row-major 16x16.
+GDN_DEV constexpr int mbi(int a, int b) { return a * (a + 1) / 2 + b; }
+
 struct Smem {
-    uint16_t Kb[2][C * D];   // k rows, two buffers (chunk n and n+1)
-    uint16_t Qb[2][C * D];   // q rows (output passes)
+    uint16_t Kb[3][C * D];   // k rows of chunks n, n+1, n+2
+    uint16_t Qb[2][C * D];   // q rows (output segments)
     uint16_t Vb[2][C * D];   // v rows
-    float grb[2][C], btb[2][C];  // log-gates, beta
-    uint16_t Wt[D][PC];   // -W^T  [d][i]
-    uint16_t At[C][PA];   // A^T   [j][i]
-    uint16_t Ot[D][PC];   // o^T of the chunk, staged for row stores
-    u32x2_t Mf[6][64];    // A fragments of -M_ab (a > b), 16x16x16 layout
-    u32x2_t Lf[4][64];    // A fragments of T_aa - I
-    float G2[C], eG[C], eGl[C], bt[C], bg[C];  // G2 = G log2(e)
+    float graw[2][C], braw[2][C];  // log-gates and betas as loaded
+    Gates gt[2];
+    u32x4_t Af[2][6][64];    // A fragments (output segments), two chunks
+    u32x4_t Tf[2][6][64];    // (T - I) fragments, two chunks
+    float Mb[10][256];       // M blocks of the next chunk, fp32 column-major:
+                             // Mb[.][16 j + i] = M[i][j]
+    float hg[4][2][C];       // per helper wave: G log2(e) and beta of its chunk
 };
 
-// The rows of one chunk in LDS.
-struct ChunkView {
-    const uint16_t *K, *Q, *V;
-    const float *gr, *bt;
-};
-GDN_DEV ChunkView chunk_view(const Smem &sm, int buf) {
-    return ChunkView{sm.Kb[buf], sm.Qb[buf], sm.Vb[buf], sm.grb[buf], sm.btb[buf]};
-}
+// ---------------------------------------------------------------------------
+// Loads (helper waves hw = 0..3)
+// ---------------------------------------------------------------------------
 
-GDN_DEV int mf_index(int a, int b) { return a * (a - 1) / 2 + b; }  // a > b
-
-// Per-lane element offsets of the direct loads within one chunk (fixed for a
-// segment).  Wave w fills rows 8w .. 8w+7 of each tile, 4 rows per
-// instruction: lane L of instruction j takes row i = 8w + 4j + L/16 and LDS
-// slot L%16, i.e. piece c = (L%16) ^ fsw(i) of the row in HBM.
-struct LoadPlan {
-    int kq[2], v[2];  // row offset * row stride + 8c, for k/q and for v
-    int row[2];       // i
+// Per-lane element offsets of a helper's direct loads: rows 16 hw .. 16 hw
+// + 15 of a chunk, 4 rows per instruction (lane L of instruction j takes row
+// i = 16 hw + 4 j + L/16 and LDS slot L%16, i.e. piece (L%16) ^ fsw(i) of
+// the row in HBM).  Rows at or past `valid` read row valid - 1 (their values
+// are multiplied by beta = 0 or never stored).
+struct LoadOffs {
+    int kq[4], v[4];  // k and q rows (stride Hk * 128), v rows (stride Hv * 128)
 };
-GDN_DEV LoadPlan load_plan(int Hv, int Hk, int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
-    LoadPlan lp;
+GDN_DEV LoadOffs load_offs(int Hk, int Hv, int valid, int hw, int lane) {
+    LoadOffs o;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int i = 8 * wave + 4 * j + (lane >> 4);
+    for (int j = 0; j < 4; ++j) {
+        const int i = 16 * hw + 4 * j + (lane >> 4);
         const int c = (lane & 15) ^ fsw(i);
-        lp.row[j] = i;
-        lp.kq[j] = i * Hk * D + 8 * c;
-        lp.v[j] = i * Hv * D + 8 * c;
+        const int ii = min(i, valid - 1);
+        o.kq[j] = ii * Hk * D + 8 * c;
+        o.v[j] = ii * Hv * D + 8 * c;
     }
-    return lp;
+    return o;
 }
-
-// Issue the direct loads of chunk n into buffer `buf` (completion: vmcnt).
-// Rows past the sequence end read row T-1 and are zeroed later.  Waves 0 and
-// 1 also load the 64 log-gates and betas (4 bytes per lane).
-template <bool WITH_Q>
-GDN_DEV void load_chunk(Smem &sm, int buf, const LoadPlan &lp, const uint16_t *q,
-                        const uint16_t *k, const uint16_t *v, const float *g, const float *beta,
-                        int b, int h, int kh, int n, int T, int Hv, int Hk, int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
-    const size_t t0 = (size_t)b * T + (size_t)n * C;   // first row of the chunk
-    const uint16_t *kb = k + (t0 * Hk + kh) * D;
-    const uint16_t *qb = q + (t0 * Hk + kh) * D;
-    const uint16_t *vb = v + (t0 * Hv + h) * D;
-    const bool tail = n * C + C > T;
+// Row 0 of chunk ci of head `head` of a [B][T][H][128] tensor.
+GDN_DEV const uint16_t *chunk_rows(const uint16_t *x, int H, int head, int b, int ci, int T) {
+    return x + (((size_t)b * T + (size_t)ci * C) * H + head) * D;
+}
+GDN_DEV void load_rows(uint16_t *tile, const uint16_t *rows, const int (&off)[4], int hw) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int i0 = 8 * wave + 4 * j;
-        int okq = lp.kq[j], ov = lp.v[j];
-        if (tail) {
-            const int last = T - 1 - n * C;  // last row inside the sequence
-            const int dr = min(lp.row[j], last) - lp.row[j];
-            okq += dr * Hk * D;
-            ov += dr * Hv * D;
-        }
-        __builtin_amdgcn_global_load_lds(kb + okq, (lds_void_t *)&sm.Kb[buf][i0 * D], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vb + ov, (lds_void_t *)&sm.Vb[buf][i0 * D], 16, 0, 0);
-        if constexpr (WITH_Q)
-            __builtin_amdgcn_global_load_lds(qb + okq, (lds_void_t *)&sm.Qb[buf][i0 * D], 16, 0, 0);
-    }
-    if (wave < 2) {
-        const int tc = min(n * C + lane, T - 1);
-        const float *src = (wave == 0 ? g : beta) + ((size_t)b * T + tc) * Hv + h;
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(wave == 0 ? sm.grb[buf] : sm.btb[buf]),
-                                         4, 0, 0);
+    for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(rows + off[j], (lds_void_t *)&tile[(16 * hw + 4 * j) * D], 16, 0, 0);
+}
+
+// Log-gates (helpers 0, 1) or betas (2, 3), 32 tokens each.
+GDN_DEV void load_gates(Smem &sm, int slot, const float *g, const float *beta, int b, int h, int Hv,
+                        int ci, int T, int hw, int lane) {
+    if (lane < 32) {
+        const int t = 32 * (hw & 1) + lane;
+        const int tc = min(ci * C + t, T - 1);
+        const float *src = (hw < 2 ? g : beta) + ((size_t)b * T + tc) * Hv + h;
+        float *dst = (hw < 2 ? sm.graw[slot] : sm.braw[slot]) + 32 * (hw & 1);
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 4, 0, 0);
     }
 }
 
-// Wait for this thread's outstanding global loads and stores (including the
-// direct LDS loads).
-GDN_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+// ---------------------------------------------------------------------------
+// Operand readers
+// ---------------------------------------------------------------------------
 
-// Workgroup barrier for LDS traffic only.  __syncthreads() is also a release
-// fence for global memory, which would wait for the next chunk's direct loads
-// at every barrier; here the waves only exchange data through LDS, so the
-// barrier waits for this wave's LDS operations and nothing else.  Global
-// visibility of the direct loads is established by wait_vmem() before the
-// barrier that ends a chunk.
-GDN_DEV void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The lane index, opaque to the optimiser: offsets derived from it inside a
+// loop are recomputed there (a few VALU operations) instead of being kept
+// live in VGPRs across the loop.
+GDN_DEV int opaque_lane(int lane) {
+    __asm__ volatile("" : "+v"(lane));
+    return lane;
+}
 
-// Rows of chunk n past the sequence end read as zero (HF pads with zeros).
-// Call between barriers, after the chunk's loads have landed.
-template <bool WITH_Q>
-GDN_DEV void zero_tail(Smem &sm, int buf, int n, int T, int tid) {
-    const int valid = T - n * C;  // 1 .. 63
-    for (int e = tid; e < (C - valid) * (D / 8); e += NT) {
-        const int i = valid + e / (D / 8), c = e % (D / 8);
-        const uint4 z = make_uint4(0, 0, 0, 0);
-        *reinterpret_cast<uint4 *>(&sm.Kb[buf][i * D + 8 * c]) = z;
-        *reinterpret_cast<uint4 *>(&sm.Vb[buf][i * D + 8 * c]) = z;
-        if constexpr (WITH_Q) *reinterpret_cast<uint4 *>(&sm.Qb[buf][i * D + 8 * c]) = z;
+// Per-lane element offsets into a swizzled [64][128] chunk tile.  The
+// swizzle permutes the 16-byte pieces of a row by a function of the row's
+// low 4 bits only, so moving by 16 rows or by 32 columns adds a constant:
+// each operand below is one of four per-lane offsets plus an immediate.
+struct TileOffs {
+    int nat[4];  // row r, columns 32 kb + 8 g .. +7
+    int tr[4];   // row 4 g + r/4, 8-byte piece at column 32 q + 8 (r & 3)
+};
+GDN_DEV TileOffs tile_offs(int g, int r) {
+    TileOffs o;
+    const int row = 4 * g + (r >> 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        o.nat[j] = sw(r, 32 * j + 8 * g);
+        o.tr[j] = row * D + 8 * ((4 * j + (r & 3)) ^ fsw(row));
     }
-    if (tid >= valid && tid < C) {
-        sm.grb[buf][tid] = 0.f;
-        sm.btb[buf][tid] = 0.f;
-    }
+    return o;
 }
 
-// Row-order operand of a swizzled chunk tile: element k = 8g + s of row
-// row0 + r (one 16-byte read).
-GDN_DEV bf16x8_t sfrag_nat(const uint16_t *base, int row0, int k0, int g, int r) {
-    return as_bf16x8(*reinterpret_cast<const u32x4_t *>(base + sw(row0 + r, k0 + 8 * g)));
+// Row-order operand: lane (g, r) gets row 16 rt + r, elements 32 kb + 8 g ..
+// +7 (one 16-byte read).
+GDN_DEV bf16x8_t nat_frag(const uint16_t *tile, const TileOffs &o, int rt, int kb) {
+    return as_bf16x8(*reinterpret_cast<const u32x4_t *>(tile + 16 * rt * D + o.nat[kb]));
 }
 
-// A operand of K^T for the state update, k = t in the t order above and rows
-// in state tile order: lane (g, r) gets K[k0 + {4g..4g+3, 16+4g..16+4g+3}]
-// [d], d = the state row of tile rt held at row r (two transposing reads:
-// source lane m + 4j addresses row k0 + 4g + j, columns 8m + .. of the
-// tile's 32-block, so output lane 4m + e gets column 32 (rt>>1) + 8m +
-// 4 (rt&1) + e).
-GDN_DEV bf16x8_t kfrag_t(const uint16_t *base, int k0, int rt, int g, int r) {
-    const int row = k0 + 4 * g + (r >> 2);
-    const int col = 32 * (rt >> 1) + 8 * (r & 3) + 4 * (rt & 1);
-    return as_bf16x8(join(lds_tr(base + sw(row, col)), lds_tr(base + sw(row + 16, col))));
+// A operand of K^T for the state update, k = t in t order and rows in state
+// tile order: lane (g, r) gets K[32 kb + {4g..4g+3, 16+4g..16+4g+3}][d], d =
+// the state row of tile rt held at row r (two transposing reads: source lane
+// m + 4j addresses row 32 kb + 4g + j, columns 8m + .. of the tile's
+// 32-block, so output lane 4m + e gets column 32 (rt>>1) + 8m + 4 (rt&1) + e).
+GDN_DEV bf16x8_t kt_frag(const uint16_t *tile, const TileOffs &o, int rt, int kb) {
+    const uint16_t *p = tile + 32 * kb * D + o.tr[rt >> 1] + 4 * (rt & 1);
+    return as_bf16x8(join(lds_tr(p), lds_tr(p + 16 * D)));
 }
 
-// A operand of W for v = U - W S (rows t = 16 rt + r, k = d natural) from
-// -W^T [d][t]: source lane m + 4j addresses row 32 kb + 8g + j (+4).
-GDN_DEV bf16x8_t wfrag(const uint16_t (&Wt)[D][PC], int kb, int rt, int g, int r) {
-    const uint16_t *p = &Wt[32 * kb + 8 * g + (r >> 2)][16 * rt + 4 * (r & 3)];
-    return as_bf16x8(join(lds_tr(p), lds_tr(p + 4 * PC)));
+// Offset of the accumulator tile (rows 4g + e, column 16 cb + r) of column
+// block cb of a chunk tile, for acc_tile.
+GDN_DEV int acc_off(int cb, int g, int r) {
+    const int row = 4 * g + (r >> 2);
+    return row * D + 8 * ((2 * cb + ((r >> 1) & 1)) ^ fsw(row)) + 4 * (r & 1);
 }
-
-// A operand of A for o += A v (rows i = 16 rt + r, k = j in t order) from
-// A^T [j][i].
-GDN_DEV bf16x8_t afrag(const uint16_t (&At)[C][PA], int kb, int rt, int g, int r) {
-    const uint16_t *p = &At[32 * kb + 4 * g + (r >> 2)][16 * rt + 4 * (r & 3)];
-    return as_bf16x8(join(lds_tr(p), lds_tr(p + 16 * PA)));
-}
-
-// Accumulator tile (rows row0 .. row0+15, columns col .. col+15) of a chunk
-// tile, scaled per row by sc (rows row0 + 4g .. +3): one transposing read.
-GDN_DEV f32x4_t rhs_tile(const uint16_t *base, int row0, int col, const f32x4_t &sc, int g, int r) {
-    const u32x2_t w = lds_tr(base + sw(row0 + 4 * g + (r >> 2), col + 4 * (r & 3)));
+// Accumulator tile (rows 16 rt + 4g + e, column 16 cb + r): one transposing
+// read at the offset acc_off(cb).
+GDN_DEV f32x4_t acc_tile(const uint16_t *tile, int off, int rt) {
+    const u32x2_t w = lds_tr(tile + 16 * rt * D + off);
     f32x4_t x;
-    x[0] = __uint_as_float(w[0] << 16) * sc[0];
-    x[1] = __uint_as_float(w[0] & 0xFFFF0000u) * sc[1];
-    x[2] = __uint_as_float(w[1] << 16) * sc[2];
-    x[3] = __uint_as_float(w[1] & 0xFFFF0000u) * sc[3];
+    x[0] = __uint_as_float(w[0] << 16);
+    x[1] = __uint_as_float(w[0] & 0xFFFF0000u);
+    x[2] = __uint_as_float(w[1] << 16);
+    x[3] = __uint_as_float(w[1] & 0xFFFF0000u);
     return x;
 }
 
 GDN_DEV f32x4_t lds_f4(const float *p) { return *reinterpret_cast<const f32x4_t *>(p); }
+GDN_DEV bf16x8_t frag_ld(const u32x4_t &p) { return as_bf16x8(p); }
 
-// Stage A for the chunk in view cv (landed and visible to all threads).
-//  - wave 0 derives the gates: G = cumsum(g) (kept as G log2(e)), e^G,
-//    e^{G_last - G}, beta, beta e^G;
-//  - waves 0..3: row tile w of K K^T; waves 4..7 (output passes): row tile
-//    w-4 of Q K^T;
-//  - waves 0..3: K K^T is symmetric, so the upper tiles of its row tile give
-//    the A operands of the lower blocks of M directly and the diagonal tile
-//    gives both Z = -M_ww and Z^T.  The wave inverts its diagonal block,
-//    T_ww = (I + Z)(I + Z^2)(I + Z^4)(I + Z^8) (Z is nilpotent), on fp32
-//    MFMA.  Waves 4..7 write A^T;
-//  - each wave solves (I + M) X = R by block rows for its right-hand sides:
-//    W columns 16w .. 16w+15 (R = diag(beta e^G) K) and U columns
-//    ucol0 .. ucol0 + 16 NUT - 1 (R = diag(beta) V), kept in registers;
-//  - -W^T goes to LDS.
-template <bool WITH_Q, int NUT, bool DO_U>
-GDN_DEV void stage_a(Smem &sm, const ChunkView &cv, float q_scale, int tid, int ucol0,
-                     f32x4_t (&U)[4][NUT]) {
-    const int lane = tid & 63, wave = tid >> 6;
+// ---------------------------------------------------------------------------
+// Helper work
+// ---------------------------------------------------------------------------
+
+// Gates of chunk c for this lane's token (lane = row of the chunk), both
+// zeroed past the sequence end (HF pads the last chunk with zeros): G log2(e)
+// and beta go to the helper's own copy hg[hw] (read back by this wave only);
+// with `write` the wave also stores the state waves' per-chunk gates.
+GDN_DEV void chunk_gates(Smem &sm, int slot, int c, int T, float q_scale, int hw, int lane, bool write) {
+    const int valid = min(C, T - c * C);
+    const float x = lane < valid ? sm.graw[slot][lane] : 0.f;
+    const float bv = lane < valid ? sm.braw[slot][lane] : 0.f;
+    const float G = wave_incl_scan(x);
+    const float Gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), 63));
+    sm.hg[hw][0][lane] = G * kLog2e;
+    sm.hg[hw][1][lane] = bv;
+    if (write) {
+        Gates &gt = sm.gt[slot];
+        const float eg = expf(G);
+        gt.bt[lane] = bv;
+        gt.eg[lane] = eg;
+        gt.egl[lane] = expf(Gl - G);
+        gt.seg[lane] = q_scale * eg;
+        if (lane == 0) gt.gam = expf(Gl);
+    }
+    lds_fence();
+}
+
+// K K^T tiles of row blocks A0 < A1 (all column blocks b <= a), then
+// M_ab = beta_i Gamma_ij (k_i . k_j) for i > j into Mb (fp32 row-major).
+template <int A> GDN_DEV void write_m(Smem &sm, const f32x4_t (&acc)[A + 1], const float *G2, const float *Bt,
+                                      int g, int r) {
+    const f32x4_t Gi = lds_f4(&G2[16 * A + 4 * g]);
+    const f32x4_t Bi = lds_f4(&Bt[16 * A + 4 * g]);
+#pragma unroll
+    for (int b = 0; b <= A; ++b) {
+        const float Gj = G2[16 * b + r];
+        f32x4_t m;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool lower = (b < A) || (4 * g + e > r);
+            const float gm = __builtin_amdgcn_exp2f(lower ? Gi[e] - Gj : 0.f);
+            m[e] = lower ? Bi[e] * gm * acc[b][e] : 0.f;
+        }
+        // column-major: lane (g, r) holds rows 4g .. 4g+3 of column r
+        *reinterpret_cast<f32x4_t *>(&sm.Mb[mbi(A, b)][16 * r + 4 * g]) = m;
+    }
+}
+// K Q^T tiles (b, a) for q row blocks A0 < A1 and b <= a: lane (g, r),
+// element e holds k_{t'} . q_t with t' = 16 b + 4 g + e, t = 16 a + r, which
+// is the A-fragment slot layout, so each tile is one 8-byte store of
+// A[t][t'] = scale Gamma_{t t'} (q_t . k_t'), t' <= t.
+template <int A> GDN_DEV void write_a(u32x4_t (&af)[6][64], const f32x4_t (&acc)[A + 1], const float *G2,
+                                      float q_scale, int lane, int g, int r) {
+    const float Gt = G2[16 * A + r];
+#pragma unroll
+    for (int b = 0; b <= A; ++b) {
+        const f32x4_t Gp = lds_f4(&G2[16 * b + 4 * g]);
+        f32x4_t x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool lower = (b < A) || (4 * g + e <= r);
+            const float gm = __builtin_amdgcn_exp2f(lower ? Gt - Gp[e] : 0.f);
+            x[e] = lower ? q_scale * gm * acc[b][e] : 0.f;
+        }
+        *reinterpret_cast<u32x2_t *>(reinterpret_cast<char *>(&af[fidx(A, b >> 1)][lane]) + 8 * (b & 1)) =
+            bf4u(x);
+    }
+}
+// The Gram tiles of chunk rows A0 < A1 (every column block b <= a): with
+// WITH_K, K K^T tiles (a, b) -> M blocks; with WITH_Q, K Q^T tiles (b, a) ->
+// A fragments.
+template <int A0, int A1, bool WITH_K, bool WITH_Q>
+GDN_DEV void gram_rows(Smem &sm, u32x4_t (&af)[6][64], const uint16_t *K, const uint16_t *Q,
+                       const float *G2, const float *Bt, float q_scale, int lane, int g, int r) {
+    const TileOffs to = tile_offs(g, r);
+    f32x4_t kk0[A0 + 1], kk1[A1 + 1], qk0[A0 + 1], qk1[A1 + 1];
+#pragma unroll
+    for (int b = 0; b <= A0; ++b) kk0[b] = qk0[b] = zero4();
+#pragma unroll
+    for (int b = 0; b <= A1; ++b) kk1[b] = qk1[b] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) {
+        bf16x8_t kf[A1 + 1];
+#pragma unroll
+        for (int b = 0; b <= A1; ++b) kf[b] = nat_frag(K, to, b, kb);
+        if constexpr (WITH_K) {
+#pragma unroll
+            for (int b = 0; b <= A0; ++b) kk0[b] = mfma_16x16x32_bf16(kf[A0], kf[b], kk0[b]);
+#pragma unroll
+            for (int b = 0; b <= A1; ++b) kk1[b] = mfma_16x16x32_bf16(kf[A1], kf[b], kk1[b]);
+        }
+        if constexpr (WITH_Q) {
+            const bf16x8_t q0 = nat_frag(Q, to, A0, kb);
+            const bf16x8_t q1 = nat_frag(Q, to, A1, kb);
+#pragma unroll
+            for (int b = 0; b <= A0; ++b) qk0[b] = mfma_16x16x32_bf16(kf[b], q0, qk0[b]);
+#pragma unroll
+            for (int b = 0; b <= A1; ++b) qk1[b] = mfma_16x16x32_bf16(kf[b], q1, qk1[b]);
+        }
+    }
+    if constexpr (WITH_K) {
+        write_m<A0>(sm, kk0, G2, Bt, g, r);
+        write_m<A1>(sm, kk1, G2, Bt, g, r);
+    }
+    if constexpr (WITH_Q) {
+        write_a<A0>(af, qk0, G2, q_scale, lane, g, r);
+        write_a<A1>(af, qk1, G2, q_scale, lane, g, r);
+    }
+}
+
+// T = (I + M)^-1 of the chunk whose M is in Mb, as (T - I) fragments in Tf.
+//  1. Diagonal blocks by substitution in fp32 on the VALU (the row
+//     recurrence of HF, modeling_qwen3_5.py:294-297, on each 16x16 block,
+//     solved for the rows of T_aa): lane (a, j) computes row j of T_aa.
+//  2. Off-diagonal blocks T_ab = -T_aa sum_{c=b}^{a-1} M_ac T_cb on bf16
+//     MFMA, with T_aa = I + L_aa so that the identity parts stay exact:
+//     Y = M_ab + M_ab L_bb + sum_{c>b} M_ac T_cb,  T_ab = -(Y + L_aa Y).
+// Step K of the row substitution in build_t: x[K] is final, then
+// acc[i] += x[K] M[K][i] for i < K, M[K][i] broadcast from lane i of the row.
+template <int K, int... Is>
+GDN_DEV void subst_update(float (&acc)[16], float xk, float mk, std::integer_sequence<int, Is...>) {
+    (fma_row_bcast<K - 1 - Is>(acc[K - 1 - Is], mk, xk), ...);  // next row's term first
+}
+template <int K>
+GDN_DEV void back_subst_step(float (&acc)[16], float (&x)[16], const f32x4_t (&mcol)[4], int j) {
+    x[K] = ((K == j) ? 1.f : 0.f) - acc[K];
+    if constexpr (K > 0) {
+        subst_update<K>(acc, x[K], mcol[K >> 2][K & 3], std::make_integer_sequence<int, K>{});
+        back_subst_step<K - 1>(acc, x, mcol, j);
+    }
+}
+
+GDN_DEV void build_t(Smem &sm, u32x4_t (&Tf)[6][64], int lane) {
     const int g = lane >> 4, r = lane & 15;
-    const int rw = wave & 3;  // row tile of this wave's Gram product
-    const bool gram = wave < 4 || WITH_Q;
-    const bool kk_wave = wave < 4;
-
-    if (wave == 0) {
-        const float x = wave_incl_scan(cv.gr[lane]);
-        const float glast = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-        const float eg = expf(x);
-        sm.G2[lane] = x * 1.4426950408889634f;
-        sm.eG[lane] = eg;
-        sm.eGl[lane] = expf(glast - x);
-        const float bv = cv.bt[lane];
-        sm.bt[lane] = bv;
-        sm.bg[lane] = bv * eg;
+    // One LDS round trip for every input: lane (a, j) reads column j of M_aa
+    // (for the substitution), every lane the accumulator tiles of the six
+    // off-diagonal blocks.  MC index: (1,0) 0, (2,1) 1, (3,2) 2, (2,0) 3,
+    // (3,1) 4, (3,0) 5.
+    const int a = lane >> 4, j = lane & 15;
+    f32x4_t mcol[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) mcol[q] = lds_f4(&sm.Mb[mbi(a, a)][16 * j + 4 * q]);
+    constexpr int off_a[6] = {1, 2, 3, 2, 3, 3}, off_b[6] = {0, 1, 2, 0, 1, 0};
+    f32x4_t MC[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) MC[i] = lds_f4(&sm.Mb[mbi(off_a[i], off_b[i])][16 * r + 4 * g]);
+    // identity, accumulator layout (bf16): transposes by one MFMA
+    s4_t I4;
+    {
+        f32x4_t id;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) id[e] = (4 * g + e == r) ? 1.f : 0.f;
+        I4 = bf4(id);
     }
-    lds_barrier();
-    f32x4_t acc[4];
+    // Lane (a, j) computes row j of T_aa from T (I + M) = I:
+    // T[j][i] = delta_ji - sum_{k>i} T[j][k] M[k][i], for i = 15 down to 0,
+    // right-looking: once x[k] = T[j][k] is final, row k of M updates every
+    // earlier column.  M[k][i] is element k of lane (a, i)'s column,
+    // broadcast within the 16-lane row of block a (DPP row_newbcast).
+    uint32_t w01[4], w23[4];  // bf16 pairs of L = T_aa - I: row j, columns 4q .. 4q+3
+    {
+        float acc[16], x[16];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) acc[ct] = zero4();
-    if (gram) {
-        const uint16_t *X = kk_wave ? cv.K : cv.Q;
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        back_subst_step<15>(acc, x, mcol, j);
+        // x[j] is exactly 1 (x[k] = 0 for k > j)
 #pragma unroll
-        for (int kb = 0; kb < D / 32; ++kb) {
-            const bf16x8_t ax = sfrag_nat(X, 16 * rw, 32 * kb, g, r);
-            // all four column tiles: branch-free code lets the LDS reads run
-            // ahead of the MFMAs (tiles outside the triangle are discarded)
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct)
-                acc[ct] = mfma_16x16x32_bf16(ax, sfrag_nat(cv.K, 16 * ct, 32 * kb, g, r), acc[ct]);
-        }
-    }
-
-    if (gram) {
-        // Gates of this lane's rows (16 rw + 4g + e) and columns (16 ct + r).
-        // Every element below uses exactly one Gamma factor: exp(G_i - G_j)
-        // where row i >= column j (A, Z) and exp(G_j - G_i) where j > i (the
-        // transposed entries of M); masked elements take the other direction
-        // and are discarded by the select.
-        const f32x4_t Gw = lds_f4(&sm.G2[16 * rw + 4 * g]);
-        float Gc[4];
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) Gc[ct] = sm.G2[16 * ct + r];
-        f32x4_t ga[4];  // ga[ct][e] = Gamma for row 16 rw + 4g + e, column 16 ct + r
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool lower = 16 * ct + r <= 16 * rw + 4 * g + e;
-                ga[ct][e] = __builtin_amdgcn_exp2f(lower ? Gw[e] - Gc[ct] : Gc[ct] - Gw[e]);
-            }
-        if (!kk_wave) {
-            // A^T [j][i] = scale Gamma_ij (q_i . k_j), j <= i; zero above
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                const int j = 16 * ct + r;
-                f32x4_t av;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int i = 16 * rw + 4 * g + e;
-                    av[e] = (j <= i) ? q_scale * acc[ct][e] * ga[ct][e] : 0.f;
-                }
-                *reinterpret_cast<u32x2_t *>(&sm.At[j][16 * rw + 4 * g]) = bf4u(av);
-            }
-        } else {
-            const f32x4_t Bw = lds_f4(&sm.bt[16 * rw + 4 * g]);
-            float Bc[4];
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) Bc[ct] = sm.bt[16 * ct + r];
-            // A fragments of -M_{a,rw}, a > rw: element e of lane (g, r) is
-            // -M[16a + r][16 rw + 4g + e] = -beta Gamma (k.k) from tile (rw, a)
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                if (ct > rw) {
-                    f32x4_t m;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) m[e] = -Bc[ct] * ga[ct][e] * acc[ct][e];
-                    sm.Mf[mf_index(ct, rw)][lane] = bf4u(m);
-                }
-            }
-            // diagonal block: Z = -M_ww and Z^T as accumulator tiles (tile
-            // ct = rw, selected without indexing registers by a runtime value)
-            f32x4_t Z = zero4(), Zt = zero4(), I4;
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                if (ct == rw) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int i = 4 * g + e, j = r;
-                        Z[e] = (i > j) ? -Bw[e] * ga[ct][e] * acc[ct][e] : 0.f;
-                        Zt[e] = (j > i) ? -Bc[ct] * ga[ct][e] * acc[ct][e] : 0.f;
-                    }
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) I4[e] = (4 * g + e == r) ? 1.f : 0.f;
-            const f32x4_t Z2 = mfma_f32x16(Zt, Z, zero4());
-            const f32x4_t Z2t = mfma_f32x16(Z, Zt, zero4());
-            const f32x4_t Z4 = mfma_f32x16(Z2t, Z2, zero4());
-            const f32x4_t Z4t = mfma_f32x16(Z2, Z2t, zero4());
-            const f32x4_t Z8 = mfma_f32x16(Z4t, Z4, zero4());
-            // T^T = (I + Z^8)^T (I + Z^4)^T (I + Z^2)^T (I + Z)^T, built up as
-            // P^T <- P^T + (Z^k)^T P^T = P^T + mfma(C(Z^k), C(P^T))
-            f32x4_t Pt = I4 + Zt;
-            Pt = mfma_f32x16(Z2, Pt, Pt);
-            Pt = mfma_f32x16(Z4, Pt, Pt);
-            Pt = mfma_f32x16(Z8, Pt, Pt);
-            sm.Lf[rw][lane] = bf4u(Pt - I4);  // A fragment of T - I
+        for (int q = 0; q < 4; ++q) {
+            w01[q] = pack2_bf16_hw(4 * q == j ? 0.f : x[4 * q], 4 * q + 1 == j ? 0.f : x[4 * q + 1]);
+            w23[q] = pack2_bf16_hw(4 * q + 2 == j ? 0.f : x[4 * q + 2], 4 * q + 3 == j ? 0.f : x[4 * q + 3]);
         }
     }
-    lds_barrier();
-
-    // block forward substitution: X_a = T_aa (R_a - sum_{b<a} M_ab X_b)
-    f32x4_t Wx[4];
+    // the diagonal fragment halves for the state waves: row j, columns
+    // 4q .. 4q+3 of block (a, a) -> fragment fidx(a, a/2), lane 16 q + j,
+    // slots 4 (a&1) .. +3
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        Wx[a] = rhs_tile(cv.K, 16 * a, 16 * wave, lds_f4(&sm.bg[16 * a + 4 * g]), g, r);  // beta e^G
-        if constexpr (DO_U) {
-            const f32x4_t su = lds_f4(&sm.bt[16 * a + 4 * g]);  // beta
-#pragma unroll
-            for (int t = 0; t < NUT; ++t) U[a][t] = rhs_tile(cv.V, 16 * a, ucol0 + 16 * t, su, g, r);
-        }
-#pragma unroll
-        for (int b = 0; b < a; ++b) {
-            const s4_t am = __builtin_bit_cast(s4_t, sm.Mf[mf_index(a, b)][lane]);
-            Wx[a] = mfma16(am, bf4(Wx[b]), Wx[a]);
-            if constexpr (DO_U) {
-#pragma unroll
-                for (int t = 0; t < NUT; ++t) U[a][t] = mfma16(am, bf4(U[b][t]), U[a][t]);
-            }
-        }
-        const s4_t al = __builtin_bit_cast(s4_t, sm.Lf[a][lane]);
-        Wx[a] = mfma16(al, bf4(Wx[a]), Wx[a]);
-        if constexpr (DO_U) {
-#pragma unroll
-            for (int t = 0; t < NUT; ++t) U[a][t] = mfma16(al, bf4(U[a][t]), U[a][t]);
-        }
+    for (int q = 0; q < 4; ++q) {
+        u32x2_t w;
+        w[0] = w01[q];
+        w[1] = w23[q];
+        reinterpret_cast<u32x2_t *>(&Tf[fidx(a, a >> 1)][16 * q + j])[a & 1] = w;
     }
-    // -W^T [d][i]
+    // The same values in the 16x16x16 A layout for the chain: lane (g, r) of
+    // L_bb's A operand holds row r, columns 4g .. 4g+3 of block b, i.e. what
+    // lane (b, r) holds in its words for q = g: a transpose of (row, q).
+    row_transpose4(w01);
+    row_transpose4(w23);
+    // L_aa in the accumulator layout (A layout of L times I) and M_ab in the
+    // A layout (accumulator of M_ab read as an A operand is M_ab^T; times I
+    // gives M_ab^T in the accumulator layout = M_ab in the A layout).  The
+    // transposes are exact: bf16 values times 1.
+    s4_t LA[4], LB[3], MA[6];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-        *reinterpret_cast<u32x2_t *>(&sm.Wt[16 * wave + r][16 * a + 4 * g]) = bf4u(-Wx[a]);
-    lds_barrier();
+    for (int b = 0; b < 4; ++b) {
+        u32x2_t w;
+        w[0] = w01[b];
+        w[1] = w23[b];
+        LA[b] = __builtin_bit_cast(s4_t, w);
+    }
+#pragma unroll
+    for (int b = 0; b < 3; ++b) LB[b] = bf4(mfma16(LA[b], I4, zero4()));
+#pragma unroll
+    for (int i = 0; i < 6; ++i) MA[i] = bf4(mfma16(bf4(MC[i]), I4, zero4()));
+    auto fin = [&](int a2, const f32x4_t &y) { return -mfma16(LA[a2], bf4(y), y); };
+    f32x4_t y;
+    y = mfma16(MA[0], LB[0], MC[0]);
+    const f32x4_t T10 = fin(1, y);
+    y = mfma16(MA[1], LB[1], MC[1]);
+    const f32x4_t T21 = fin(2, y);
+    y = mfma16(MA[2], LB[2], MC[2]);
+    const f32x4_t T32 = fin(3, y);
+    y = mfma16(MA[3], LB[0], MC[3]);
+    y = mfma16(MA[1], bf4(T10), y);
+    const f32x4_t T20 = fin(2, y);
+    y = mfma16(MA[4], LB[1], MC[4]);
+    y = mfma16(MA[2], bf4(T21), y);
+    const f32x4_t T31 = fin(3, y);
+    y = mfma16(MA[5], LB[0], MC[5]);
+    y = mfma16(MA[4], bf4(T10), y);
+    y = mfma16(MA[2], bf4(T20), y);
+    const f32x4_t T30 = fin(3, y);
+    // block (a2, b) into its fragment half (A layout, by the same transpose):
+    // one 8-byte store
+    auto put = [&](int a2, int b, const f32x4_t &x) {
+        const f32x4_t xa = mfma16(bf4(x), I4, zero4());
+        reinterpret_cast<u32x2_t *>(&Tf[fidx(a2, b >> 1)][lane])[b & 1] = bf4u(xa);
+    };
+    put(1, 0, T10);
+    put(2, 0, T20);
+    put(2, 1, T21);
+    put(3, 0, T30);
+    put(3, 1, T31);
+    put(3, 2, T32);
 }
 
 // ---------------------------------------------------------------------------
@@ -546,7 +668,7 @@ GDN_DEV const float *carry_slot(const float *carry, int b, int h, int Hv, int P,
 constexpr int kSst = 0, kPhi = 1, kCst = 2;
 
 // ---------------------------------------------------------------------------
-// Segment kernels
+// Segment loops
 // ---------------------------------------------------------------------------
 
 struct SegArgs {
@@ -559,180 +681,360 @@ struct SegArgs {
     float q_scale;
 };
 
-// The recurrence with output over chunks [n0, n1) of one (b, h), from the
-// state `S` in registers (wave w owns columns 16w .. 16w+15).
-GDN_DEV void run_output_segment(Smem &sm, f32x4_t (&S)[8][1], const SegArgs &a, int b, int h,
-                                int n0, int n1) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Ring slots of chunk n in a segment starting at n0.
+GDN_DEV int kslot(int n, int n0) { return (n - n0) % 3; }
+GDN_DEV int pslot(int n, int n0) { return (n - n0) & 1; }
+
+// Zero the two upper blocks of the fragment layouts (constant).
+GDN_DEV void zero_upper_halves(Smem &sm, int tid) {
+    if (tid < 64 * 8) {
+        const int which = tid >> 6, lane = tid & 63;
+        u32x4_t(*f)[64] = which < 4 ? sm.Tf[which >> 1] : sm.Af[(which - 4) >> 1];
+        const int frag = (which & 1) ? fidx(2, 1) : fidx(0, 0);
+        reinterpret_cast<u32x2_t *>(&f[frag][lane])[1] = u32x2_t{0u, 0u};
+    }
+}
+
+// Helper waves (hw = wave - 4) of a segment over chunks [n0, n1).  WITH_Q:
+// output segment (q rows, K Q^T and the A fragments).  The barrier sequence
+// matches state_loop's.
+template <bool WITH_Q>
+GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n1, int hw, int lane) {
     const int g = lane >> 4, r = lane & 15;
     const int kh = h / (a.Hv / a.Hk);
-    const int c0 = 16 * wave;
-    const LoadPlan lp = load_plan(a.Hv, a.Hk, tid);
-    load_chunk<true>(sm, 0, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
-    wait_vmem();
+    const int NC = a.NC;
+    const LoadOffs lfull = load_offs(a.Hk, a.Hv, C, hw, lane);
+    // direct loads of chunk ci's k (and q) rows and of its v rows
+    auto load_kq = [&](uint16_t *tile, const uint16_t *x, int ci) {
+        const int valid = min(C, a.T - ci * C);
+        const uint16_t *rows = chunk_rows(x, a.Hk, kh, b, ci, a.T);
+        if (valid == C) load_rows(tile, rows, lfull.kq, hw);
+        else load_rows(tile, rows, load_offs(a.Hk, a.Hv, valid, hw, lane).kq, hw);
+    };
+    auto load_v = [&](uint16_t *tile, int ci) {
+        const int valid = min(C, a.T - ci * C);
+        const uint16_t *rows = chunk_rows(a.v, a.Hv, h, b, ci, a.T);
+        if (valid == C) load_rows(tile, rows, lfull.v, hw);
+        else load_rows(tile, rows, load_offs(a.Hk, a.Hv, valid, hw, lane).v, hw);
+    };
+    auto loads_start = [&](int n) {  // k, gates of chunk n+2 and v of chunk n+1
+        const int c2 = min(n + 2, NC - 1), c1 = min(n + 1, NC - 1);
+        load_kq(sm.Kb[kslot(n + 2, n0)], a.k, c2);
+        load_gates(sm, pslot(n + 2, n0), a.g, a.beta, b, h, a.Hv, c2, a.T, hw, lane);
+        load_v(sm.Vb[pslot(n + 1, n0)], c1);
+    };
+    // phase 1 of the chunk before c: gates (helper 0 also stores them for the
+    // state waves) and M of chunk c on helpers 0 and 1 (K K^T rows {0, 3} and
+    // {1, 2})
+    auto kk_step = [&](int c) {
+        if (hw >= 2) return;
+        const int ps = pslot(c, n0);
+        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, hw == 0);
+        const float *G2 = sm.hg[hw][0], *Bt = sm.hg[hw][1];
+        const uint16_t *K = sm.Kb[kslot(c, n0)];
+        if (hw == 0) gram_rows<0, 3, true, false>(sm, sm.Af[ps], K, K, G2, Bt, a.q_scale, lane, g, r);
+        else gram_rows<1, 2, true, false>(sm, sm.Af[ps], K, K, G2, Bt, a.q_scale, lane, g, r);
+    };
+    // phase 2 of the chunk before c: T of chunk c (helper 0) and its A
+    // fragments (helpers 2 and 3: K Q^T rows {0, 3} and {1, 2})
+    auto t_step = [&](int c) {
+        const int ps = pslot(c, n0);
+        if (hw == 0) {
+            build_t(sm, sm.Tf[ps], lane);
+        } else if (WITH_Q && hw >= 2) {
+            chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, false);
+            const float *G2 = sm.hg[hw][0], *Bt = sm.hg[hw][1];
+            const uint16_t *K = sm.Kb[kslot(c, n0)];
+            const uint16_t *Q = sm.Qb[ps];
+            if (hw == 2) gram_rows<0, 3, false, true>(sm, sm.Af[ps], K, Q, G2, Bt, a.q_scale, lane, g, r);
+            else gram_rows<1, 2, false, true>(sm, sm.Af[ps], K, Q, G2, Bt, a.q_scale, lane, g, r);
+        }
+    };
+    // prologue: chunk n0 (all tiles) and n0+1 (k, q, gates)
+    {
+        const int c1 = min(n0 + 1, NC - 1);
+        load_kq(sm.Kb[0], a.k, n0);
+        load_v(sm.Vb[0], n0);
+        load_gates(sm, 0, a.g, a.beta, b, h, a.Hv, n0, a.T, hw, lane);
+        load_kq(sm.Kb[1], a.k, c1);
+        load_gates(sm, 1, a.g, a.beta, b, h, a.Hv, c1, a.T, hw, lane);
+        if (WITH_Q) {
+            load_kq(sm.Qb[0], a.q, n0);
+            load_kq(sm.Qb[1], a.q, c1);
+        }
+        wait_vmem0();
+    }
+    lds_barrier();
+    kk_step(n0);
+    lds_barrier();
+    t_step(n0);
     lds_barrier();
     for (int n = n0; n < n1; ++n) {
-        const int buf = (n - n0) & 1;
-        if (n * C + C > a.T) {  // last, partial chunk
-            zero_tail<true>(sm, buf, n, a.T, tid);
-            lds_barrier();
-        }
-        if (n + 1 < n1)  // the next chunk's rows stream into the other buffer
-            load_chunk<true>(sm, buf ^ 1, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
-                             a.Hk, tid);
-        const ChunkView cv = chunk_view(sm, buf);
-        // v starts as U = T diag(beta) V (this wave's columns), o as 0
-        f32x4_t vacc[4][1], oacc[4];
-        stage_a<true, 1, true>(sm, cv, a.q_scale, tid, c0, vacc);
+        loads_start(n);
+        if (n + 1 < n1) kk_step(n + 1);
+        wait_vmem9();   // everything issued before this chunk's loads has landed
+        lds_barrier();  // X
+        if (WITH_Q)     // q of chunk n+2 into the buffer chunk n's q leaves
+            load_kq(sm.Qb[pslot(n + 2, n0)], a.q, min(n + 2, NC - 1));
+        if (n + 1 < n1) t_step(n + 1);
+        // k rows and gates of chunk n+2 (issued at this chunk's start) have
+        // landed: only the q loads may still be in flight
+        if (WITH_Q) wait_vmem4();
+        else wait_vmem0();
+        lds_barrier();  // Y
+    }
+    wait_vmem0();
+}
+
+// State waves of an output segment: columns c0 .. c0 + 31 (two tiles).
+// o^T tiles: lane (g, r) of tile (ct, tt) holds o[t = 16 tt + r][c0 + 16 ct
+// + 4g .. +3], one 8-byte store.
+GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h, int n0,
+                            int n1, int c0, int lane) {
+    const int g = lane >> 4, r = lane & 15;
+    const TileOffs to = tile_offs(g, r);
+    const int voff[2] = {acc_off(c0 / 16, g, r), acc_off(c0 / 16 + 1, g, r)};
+    lds_barrier();  // prologue loads landed
+    lds_barrier();  // chunk n0's gates and M written
+    lds_barrier();  // chunk n0's T and A fragments written
+    for (int n = n0; n < n1; ++n) {
+        const uint16_t *K = sm.Kb[kslot(n, n0)];
+        const uint16_t *Q = sm.Qb[pslot(n, n0)];
+        const uint16_t *V = sm.Vb[pslot(n, n0)];
+        const Gates &gt = sm.gt[pslot(n, n0)];
+        // phase 1: P = K S, O^T = S^T Q^T
+        f32x4_t P[4][2], O[2][4];
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) oacc[rt] = zero4();
-        // v -= W S ;  o = q S
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                P[i][ct] = zero4();
+                O[ct][i] = zero4();
+            }
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
-            const bf16x8_t sb = frag_acc(S[2 * kb][0], S[2 * kb + 1][0]);
+            bf16x8_t sf[2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) sf[ct] = frag_acc(S[2 * kb][ct], S[2 * kb + 1][ct]);
 #pragma unroll
             for (int rt = 0; rt < 4; ++rt) {
-                vacc[rt][0] = mfma_16x16x32_bf16(wfrag(sm.Wt, kb, rt, g, r), sb, vacc[rt][0]);
-                oacc[rt] = mfma_16x16x32_bf16(sfrag_nat(cv.Q, 16 * rt, 32 * kb, g, r), sb, oacc[rt]);
+                const bf16x8_t kf = nat_frag(K, to, rt, kb);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) P[rt][ct] = mfma_16x16x32_bf16(kf, sf[ct], P[rt][ct]);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const bf16x8_t qf = nat_frag(Q, to, tt, kb);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) O[ct][tt] = mfma_16x16x32_bf16(sf[ct], qf, O[ct][tt]);
             }
         }
-        // o = e^G scale (q S) + A v
+        lds_barrier();  // X: T of chunk n is ready
+        // R = beta (V - e^G P)
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
-            const f32x4_t eg = lds_f4(&sm.eG[16 * rt + 4 * g]);
+            const f32x4_t bt = lds_f4(&gt.bt[16 * rt + 4 * g]);
+            const f32x4_t eg = lds_f4(&gt.eg[16 * rt + 4 * g]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) oacc[rt][e] *= a.q_scale * eg[e];
+            for (int ct = 0; ct < 2; ++ct) {
+                const f32x4_t vv = acc_tile(V, voff[ct], rt);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) P[rt][ct][e] = bt[e] * (vv[e] - eg[e] * P[rt][ct][e]);
+            }
         }
+        // v = R + (T - I) R, with R as a hi + lo pair: consecutive rows of R
+        // can nearly cancel in T R (repeated keys), so R keeps 16 bits here
+        {
+            bf16x8_t rh[2][2], rl[2][2];
 #pragma unroll
-        for (int kb = 0; kb < C / 32; ++kb) {
-            const bf16x8_t vb = frag_acc(vacc[2 * kb][0], vacc[2 * kb + 1][0]);
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) frag_acc_split(P[2 * kb][ct], P[2 * kb + 1][ct], rh[kb][ct], rl[kb][ct]);
 #pragma unroll
             for (int rt = 0; rt < 4; ++rt)
-                oacc[rt] = mfma_16x16x32_bf16(afrag(sm.At, kb, rt, g, r), vb, oacc[rt]);
+#pragma unroll
+                for (int kb = 0; kb <= (rt >> 1); ++kb) {
+                    const bf16x8_t tf = frag_ld(sm.Tf[pslot(n, n0)][fidx(rt, kb)][lane]);
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) {
+                        P[rt][ct] = mfma_16x16x32_bf16(tf, rh[kb][ct], P[rt][ct]);
+                        P[rt][ct] = mfma_16x16x32_bf16(tf, rl[kb][ct], P[rt][ct]);
+                    }
+                }
         }
-        // o -> HBM through LDS: each wave writes its columns of o^T (4 rows of
-        // one column per 8-byte write), reads them back transposed (row t,
-        // 8 consecutive columns per lane) and stores 16 B per lane.  Only this
-        // wave touches its columns, so no barrier is needed.
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
-            *reinterpret_cast<u32x2_t *>(&sm.Ot[c0 + r][16 * rt + 4 * g]) = bf4u(oacc[rt]);
+        // o^T = scale e^G O^T + v^T A^T
         {
-            const int t = n * C + 16 * g + r;   // lane (g, r) stores row 16g + r
-            uint16_t *orow = a.o + (((size_t)b * a.T + t) * a.Hv + h) * D + c0;
+            const int ps = pslot(n, n0);
 #pragma unroll
-            for (int qd = 0; qd < 2; ++qd) {
-                const uint16_t *src = &sm.Ot[c0 + 8 * qd + (r >> 2)][16 * g + 4 * (r & 3)];
-                const u32x4_t w = join(lds_tr(src), lds_tr(src + 4 * PC));
-                if (t < a.T) *reinterpret_cast<u32x4_t *>(orow + 8 * qd) = w;
+            for (int tt = 0; tt < 4; ++tt) {
+                const float s = gt.seg[16 * tt + r];
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) O[ct][tt][e] *= s;
+            }
+            bf16x8_t vf[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) vf[kb][ct] = frag_acc(P[2 * kb][ct], P[2 * kb + 1][ct]);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int kb = 0; kb <= (tt >> 1); ++kb) {
+                    const bf16x8_t af = frag_ld(sm.Af[ps][fidx(tt, kb)][lane]);
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) O[ct][tt] = mfma_16x16x32_bf16(vf[kb][ct], af, O[ct][tt]);
+                }
+            const int valid = min(C, a.T - n * C);
+            uint16_t *ob = a.o + (((size_t)b * a.T + (size_t)n * C) * a.Hv + h) * D + c0 + 4 * g;
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const int t = 16 * tt + r;
+                if (t < valid) {
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        *reinterpret_cast<u32x2_t *>(ob + (size_t)t * a.Hv * D + 16 * ct) = bf4u(O[ct][tt]);
+                }
             }
         }
         // S = e^{G_last} S + K^T diag(e^{G_last - G}) v
         {
-            const float gam = sm.eG[C - 1];
-#pragma unroll
-            for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) S[rt][0][e] *= gam;
-#pragma unroll
-            for (int kb = 0; kb < C / 32; ++kb) {
-                const bf16x8_t vg = frag_acc_scaled(vacc[2 * kb][0], vacc[2 * kb + 1][0],
-                                                    lds_f4(&sm.eGl[32 * kb + 4 * g]),
-                                                    lds_f4(&sm.eGl[32 * kb + 16 + 4 * g]));
-#pragma unroll
-                for (int rt = 0; rt < 8; ++rt)
-                    S[rt][0] = mfma_16x16x32_bf16(kfrag_t(cv.K, 32 * kb, rt, g, r), vg, S[rt][0]);
-            }
-        }
-        wait_vmem();      // the next chunk's rows have landed
-        lds_barrier();    // and this chunk's buffer may be refilled
-    }
-}
-
-// Middle segment of pass 1: the recurrence from S = 0 on state columns
-// 0..127 (waves 0..3) and from Phi = I with U = 0 on 128 more columns
-// (waves 4..7), without output.  Wave w owns columns 32 (w & 3) .. +31 of
-// its block.
-GDN_DEV void run_transition_segment(Smem &sm, const SegArgs &a, int b, int h, int p, int n0,
-                                    int n1) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 4, r = lane & 15;
-    const int kh = h / (a.Hv / a.Hk);
-    const LoadPlan lp = load_plan(a.Hv, a.Hk, tid);
-    const bool is_phi = wave >= 4;
-    const int c0 = 32 * (wave & 3);   // column of the S or Phi block
-    f32x4_t X[8][2];
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                X[rt][ct][e] = (is_phi && srow(rt, g, e) == c0 + 16 * ct + r) ? 1.f : 0.f;
-
-    load_chunk<false>(sm, 0, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n0, a.T, a.Hv, a.Hk, tid);
-    wait_vmem();
-    lds_barrier();
-    for (int n = n0; n < n1; ++n) {
-        const int buf = (n - n0) & 1;
-        if (n * C + C > a.T) {
-            zero_tail<false>(sm, buf, n, a.T, tid);
-            lds_barrier();
-        }
-        if (n + 1 < n1)
-            load_chunk<false>(sm, buf ^ 1, lp, a.q, a.k, a.v, a.g, a.beta, b, h, kh, n + 1, a.T, a.Hv,
-                              a.Hk, tid);
-        const ChunkView cv = chunk_view(sm, buf);
-        // v starts as U (state waves) or 0 (transition waves)
-        f32x4_t vacc[4][2];
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) vacc[rt][ct] = zero4();
-        if (is_phi)
-            stage_a<false, 2, false>(sm, cv, a.q_scale, tid, c0, vacc);
-        else
-            stage_a<false, 2, true>(sm, cv, a.q_scale, tid, c0, vacc);
-#pragma unroll
-        for (int kb = 0; kb < D / 32; ++kb) {
-            bf16x8_t xb[2];
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) xb[ct] = frag_acc(X[2 * kb][ct], X[2 * kb + 1][ct]);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                const bf16x8_t aw = wfrag(sm.Wt, kb, rt, g, r);
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) vacc[rt][ct] = mfma_16x16x32_bf16(aw, xb[ct], vacc[rt][ct]);
-            }
-        }
-        {
-            const float gam = sm.eG[C - 1];
+            const float gam = gt.gam;
 #pragma unroll
             for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
                 for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) X[rt][ct][e] *= gam;
+                    for (int e = 0; e < 4; ++e) S[rt][ct][e] *= gam;
 #pragma unroll
-            for (int kb = 0; kb < C / 32; ++kb) {
-                const f32x4_t slo = lds_f4(&sm.eGl[32 * kb + 4 * g]);
-                const f32x4_t shi = lds_f4(&sm.eGl[32 * kb + 16 + 4 * g]);
+            for (int kb = 0; kb < 2; ++kb) {
+                const f32x4_t slo = lds_f4(&gt.egl[32 * kb + 4 * g]);
+                const f32x4_t shi = lds_f4(&gt.egl[32 * kb + 16 + 4 * g]);
                 bf16x8_t vg[2];
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
-                    vg[ct] = frag_acc_scaled(vacc[2 * kb][ct], vacc[2 * kb + 1][ct], slo, shi);
+                for (int ct = 0; ct < 2; ++ct) vg[ct] = frag_acc_scaled(P[2 * kb][ct], P[2 * kb + 1][ct], slo, shi);
 #pragma unroll
                 for (int rt = 0; rt < 8; ++rt) {
-                    const bf16x8_t ak = kfrag_t(cv.K, 32 * kb, rt, g, r);
+                    const bf16x8_t kt = kt_frag(K, to, rt, kb);
 #pragma unroll
-                    for (int ct = 0; ct < 2; ++ct) X[rt][ct] = mfma_16x16x32_bf16(ak, vg[ct], X[rt][ct]);
+                    for (int ct = 0; ct < 2; ++ct) S[rt][ct] = mfma_16x16x32_bf16(kt, vg[ct], S[rt][ct]);
                 }
             }
         }
-        wait_vmem();
-        lds_barrier();
+        lds_barrier();  // Y
     }
-    tiles_store<kF32, 2>(X, carry_slot(a.carry, b, h, a.Hv, a.P, p, is_phi ? kPhi : kCst), c0, g, r);
+}
+
+// State waves of a transition segment: 64 columns of the 256-column state
+// [C | Phi] (waves 0, 1: C from 0 driven by V; waves 2, 3: Phi from I with
+// V = 0), no output.
+GDN_DEV void state_loop_trans(Smem &sm, f32x4_t (&X)[8][4], const SegArgs &a, int n0, int n1, int c0,
+                              bool is_phi, int lane) {
+    const int g = lane >> 4;
+    lds_barrier();
+    lds_barrier();
+    lds_barrier();
+    for (int n = n0; n < n1; ++n) {
+        TileOffs to;
+        {
+            const int ln = opaque_lane(lane);
+            to = tile_offs(ln >> 4, ln & 15);
+        }
+        const uint16_t *K = sm.Kb[kslot(n, n0)];
+        const uint16_t *V = sm.Vb[pslot(n, n0)];
+        const Gates &gt = sm.gt[pslot(n, n0)];
+        f32x4_t P[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) P[i][ct] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            bf16x8_t xf[4];
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) xf[ct] = frag_acc(X[2 * kb][ct], X[2 * kb + 1][ct]);
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const bf16x8_t kf = nat_frag(K, to, rt, kb);
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) P[rt][ct] = mfma_16x16x32_bf16(kf, xf[ct], P[rt][ct]);
+            }
+            // one k-block of bf16 state fragments live at a time (registers)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        lds_barrier();  // X
+        // R = beta (V - e^G P)  (Phi columns: V = 0)
+        int voff[4];
+        {
+            const int ln = opaque_lane(lane);
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) voff[ct] = acc_off(c0 / 16 + ct, ln >> 4, ln & 15);
+        }
+        if (is_phi) {
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const f32x4_t bt = lds_f4(&gt.bt[16 * rt + 4 * g]);
+                const f32x4_t eg = lds_f4(&gt.eg[16 * rt + 4 * g]);
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) P[rt][ct][e] = -bt[e] * eg[e] * P[rt][ct][e];
+            }
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const f32x4_t bt = lds_f4(&gt.bt[16 * rt + 4 * g]);
+                const f32x4_t eg = lds_f4(&gt.eg[16 * rt + 4 * g]);
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                    const f32x4_t vv = acc_tile(V, voff[ct], rt);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) P[rt][ct][e] = bt[e] * (vv[e] - eg[e] * P[rt][ct][e]);
+                }
+            }
+        }
+        // v = R + (T - I) R (R as a hi + lo pair), one column tile at a time
+        // (registers)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            bf16x8_t rh[2], rl[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) frag_acc_split(P[2 * kb][ct], P[2 * kb + 1][ct], rh[kb], rl[kb]);
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                for (int kb = 0; kb <= (rt >> 1); ++kb) {
+                    const bf16x8_t tf = frag_ld(sm.Tf[pslot(n, n0)][fidx(rt, kb)][lane]);
+                    P[rt][ct] = mfma_16x16x32_bf16(tf, rh[kb], P[rt][ct]);
+                    P[rt][ct] = mfma_16x16x32_bf16(tf, rl[kb], P[rt][ct]);
+                }
+        }
+        {
+            const float gam = gt.gam;
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) X[rt][ct][e] *= gam;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const f32x4_t slo = lds_f4(&gt.egl[32 * kb + 4 * g]);
+                const f32x4_t shi = lds_f4(&gt.egl[32 * kb + 16 + 4 * g]);
+                bf16x8_t vg[4];
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) vg[ct] = frag_acc_scaled(P[2 * kb][ct], P[2 * kb + 1][ct], slo, shi);
+#pragma unroll
+                for (int rt = 0; rt < 8; ++rt) {
+                    const bf16x8_t kt = kt_frag(K, to, rt, kb);
+#pragma unroll
+                    for (int ct = 0; ct < 4; ++ct) X[rt][ct] = mfma_16x16x32_bf16(kt, vg[ct], X[rt][ct]);
+                }
+            }
+        }
+        lds_barrier();  // Y
+    }
 }
 
 // Start state of segment p >= 1 of pass 2, composed by the workgroup itself:
@@ -742,9 +1044,9 @@ GDN_DEV void run_transition_segment(Smem &sm, const SegArgs &a, int b, int h, in
 // step q computes; at the start of a step the threads split the staged Phi
 // into bf16 hi and lo halves, so every wave reads MFMA-ready A fragments; the
 // product is hi*hi + hi*lo + lo*hi (near-fp32 accuracy).  Wave w keeps
-// columns 16w .. 16w+15, as the output pass does.  The halves are unpadded
-// [128][128] tiles with the 16-byte piece c of row i in slot c ^ csw(i):
-// the sixteen rows of one state tile land in sixteen different slots.
+// columns 16w .. 16w+15.  The halves are unpadded [128][128] tiles with the
+// 16-byte piece c of row i in slot c ^ csw(i): the sixteen rows of one state
+// tile land in sixteen different slots.
 struct CombSmem {
     float raw[D * D];       // Phi as loaded, row-major fp32
     uint16_t hi[D * D];
@@ -755,7 +1057,7 @@ GDN_DEV int cidx(int row, int col) { return row * D + ((((col >> 3) ^ csw(row)) 
 
 // Direct loads of one 64 KiB Phi: wave w moves kilobytes 8w .. 8w+7.
 GDN_DEV void comb_fetch(CombSmem &sm, const float *phi, int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = wave_id();
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int blk = 8 * wave + j;  // 1 KiB = 256 floats
@@ -766,7 +1068,7 @@ GDN_DEV void comb_fetch(CombSmem &sm, const float *phi, int tid) {
 
 GDN_DEV void combine_prefix(CombSmem &sm, f32x4_t (&S)[8][1], const float *carry, int b, int h,
                             int Hv, int P, int p, int tid) {
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = wave_id();
     const int g = lane >> 4, r = lane & 15;
     const int c0 = 16 * wave;
     tiles_load<kF32, 1>(S, carry_slot(carry, b, h, Hv, P, 1, kSst), c0, g, r);
@@ -774,7 +1076,7 @@ GDN_DEV void combine_prefix(CombSmem &sm, f32x4_t (&S)[8][1], const float *carry
     f32x4_t cn[8][1];
     tiles_load<kF32, 1>(cn, carry_slot(carry, b, h, Hv, P, 1, kCst), c0, g, r);
     comb_fetch(sm, carry_slot(carry, b, h, Hv, P, 1, kPhi), tid);
-    wait_vmem();
+    wait_vmem0();
     lds_barrier();
     for (int q = 1; q < p; ++q) {
 #pragma unroll 4
@@ -814,9 +1116,23 @@ GDN_DEV void combine_prefix(CombSmem &sm, f32x4_t (&S)[8][1], const float *carry
         }
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt) S[rt][0] = acc[rt];
-        wait_vmem();    // the next Phi has landed
+        wait_vmem0();   // the next Phi has landed
         lds_barrier();  // and every wave is done with the halves
     }
+}
+
+// Value head of workgroup column x.  Workgroups go to the 8 XCDs round-robin
+// by linear id, and gridDim.x = Hv, so x % 8 names the XCD: heads are laid
+// out so that each XCD holds Hv/8 consecutive heads, which keeps the value
+// heads of one key head (and their shared k and q rows) in one L2.
+GDN_DEV int head_of(int x, int Hv) { return (Hv % 8 == 0) ? (Hv / 8) * (x % 8) + x / 8 : x; }
+
+// Output segment over chunks [n0, n1) from S (state waves' registers).
+GDN_DEV void run_output(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h, int n0, int n1) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    zero_upper_halves(sm, tid);
+    if (wave < NSW) state_loop_out(sm, S, a, b, h, n0, n1, 32 * wave, lane);
+    else helper_loop<true>(sm, a, b, h, n0, n1, wave - NSW, lane);
 }
 
 // Pass 1: slot p = blockIdx.y < P-1.  Segment 0 runs the output recurrence
@@ -825,43 +1141,70 @@ template <int IN_FMT, int OUT_FMT>
 __global__ __launch_bounds__(NT) void prefill_pass1_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
-    const int h = blockIdx.x, p = blockIdx.y, b = blockIdx.z;
+    const int h = head_of(blockIdx.x, a.Hv), p = blockIdx.y, b = blockIdx.z;
     const int n0 = p * a.L, n1 = min(a.NC, n0 + a.L);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int g = lane >> 4, r = lane & 15;
     if (p == 0) {
-        f32x4_t S[8][1];
-        void *Sg = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (IN_FMT == kF16 ? 2 : 4);
-        tiles_load<IN_FMT, 1>(S, Sg, 16 * wave, g, r);
-        run_output_segment(sm, S, a, b, h, n0, n1);
-        if (a.P == 1) {
-            void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
-            tiles_store<OUT_FMT, 1>(S, So, 16 * wave, g, r);
-        } else {
-            tiles_store<kF32, 1>(S, carry_slot(a.carry, b, h, a.Hv, a.P, 1, kSst), 16 * wave, g, r);
+        f32x4_t S[8][2];
+        const void *Sg = static_cast<const char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (IN_FMT == kF16 ? 2 : 4);
+        if (wave < NSW) tiles_load<IN_FMT, 2>(S, Sg, 32 * wave, g, r);
+        run_output(sm, S, a, b, h, n0, n1);
+        if (wave < NSW) {
+            if (a.P == 1) {
+                void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
+                tiles_store<OUT_FMT, 2>(S, So, 32 * wave, g, r);
+            } else {
+                tiles_store<kF32, 2>(S, carry_slot(a.carry, b, h, a.Hv, a.P, 1, kSst), 32 * wave, g, r);
+            }
         }
     } else {
-        run_transition_segment(sm, a, b, h, p, n0, n1);
+        zero_upper_halves(sm, tid);
+        if (wave < NSW) {
+            const bool is_phi = wave >= 2;
+            const int c0 = 64 * (wave & 1);
+            f32x4_t X[8][4];
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        X[rt][ct][e] = (is_phi && srow(rt, g, e) == c0 + 16 * ct + r) ? 1.f : 0.f;
+            state_loop_trans(sm, X, a, n0, n1, c0, is_phi, lane);
+            tiles_store<kF32, 4>(X, carry_slot(a.carry, b, h, a.Hv, a.P, p, is_phi ? kPhi : kCst), c0, g, r);
+        } else {
+            helper_loop<false>(sm, a, b, h, n0, n1, wave - NSW, lane);
+        }
     }
 }
 
 // Pass 2: slot blockIdx.y -> segment p = blockIdx.y + 1, from S_start(p),
-// which the workgroup first composes from the pass-1 results.
+// which the workgroup first composes from the pass-1 results (all eight
+// waves, 16 columns each) and hands to the state waves through LDS.
 template <int OUT_FMT>
 __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
-    const int h = blockIdx.x, p = blockIdx.y + 1, b = blockIdx.z;
+    const int h = head_of(blockIdx.x, a.Hv), p = blockIdx.y + 1, b = blockIdx.z;
     const int n0 = p * a.L, n1 = min(a.NC, n0 + a.L);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int g = lane >> 4, r = lane & 15;
-    f32x4_t S[8][1];
-    combine_prefix(*reinterpret_cast<CombSmem *>(smem_raw), S, a.carry, b, h, a.Hv, a.P, p,
-                   threadIdx.x);
-    run_output_segment(sm, S, a, b, h, n0, n1);
-    if (p == a.P - 1) {
+    f32x4_t S[8][2];
+    {
+        f32x4_t S16[8][1];
+        combine_prefix(*reinterpret_cast<CombSmem *>(smem_raw), S16, a.carry, b, h, a.Hv, a.P, p, tid);
+        float *Sl = reinterpret_cast<float *>(smem_raw);  // [128][128] fp32 hand-off
+        lds_barrier();
+        tiles_store<kF32, 1>(S16, Sl, 16 * wave, g, r);
+        lds_barrier();
+        if (wave < NSW) tiles_load<kF32, 2>(S, Sl, 32 * wave, g, r);
+        lds_barrier();
+    }
+    run_output(sm, S, a, b, h, n0, n1);
+    if (wave < NSW && p == a.P - 1) {
         void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
-        tiles_store<OUT_FMT, 1>(S, So, 16 * wave, g, r);
+        tiles_store<OUT_FMT, 2>(S, So, 32 * wave, g, r);
     }
 }
 
@@ -919,6 +1262,7 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
     plan_segments(B, Hv, NC, a.P, a.L);
     if (a.P > 1 && !carry) return hipErrorInvalidValue;
     static_assert(sizeof(CombSmem) <= sizeof(Smem), "the start-state staging reuses the chunk LDS");
+    static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget");
     const size_t smem = sizeof(Smem);
     auto pass1 = narrow_state == kF16 ? prefill_pass1_kernel<kF16, kF16> : prefill_pass1_kernel<kF32, kF32>;
     auto pass2 = narrow_state == kF16 ? prefill_pass2_kernel<kF16> : prefill_pass2_kernel<kF32>;
