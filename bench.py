@@ -15,8 +15,10 @@ The JSON line also carries:
                 launch time from HIP events on the launch stream, vs 8 TB/s
   cpu_baseline  the CPU oracle (oracle/, OpenMP over (sequence, head)) on a
                 bounded sample of the same step, on this host's cores
-  secondary     prefill (config 3, T=16K), conv+SiLU (config 1) and
-                cumulative decay ([4096][8192]) throughput and roofline
+  secondary     prefill (config 3, T=16K), the fp16-state prefill at
+                T in {1K, 8K, 32K, 128K} (config 4: tokens/s and the per-layer
+                state footprint), conv+SiLU (config 1) and cumulative decay
+                ([4096][8192]) throughput and roofline
 Synthetic inputs with the BASELINE distributions; random state.
 """
 from __future__ import annotations
@@ -172,6 +174,62 @@ def bench_prefill(L, ob, torch, timer, reps=5):
             "achieved_tflops": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
 
 
+def device_prefill_inputs(torch, seed, T, Hv, Hk, d=128):
+    """Synthetic prefill inputs with the BASELINE distributions, generated on
+    the GPU (the long-sequence lines would take minutes on the host): q, k
+    L2-normalised N(0,1) and v ~ N(0,1), as bf16 bit patterns in int16
+    tensors; g = -softplus(N(0,1)) exp(U(-2,0)), beta = sigmoid(N(0,1)),
+    S ~ N(0, 0.02), fp32."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    F = torch.nn.functional
+
+    def nrm(*shape):
+        return torch.randn(*shape, generator=gen, device="cuda")
+
+    q = F.normalize(nrm(1, T, Hk, d), dim=-1).to(torch.bfloat16).view(torch.int16)
+    k = F.normalize(nrm(1, T, Hk, d), dim=-1).to(torch.bfloat16).view(torch.int16)
+    v = nrm(1, T, Hv, d).to(torch.bfloat16).view(torch.int16)
+    beta = torch.sigmoid(nrm(1, T, Hv))
+    g = -F.softplus(nrm(1, T, Hv)) * torch.exp(
+        torch.rand(1, T, Hv, generator=gen, device="cuda") * 2.0 - 2.0)
+    S = 0.02 * nrm(1, Hv, d, d)
+    return q, k, v, g.contiguous(), beta.contiguous(), S
+
+
+def bench_prefill_f16_state(L, ob, torch, timer, lengths=(1024, 8192, 32768, 131072)):
+    """Config 4: the chunked prefill with an fp16 recurrent state (fp32
+    accumulation) at growing T; the state a layer keeps between calls is
+    Hv x 128 x 128 fp16 whatever T is."""
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    fn = L.kai_run_gdn_chunk_delta_rule_bf16_f16state_hip
+    rows = []
+    for T in lengths:
+        q, k, v, g, beta, S = device_prefill_inputs(torch, 40 + T // 1024, T, HV, HK)
+        S16 = S.half().view(torch.int16)
+        o = torch.empty((1, T, HV, 128), dtype=torch.int16, device="cuda")
+
+        def run():
+            rc = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                    o.data_ptr(), S16.data_ptr(), 1, T, HV, HK, 1 / math.sqrt(128), stream)
+            if rc:
+                ob.check(rc, "prefill fp16 state")
+
+        run()
+        reps = max(2, min(20, (1 << 17) // T * 2))
+        ms = timer.time_ms(run, reps)
+        flop = PF_FLOP_PER_CHUNK_HEAD * ((T + 63) // 64) * HV
+        rows.append({"T": T, "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                     "achieved_tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+                     "state_bytes_per_layer": HV * 128 * 128 * 2})
+        del q, k, v, g, beta, S, S16, o
+    return {"workload": "chunked WY prefill with fp16 state (fp32 accumulate), B=1 Hv=32 Hk=16 "
+                        "d=128, bf16 q/k/v (BASELINE configs[3])",
+            "state_bytes_per_layer": HV * 128 * 128 * 2,
+            "state_bytes_per_layer_fp32_state": HV * 128 * 128 * 4,
+            "lengths": rows}
+
+
 def cpu_prefill_baseline(budget_s=10.0):
     from oracle import oracle as orc
     from tests.gdn_inputs import prefill_inputs
@@ -251,6 +309,8 @@ def run_profile(which, L, ob, torch, timer, steps, warmup):
         log(f"decode: {ms:.4f} ms/step, {kern * 1e3:.2f} us/launch")
     elif which == "prefill":
         log(f"prefill: {bench_prefill(L, ob, torch, timer, reps=steps)}")
+    elif which == "prefill_f16":
+        log(f"prefill fp16 state: {bench_prefill_f16_state(L, ob, torch, timer)}")
     else:
         conv, decay = bench_stream(L, ob, torch, timer, reps=steps)
         log(f"{which}: {conv if which == 'conv' else decay}")
@@ -269,7 +329,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip prefill/conv/decay lines")
-    ap.add_argument("--profile", choices=["decode", "prefill", "conv", "cumdecay"],
+    ap.add_argument("--profile", choices=["decode", "prefill", "prefill_f16", "conv", "cumdecay"],
                     help="run only this workload (and a 256 MiB device copy that calibrates "
                          "HBM byte counters) for rocprofv3; prints no JSON line")
     args = ap.parse_args()
@@ -300,6 +360,9 @@ def main():
         log("prefill T=16K ...")
         secondary["prefill"] = bench_prefill(L, ob, torch, timer)
         log(f"prefill: {secondary['prefill']}")
+        log("prefill, fp16 state, T = 1K .. 128K ...")
+        secondary["prefill_f16_state"] = bench_prefill_f16_state(L, ob, torch, timer)
+        log(f"prefill fp16 state: {secondary['prefill_f16_state']}")
         log("conv / decay ...")
         secondary["conv"], secondary["cumdecay"] = bench_stream(L, ob, torch, timer)
         log(f"conv: {secondary['conv']}\ncumdecay: {secondary['cumdecay']}")
