@@ -33,19 +33,22 @@
 //    P = K S and O = Q S (phase 1), then v = T diag(beta)(V - e^G P),
 //    o^T = e^G scale O^T + v^T A^T and the state update (phase 2).
 //  - Helper waves 4..7 prepare the S-independent operands one chunk ahead
-//    and stream the chunk tiles: in phase 1 of chunk n one helper builds T
-//    of chunk n (forward substitution of the 16x16 diagonal blocks of M on
-//    the VALU, then the off-diagonal blocks on MFMA); in phase 2 the helpers
-//    form K K^T and K Q^T of chunk n+1 and write M and the A fragments.
+//    and stream the chunk tiles.  While the state waves are in phase 1 of
+//    chunk n, helper 0 finishes T of chunk n (the off-diagonal 16x16 blocks
+//    on MFMA), helpers 1 and 2 form K K^T of chunk n+1 and write M, and
+//    helper 3 forms half of K Q^T of chunk n+1 (the A fragments).  In
+//    phase 2, helper 0 starts T of chunk n+1 (forward substitution of the
+//    diagonal blocks of M on the VALU), helper 1 forms the other half of
+//    K Q^T, and helpers 2 and 3 load tiles.
 //  Two LDS barriers per chunk separate the phases, so the MFMA-heavy state
 //  work of one role overlaps the latency-bound work of the other.
 //
-// Loads: the helpers move chunk tiles straight from HBM into LDS
-// (global_load_lds_dwordx4, 1 KiB per wave instruction): at the start of
-// chunk n the k rows, gates and betas of chunk n+2 and the v rows of n+1,
-// after the first barrier the q rows of chunk n+2.  Every load is issued,
-// with its chunk index clamped to the sequence, so that each helper has the
-// same count in flight and waits with a fixed vmcnt.
+// Loads: helpers 2 and 3 move chunk tiles straight from HBM into LDS
+// (global_load_lds_dwordx4, 1 KiB per wave instruction) in phase 2 of
+// chunk n: the k and q rows, gates and betas of chunk n+2 and the v rows
+// of chunk n+1, and wait for them before the barrier that ends the chunk.
+// Rows past the sequence end read its last row (their values are
+// multiplied by beta = 0 or never stored).
 //
 // Fragment orders.  The 32 k-indices of one 16x16x32 MFMA may be assigned
 // to lanes in any order as long as both operands use the same order.
@@ -222,8 +225,6 @@ GDN_DEV void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier
 
 // vmcnt(n): at most n of this wave's vector memory operations outstanding.
 GDN_DEV void wait_vmem0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-GDN_DEV void wait_vmem9() { __builtin_amdgcn_s_waitcnt(0x0F79); }  // 4 k, 4 v, 1 gate load
-GDN_DEV void wait_vmem4() { __builtin_amdgcn_s_waitcnt(0x0F74); }  // 4 q loads
 
 // ---------------------------------------------------------------------------
 // Shared memory
@@ -271,39 +272,13 @@ struct Smem {
 };
 
 // ---------------------------------------------------------------------------
-// Loads (helper waves hw = 0..3)
+// Loads
 // ---------------------------------------------------------------------------
 
-// Per-lane element offsets of a helper's direct loads: rows 16 hw .. 16 hw
-// + 15 of a chunk, 4 rows per instruction (lane L of instruction j takes row
-// i = 16 hw + 4 j + L/16 and LDS slot L%16, i.e. piece (L%16) ^ fsw(i) of
-// the row in HBM).  Rows at or past `valid` read row valid - 1 (their values
-// are multiplied by beta = 0 or never stored).
-struct LoadOffs {
-    int kq[4], v[4];  // k and q rows (stride Hk * 128), v rows (stride Hv * 128)
-};
-GDN_DEV LoadOffs load_offs(int Hk, int Hv, int valid, int hw, int lane) {
-    LoadOffs o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = 16 * hw + 4 * j + (lane >> 4);
-        const int c = (lane & 15) ^ fsw(i);
-        const int ii = min(i, valid - 1);
-        o.kq[j] = ii * Hk * D + 8 * c;
-        o.v[j] = ii * Hv * D + 8 * c;
-    }
-    return o;
-}
 // Row 0 of chunk ci of head `head` of a [B][T][H][128] tensor.
 GDN_DEV const uint16_t *chunk_rows(const uint16_t *x, int H, int head, int b, int ci, int T) {
     return x + (((size_t)b * T + (size_t)ci * C) * H + head) * D;
 }
-GDN_DEV void load_rows(uint16_t *tile, const uint16_t *rows, const int (&off)[4], int hw) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(rows + off[j], (lds_void_t *)&tile[(16 * hw + 4 * j) * D], 16, 0, 0);
-}
-
 // Log-gates (helpers 0, 1) or betas (2, 3), 32 tokens each.
 GDN_DEV void load_gates(Smem &sm, int slot, const float *g, const float *beta, int b, int h, int Hv,
                         int ci, int T, int hw, int lane) {
@@ -313,6 +288,33 @@ GDN_DEV void load_gates(Smem &sm, int slot, const float *g, const float *beta, i
         const float *src = (hw < 2 ? g : beta) + ((size_t)b * T + tc) * Hv + h;
         float *dst = (hw < 2 ? sm.graw[slot] : sm.braw[slot]) + 32 * (hw & 1);
         __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 4, 0, 0);
+    }
+}
+
+// All 64 log-gates (which = 0) or betas (which = 1) of chunk ci: one
+// instruction.
+GDN_DEV void load_gates_all(Smem &sm, int slot, const float *x, int b, int h, int Hv, int ci, int T,
+                            int which, int lane) {
+    const int tc = min(ci * C + lane, T - 1);
+    __builtin_amdgcn_global_load_lds(x + ((size_t)b * T + tc) * Hv + h,
+                                     (lds_void_t *)(which == 0 ? sm.graw[slot] : sm.braw[slot]), 4, 0, 0);
+}
+
+// Rows r0 .. r0 + 4 NJ - 1 of chunk ci of one head of a [B][T][H][128]
+// tensor into its swizzled LDS tile (NJ instructions; offsets computed here:
+// the wave that issues these loads has the time).
+template <int NJ>
+GDN_DEV void load_rows_n(uint16_t *tile, const uint16_t *x, int H, int head, int b, int ci, int T, int r0,
+                         int lane) {
+    const int valid = min(C, T - ci * C);
+    const uint16_t *rows = chunk_rows(x, H, head, b, ci, T);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int i = r0 + 4 * j + (lane >> 4);
+        const int c = (lane & 15) ^ fsw(i);
+        const int ii = min(i, valid - 1);
+        __builtin_amdgcn_global_load_lds(rows + (size_t)ii * H * D + 8 * c,
+                                         (lds_void_t *)&tile[(r0 + 4 * j) * D], 16, 0, 0);
     }
 }
 
@@ -495,14 +497,23 @@ GDN_DEV void gram_rows(Smem &sm, u32x4_t (&af)[6][64], const uint16_t *K, const 
     }
 }
 
-// T = (I + M)^-1 of the chunk whose M is in Mb, as (T - I) fragments in Tf.
-//  1. Diagonal blocks by substitution in fp32 on the VALU (the row
+// T = (I + M)^-1 of a chunk whose M is in Mb, as (T - I) fragments in Tf,
+// in two steps one phase apart (one helper wave, its values kept in
+// registers in between):
+//  t_subst: the diagonal blocks by substitution in fp32 on the VALU (the row
 //     recurrence of HF, modeling_qwen3_5.py:294-297, on each 16x16 block,
-//     solved for the rows of T_aa): lane (a, j) computes row j of T_aa.
-//  2. Off-diagonal blocks T_ab = -T_aa sum_{c=b}^{a-1} M_ac T_cb on bf16
-//     MFMA, with T_aa = I + L_aa so that the identity parts stay exact:
-//     Y = M_ab + M_ab L_bb + sum_{c>b} M_ac T_cb,  T_ab = -(Y + L_aa Y).
-// Step K of the row substitution in build_t: x[K] is final, then
+//     solved for the rows of T_aa): lane (a, j) computes row j of T_aa; the
+//     rows go to the diagonal fragment halves, and the step keeps them and
+//     the accumulator tiles of the off-diagonal M blocks in registers;
+//  t_chain: the off-diagonal blocks T_ab = -T_aa sum_{c=b}^{a-1} M_ac T_cb
+//     on bf16 MFMA, with T_aa = I + L_aa so that the identity parts stay
+//     exact: Y = M_ab + M_ab L_bb + sum_{c>b} M_ac T_cb,  T_ab = -(Y + L_aa Y).
+struct TRegs {
+    uint32_t w01[4], w23[4];  // bf16 pairs of L = T_aa - I: row j, columns 4q .. 4q+3
+    f32x4_t MC[6];            // accumulator tiles of M_ab: (1,0) (2,1) (3,2) (2,0) (3,1) (3,0)
+};
+
+// Step K of the row substitution in t_subst: x[K] is final, then
 // acc[i] += x[K] M[K][i] for i < K, M[K][i] broadcast from lane i of the row.
 template <int K, int... Is>
 GDN_DEV void subst_update(float (&acc)[16], float xk, float mk, std::integer_sequence<int, Is...>) {
@@ -517,34 +528,22 @@ GDN_DEV void back_subst_step(float (&acc)[16], float (&x)[16], const f32x4_t (&m
     }
 }
 
-GDN_DEV void build_t(Smem &sm, u32x4_t (&Tf)[6][64], int lane) {
+GDN_DEV void t_subst(Smem &sm, u32x4_t (&Tf)[6][64], TRegs &tr, int lane) {
     const int g = lane >> 4, r = lane & 15;
-    // One LDS round trip for every input: lane (a, j) reads column j of M_aa
-    // (for the substitution), every lane the accumulator tiles of the six
-    // off-diagonal blocks.  MC index: (1,0) 0, (2,1) 1, (3,2) 2, (2,0) 3,
-    // (3,1) 4, (3,0) 5.
+    // one LDS round trip for every input: lane (a, j) reads column j of M_aa,
+    // every lane the accumulator tiles of the six off-diagonal blocks
     const int a = lane >> 4, j = lane & 15;
     f32x4_t mcol[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) mcol[q] = lds_f4(&sm.Mb[mbi(a, a)][16 * j + 4 * q]);
     constexpr int off_a[6] = {1, 2, 3, 2, 3, 3}, off_b[6] = {0, 1, 2, 0, 1, 0};
-    f32x4_t MC[6];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) MC[i] = lds_f4(&sm.Mb[mbi(off_a[i], off_b[i])][16 * r + 4 * g]);
-    // identity, accumulator layout (bf16): transposes by one MFMA
-    s4_t I4;
-    {
-        f32x4_t id;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) id[e] = (4 * g + e == r) ? 1.f : 0.f;
-        I4 = bf4(id);
-    }
+    for (int i = 0; i < 6; ++i) tr.MC[i] = lds_f4(&sm.Mb[mbi(off_a[i], off_b[i])][16 * r + 4 * g]);
     // Lane (a, j) computes row j of T_aa from T (I + M) = I:
     // T[j][i] = delta_ji - sum_{k>i} T[j][k] M[k][i], for i = 15 down to 0,
     // right-looking: once x[k] = T[j][k] is final, row k of M updates every
     // earlier column.  M[k][i] is element k of lane (a, i)'s column,
     // broadcast within the 16-lane row of block a (DPP row_newbcast).
-    uint32_t w01[4], w23[4];  // bf16 pairs of L = T_aa - I: row j, columns 4q .. 4q+3
     {
         float acc[16], x[16];
 #pragma unroll
@@ -553,8 +552,8 @@ GDN_DEV void build_t(Smem &sm, u32x4_t (&Tf)[6][64], int lane) {
         // x[j] is exactly 1 (x[k] = 0 for k > j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            w01[q] = pack2_bf16_hw(4 * q == j ? 0.f : x[4 * q], 4 * q + 1 == j ? 0.f : x[4 * q + 1]);
-            w23[q] = pack2_bf16_hw(4 * q + 2 == j ? 0.f : x[4 * q + 2], 4 * q + 3 == j ? 0.f : x[4 * q + 3]);
+            tr.w01[q] = pack2_bf16_hw(4 * q == j ? 0.f : x[4 * q], 4 * q + 1 == j ? 0.f : x[4 * q + 1]);
+            tr.w23[q] = pack2_bf16_hw(4 * q + 2 == j ? 0.f : x[4 * q + 2], 4 * q + 3 == j ? 0.f : x[4 * q + 3]);
         }
     }
     // the diagonal fragment halves for the state waves: row j, columns
@@ -563,16 +562,28 @@ GDN_DEV void build_t(Smem &sm, u32x4_t (&Tf)[6][64], int lane) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         u32x2_t w;
-        w[0] = w01[q];
-        w[1] = w23[q];
+        w[0] = tr.w01[q];
+        w[1] = tr.w23[q];
         reinterpret_cast<u32x2_t *>(&Tf[fidx(a, a >> 1)][16 * q + j])[a & 1] = w;
     }
-    // The same values in the 16x16x16 A layout for the chain: lane (g, r) of
-    // L_bb's A operand holds row r, columns 4g .. 4g+3 of block b, i.e. what
-    // lane (b, r) holds in its words for q = g: a transpose of (row, q).
-    row_transpose4(w01);
-    row_transpose4(w23);
-    // L_aa in the accumulator layout (A layout of L times I) and M_ab in the
+}
+
+GDN_DEV void t_chain(u32x4_t (&Tf)[6][64], TRegs &tr, int lane) {
+    const int g = lane >> 4, r = lane & 15;
+    // identity, accumulator layout (bf16): transposes by one MFMA
+    s4_t I4;
+    {
+        f32x4_t id;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) id[e] = (4 * g + e == r) ? 1.f : 0.f;
+        I4 = bf4(id);
+    }
+    // L_bb in the 16x16x16 A layout: lane (g, r) holds row r, columns
+    // 4g .. 4g+3 of block b, i.e. what lane (b, r) holds in its words for
+    // q = g: a transpose of (16-lane row, q).
+    row_transpose4(tr.w01);
+    row_transpose4(tr.w23);
+    // L_bb in the accumulator layout (A layout of L times I) and M_ab in the
     // A layout (accumulator of M_ab read as an A operand is M_ab^T; times I
     // gives M_ab^T in the accumulator layout = M_ab in the A layout).  The
     // transposes are exact: bf16 values times 1.
@@ -580,14 +591,15 @@ GDN_DEV void build_t(Smem &sm, u32x4_t (&Tf)[6][64], int lane) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         u32x2_t w;
-        w[0] = w01[b];
-        w[1] = w23[b];
+        w[0] = tr.w01[b];
+        w[1] = tr.w23[b];
         LA[b] = __builtin_bit_cast(s4_t, w);
     }
 #pragma unroll
     for (int b = 0; b < 3; ++b) LB[b] = bf4(mfma16(LA[b], I4, zero4()));
 #pragma unroll
-    for (int i = 0; i < 6; ++i) MA[i] = bf4(mfma16(bf4(MC[i]), I4, zero4()));
+    for (int i = 0; i < 6; ++i) MA[i] = bf4(mfma16(bf4(tr.MC[i]), I4, zero4()));
+    const f32x4_t (&MC)[6] = tr.MC;
     auto fin = [&](int a2, const f32x4_t &y) { return -mfma16(LA[a2], bf4(y), y); };
     f32x4_t y;
     y = mfma16(MA[0], LB[0], MC[0]);
@@ -698,89 +710,88 @@ GDN_DEV void zero_upper_halves(Smem &sm, int tid) {
 // Helper waves (hw = wave - 4) of a segment over chunks [n0, n1).  WITH_Q:
 // output segment (q rows, K Q^T and the A fragments).  The barrier sequence
 // matches state_loop's.
+// Helper waves (hw = wave - 4) of a segment over chunks [n0, n1).  WITH_Q:
+// output segment (q rows, K Q^T and the A fragments).  The barrier sequence
+// matches the state loops'.  In iteration n (the state waves on chunk n):
+//   phase 1: hw0 finishes T of chunk n (t_chain); hw1, hw2 form M of chunk
+//            n+1 (K K^T rows {0, 3} and {1, 2}, gates: hw1 stores them for
+//            the state waves); hw3 the A fragments of rows {0, 3} of n+1;
+//   phase 2: hw0 starts T of chunk n+1 (t_subst); hw1 the A fragments of
+//            rows {1, 2}; hw2 and hw3 load the k, q rows and gates of chunk
+//            n+2 and the v rows of chunk n+1, and wait for them.
 template <bool WITH_Q>
 GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n1, int hw, int lane) {
     const int g = lane >> 4, r = lane & 15;
     const int kh = h / (a.Hv / a.Hk);
     const int NC = a.NC;
-    const LoadOffs lfull = load_offs(a.Hk, a.Hv, C, hw, lane);
-    // direct loads of chunk ci's k (and q) rows and of its v rows
-    auto load_kq = [&](uint16_t *tile, const uint16_t *x, int ci) {
-        const int valid = min(C, a.T - ci * C);
-        const uint16_t *rows = chunk_rows(x, a.Hk, kh, b, ci, a.T);
-        if (valid == C) load_rows(tile, rows, lfull.kq, hw);
-        else load_rows(tile, rows, load_offs(a.Hk, a.Hv, valid, hw, lane).kq, hw);
-    };
-    auto load_v = [&](uint16_t *tile, int ci) {
-        const int valid = min(C, a.T - ci * C);
-        const uint16_t *rows = chunk_rows(a.v, a.Hv, h, b, ci, a.T);
-        if (valid == C) load_rows(tile, rows, lfull.v, hw);
-        else load_rows(tile, rows, load_offs(a.Hk, a.Hv, valid, hw, lane).v, hw);
-    };
-    auto loads_start = [&](int n) {  // k, gates of chunk n+2 and v of chunk n+1
-        const int c2 = min(n + 2, NC - 1), c1 = min(n + 1, NC - 1);
-        load_kq(sm.Kb[kslot(n + 2, n0)], a.k, c2);
-        load_gates(sm, pslot(n + 2, n0), a.g, a.beta, b, h, a.Hv, c2, a.T, hw, lane);
-        load_v(sm.Vb[pslot(n + 1, n0)], c1);
-    };
-    // phase 1 of the chunk before c: gates (helper 0 also stores them for the
-    // state waves) and M of chunk c on helpers 0 and 1 (K K^T rows {0, 3} and
-    // {1, 2})
-    auto kk_step = [&](int c) {
-        if (hw >= 2) return;
+    TRegs tr;
+    auto kk = [&](int c, bool rows03) {
         const int ps = pslot(c, n0);
-        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, hw == 0);
+        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, rows03);
         const float *G2 = sm.hg[hw][0], *Bt = sm.hg[hw][1];
         const uint16_t *K = sm.Kb[kslot(c, n0)];
-        if (hw == 0) gram_rows<0, 3, true, false>(sm, sm.Af[ps], K, K, G2, Bt, a.q_scale, lane, g, r);
+        if (rows03) gram_rows<0, 3, true, false>(sm, sm.Af[ps], K, K, G2, Bt, a.q_scale, lane, g, r);
         else gram_rows<1, 2, true, false>(sm, sm.Af[ps], K, K, G2, Bt, a.q_scale, lane, g, r);
     };
-    // phase 2 of the chunk before c: T of chunk c (helper 0) and its A
-    // fragments (helpers 2 and 3: K Q^T rows {0, 3} and {1, 2})
-    auto t_step = [&](int c) {
+    auto qk = [&](int c, bool rows03) {
         const int ps = pslot(c, n0);
-        if (hw == 0) {
-            build_t(sm, sm.Tf[ps], lane);
-        } else if (WITH_Q && hw >= 2) {
-            chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, false);
-            const float *G2 = sm.hg[hw][0], *Bt = sm.hg[hw][1];
-            const uint16_t *K = sm.Kb[kslot(c, n0)];
-            const uint16_t *Q = sm.Qb[ps];
-            if (hw == 2) gram_rows<0, 3, false, true>(sm, sm.Af[ps], K, Q, G2, Bt, a.q_scale, lane, g, r);
-            else gram_rows<1, 2, false, true>(sm, sm.Af[ps], K, Q, G2, Bt, a.q_scale, lane, g, r);
-        }
+        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, false);
+        const float *G2 = sm.hg[hw][0], *Bt = sm.hg[hw][1];
+        const uint16_t *K = sm.Kb[kslot(c, n0)];
+        const uint16_t *Q = sm.Qb[ps];
+        if (rows03) gram_rows<0, 3, false, true>(sm, sm.Af[ps], K, Q, G2, Bt, a.q_scale, lane, g, r);
+        else gram_rows<1, 2, false, true>(sm, sm.Af[ps], K, Q, G2, Bt, a.q_scale, lane, g, r);
     };
-    // prologue: chunk n0 (all tiles) and n0+1 (k, q, gates)
+    // prologue: chunk n0 (all tiles) and n0+1 (k, q, gates), a quarter of
+    // the rows per helper
     {
         const int c1 = min(n0 + 1, NC - 1);
-        load_kq(sm.Kb[0], a.k, n0);
-        load_v(sm.Vb[0], n0);
+        load_rows_n<4>(sm.Kb[0], a.k, a.Hk, kh, b, n0, a.T, 16 * hw, lane);
+        load_rows_n<4>(sm.Vb[0], a.v, a.Hv, h, b, n0, a.T, 16 * hw, lane);
         load_gates(sm, 0, a.g, a.beta, b, h, a.Hv, n0, a.T, hw, lane);
-        load_kq(sm.Kb[1], a.k, c1);
+        load_rows_n<4>(sm.Kb[1], a.k, a.Hk, kh, b, c1, a.T, 16 * hw, lane);
         load_gates(sm, 1, a.g, a.beta, b, h, a.Hv, c1, a.T, hw, lane);
         if (WITH_Q) {
-            load_kq(sm.Qb[0], a.q, n0);
-            load_kq(sm.Qb[1], a.q, c1);
+            load_rows_n<4>(sm.Qb[0], a.q, a.Hk, kh, b, n0, a.T, 16 * hw, lane);
+            load_rows_n<4>(sm.Qb[1], a.q, a.Hk, kh, b, c1, a.T, 16 * hw, lane);
         }
         wait_vmem0();
     }
     lds_barrier();
-    kk_step(n0);
+    if (hw == 1) kk(n0, true);
+    else if (hw == 2) kk(n0, false);
+    else if (WITH_Q && hw == 3) qk(n0, true);
+    else if (WITH_Q && hw == 0) qk(n0, false);
     lds_barrier();
-    t_step(n0);
+    if (hw == 0) t_subst(sm, sm.Tf[pslot(n0, n0)], tr, lane);
     lds_barrier();
     for (int n = n0; n < n1; ++n) {
-        loads_start(n);
-        if (n + 1 < n1) kk_step(n + 1);
-        wait_vmem9();   // everything issued before this chunk's loads has landed
+        const bool more = n + 1 < n1;
+        if (hw == 0) t_chain(sm.Tf[pslot(n, n0)], tr, lane);
+        else if (more) {
+            if (hw == 1) kk(n + 1, true);
+            else if (hw == 2) kk(n + 1, false);
+            else if (WITH_Q) qk(n + 1, true);
+        }
         lds_barrier();  // X
-        if (WITH_Q)     // q of chunk n+2 into the buffer chunk n's q leaves
-            load_kq(sm.Qb[pslot(n + 2, n0)], a.q, min(n + 2, NC - 1));
-        if (n + 1 < n1) t_step(n + 1);
-        // k rows and gates of chunk n+2 (issued at this chunk's start) have
-        // landed: only the q loads may still be in flight
-        if (WITH_Q) wait_vmem4();
-        else wait_vmem0();
+        if (hw == 0) {
+            if (more) t_subst(sm, sm.Tf[pslot(n + 1, n0)], tr, lane);
+        } else if (hw == 1) {
+            if (WITH_Q && more) qk(n + 1, false);
+        } else {
+            // k (hw2) or q (hw3) rows and gates of chunk n+2, half of the v
+            // rows of chunk n+1 each; landed before the barrier
+            const int c2 = min(n + 2, NC - 1), c1 = min(n + 1, NC - 1);
+            if (hw == 2) {
+                load_rows_n<16>(sm.Kb[kslot(n + 2, n0)], a.k, a.Hk, kh, b, c2, a.T, 0, lane);
+                load_gates_all(sm, pslot(n + 2, n0), a.g, b, h, a.Hv, c2, a.T, 0, lane);
+            } else {
+                if (WITH_Q) load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
+                load_gates_all(sm, pslot(n + 2, n0), a.beta, b, h, a.Hv, c2, a.T, 1, lane);
+            }
+            load_rows_n<8>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 32 * (hw - 2), lane);
+            wait_vmem0();
+        }
         lds_barrier();  // Y
     }
     wait_vmem0();
