@@ -91,6 +91,23 @@ class Timer:
         e.synchronize()
         return s.elapsed_time(e) / reps
 
+    def p50_ms(self, fn, warmup=20, reps=30):
+        """The reference's protocol (bench_kai_gdn.c:55-60,86-95): `warmup`
+        untimed calls, then `reps` calls timed one by one with HIP events,
+        median by nearest rank."""
+        t = self.torch
+        for _ in range(warmup):
+            fn()
+        ev = [t.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        t.cuda.synchronize()
+        for i in range(reps):
+            ev[i].record()
+            fn()
+        ev[reps].record()
+        ev[reps].synchronize()
+        ts = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+        return ts[(reps - 1) // 2]
+
 
 
 def bench_decode(L, ob, torch, steps, warmup, timer):
@@ -165,8 +182,7 @@ def bench_prefill(L, ob, torch, timer, reps=5):
         if rc:
             ob.check(rc, "prefill")
 
-    run()
-    ms = timer.time_ms(run, reps)
+    ms = timer.p50_ms(run, warmup=20, reps=max(reps, 30))
     flop = PF_FLOP_PER_CHUNK_HEAD * (PF_T // 64) * HV
     tflops = flop / (ms * 1e-3) / 1e12
     return {"workload": "chunked WY prefill, B=1 T=16384 Hv=32 Hk=16 d=128 bf16 in, fp32 state",
@@ -215,9 +231,7 @@ def bench_prefill_f16_state(L, ob, torch, timer, lengths=(1024, 8192, 32768, 131
             if rc:
                 ob.check(rc, "prefill fp16 state")
 
-        run()
-        reps = max(2, min(20, (1 << 17) // T * 2))
-        ms = timer.time_ms(run, reps)
+        ms = timer.p50_ms(run, warmup=20, reps=30)
         flop = PF_FLOP_PER_CHUNK_HEAD * ((T + 63) // 64) * HV
         rows.append({"T": T, "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
                      "achieved_tflops": round(flop / (ms * 1e-3) / 1e12, 2),

@@ -63,7 +63,6 @@
 //    rows 32j + 8g + 4u + e (e = 0..3): the state's rows are permuted among
 //    the tiles (srow below), which the products that write the state follow
 //    by reading their A operand rows in the same order.
-#include <utility>
 
 #include "gdn_common.h"
 #include "gdn_internal.h"
@@ -186,21 +185,11 @@ GDN_DEV float wave_incl_scan(float x) {
 // that branches on a wave's role compile to scalar branches.
 GDN_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-// acc += (m in lane I of this lane's 16-lane row) * x: one DPP row_newbcast
-// FMA.  The compiler's update_dpp builtin merges row_newbcast moves of
-// different sources, so the instruction is written out; the s_nop covers
-// the VALU -> DPP read hazard on m.
-template <int I> GDN_DEV void fma_row_bcast(float &acc, float m, float x) {
-    __asm__ volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-                     : "+v"(acc)
-                     : "v"(m), "v"(x), "n"(I));
-}
-
 // 4 x 4 transpose of (16-lane row, register): afterwards x[b] row g holds
 // what x[g] row b held.  v_permlane32_swap exchanges the upper two rows of
 // its first operand with the lower two of its second, v_permlane16_swap the
 // odd rows of the first with the even rows of the second.
-GDN_DEV void row_transpose4(uint32_t (&x)[4]) {
+GDN_DEV void row_transpose4(u32x4_t &x) {
     auto s02 = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false);
     auto s13 = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
     auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
@@ -395,21 +384,25 @@ GDN_DEV bf16x8_t frag_ld(const u32x4_t &p) { return as_bf16x8(p); }
 // and beta go to the helper's own copy hg[hw] (read back by this wave only);
 // with `write` the wave also stores the state waves' per-chunk gates.
 GDN_DEV void chunk_gates(Smem &sm, int slot, int c, int T, float q_scale, int hw, int lane, bool write) {
+    // no fused multiply-adds: every inlined copy (prologue, loop, each
+    // helper) must round the gates identically
+#pragma clang fp contract(off)
     const int valid = min(C, T - c * C);
     const float x = lane < valid ? sm.graw[slot][lane] : 0.f;
     const float bv = lane < valid ? sm.braw[slot][lane] : 0.f;
     const float G = wave_incl_scan(x);
-    const float Gl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), 63));
-    sm.hg[hw][0][lane] = G * kLog2e;
+    const float G2 = G * kLog2e;
+    sm.hg[hw][0][lane] = G2;
     sm.hg[hw][1][lane] = bv;
     if (write) {
         Gates &gt = sm.gt[slot];
-        const float eg = expf(G);
+        const float Gl2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G2), 63));
+        const float eg = __builtin_amdgcn_exp2f(G2);
         gt.bt[lane] = bv;
         gt.eg[lane] = eg;
-        gt.egl[lane] = expf(Gl - G);
+        gt.egl[lane] = __builtin_amdgcn_exp2f(Gl2 - G2);
         gt.seg[lane] = q_scale * eg;
-        if (lane == 0) gt.gam = expf(Gl);
+        if (lane == 0) gt.gam = __builtin_amdgcn_exp2f(Gl2);
     }
     lds_fence();
 }
@@ -509,23 +502,40 @@ GDN_DEV void gram_rows(Smem &sm, u32x4_t (&af)[6][64], const uint16_t *K, const 
 //     on bf16 MFMA, with T_aa = I + L_aa so that the identity parts stay
 //     exact: Y = M_ab + M_ab L_bb + sum_{c>b} M_ac T_cb,  T_ab = -(Y + L_aa Y).
 struct TRegs {
-    uint32_t w01[4], w23[4];  // bf16 pairs of L = T_aa - I: row j, columns 4q .. 4q+3
+    u32x4_t w01, w23;  // bf16 pairs of L = T_aa - I: row j, columns 4q .. 4q+3 (vectors:
+                       // kept in registers across the phases)
     f32x4_t MC[6];            // accumulator tiles of M_ab: (1,0) (2,1) (3,2) (2,0) (3,1) (3,0)
 };
 
-// Step K of the row substitution in t_subst: x[K] is final, then
-// acc[i] += x[K] M[K][i] for i < K, M[K][i] broadcast from lane i of the row.
-template <int K, int... Is>
-GDN_DEV void subst_update(float (&acc)[16], float xk, float mk, std::integer_sequence<int, Is...>) {
-    (fma_row_bcast<K - 1 - Is>(acc[K - 1 - Is], mk, xk), ...);  // next row's term first
-}
-template <int K>
-GDN_DEV void back_subst_step(float (&acc)[16], float (&x)[16], const f32x4_t (&mcol)[4], int j) {
-    x[K] = ((K == j) ? 1.f : 0.f) - acc[K];
-    if constexpr (K > 0) {
-        subst_update<K>(acc, x[K], mcol[K >> 2][K & 3], std::make_integer_sequence<int, K>{});
-        back_subst_step<K - 1>(acc, x, mcol, j);
-    }
+// Row j of T_aa = (I + M_aa)^-1 in lane (a, j), from T (I + M) = I:
+// T[j][i] = delta_ji - sum_{k>i} T[j][k] M[k][i], for i = 15 down to 0,
+// right-looking: once x[k] = T[j][k] is final, row k of M updates every
+// earlier column.  mcol holds column j of M_aa (mcol[q][e] = M[4q+e][j]);
+// M[k][i] is element k of lane (a, i)'s column, broadcast within the 16-lane
+// row of block a (DPP row_newbcast).  Each step is one inline-asm block
+// with a single hazard wait (gdn_subst_steps.inc); acc starts at -delta so
+// that a step's x is one subtraction.
+#include "gdn_subst_steps.inc"
+GDN_DEV void row_subst(float (&x)[16], const f32x4_t (&mcol)[4], int j) {
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = (i == j) ? -1.f : 0.f;
+    subst_step_15(acc, x[15], mcol[3][3]);
+    subst_step_14(acc, x[14], mcol[3][2]);
+    subst_step_13(acc, x[13], mcol[3][1]);
+    subst_step_12(acc, x[12], mcol[3][0]);
+    subst_step_11(acc, x[11], mcol[2][3]);
+    subst_step_10(acc, x[10], mcol[2][2]);
+    subst_step_9(acc, x[9], mcol[2][1]);
+    subst_step_8(acc, x[8], mcol[2][0]);
+    subst_step_7(acc, x[7], mcol[1][3]);
+    subst_step_6(acc, x[6], mcol[1][2]);
+    subst_step_5(acc, x[5], mcol[1][1]);
+    subst_step_4(acc, x[4], mcol[1][0]);
+    subst_step_3(acc, x[3], mcol[0][3]);
+    subst_step_2(acc, x[2], mcol[0][2]);
+    subst_step_1(acc, x[1], mcol[0][1]);
+    x[0] = -acc[0];
 }
 
 GDN_DEV void t_subst(Smem &sm, u32x4_t (&Tf)[6][64], TRegs &tr, int lane) {
@@ -539,16 +549,10 @@ GDN_DEV void t_subst(Smem &sm, u32x4_t (&Tf)[6][64], TRegs &tr, int lane) {
     constexpr int off_a[6] = {1, 2, 3, 2, 3, 3}, off_b[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
     for (int i = 0; i < 6; ++i) tr.MC[i] = lds_f4(&sm.Mb[mbi(off_a[i], off_b[i])][16 * r + 4 * g]);
-    // Lane (a, j) computes row j of T_aa from T (I + M) = I:
-    // T[j][i] = delta_ji - sum_{k>i} T[j][k] M[k][i], for i = 15 down to 0,
-    // right-looking: once x[k] = T[j][k] is final, row k of M updates every
-    // earlier column.  M[k][i] is element k of lane (a, i)'s column,
-    // broadcast within the 16-lane row of block a (DPP row_newbcast).
+    // lane (a, j) computes row j of T_aa
     {
-        float acc[16], x[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-        back_subst_step<15>(acc, x, mcol, j);
+        float x[16];
+        row_subst(x, mcol, j);
         // x[j] is exactly 1 (x[k] = 0 for k > j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -709,16 +713,16 @@ GDN_DEV void zero_upper_halves(Smem &sm, int tid) {
 
 // Helper waves (hw = wave - 4) of a segment over chunks [n0, n1).  WITH_Q:
 // output segment (q rows, K Q^T and the A fragments).  The barrier sequence
-// matches state_loop's.
-// Helper waves (hw = wave - 4) of a segment over chunks [n0, n1).  WITH_Q:
-// output segment (q rows, K Q^T and the A fragments).  The barrier sequence
 // matches the state loops'.  In iteration n (the state waves on chunk n):
 //   phase 1: hw0 finishes T of chunk n (t_chain); hw1, hw2 form M of chunk
 //            n+1 (K K^T rows {0, 3} and {1, 2}, gates: hw1 stores them for
-//            the state waves); hw3 the A fragments of rows {0, 3} of n+1;
-//   phase 2: hw0 starts T of chunk n+1 (t_subst); hw1 the A fragments of
-//            rows {1, 2}; hw2 and hw3 load the k, q rows and gates of chunk
-//            n+2 and the v rows of chunk n+1, and wait for them.
+//            the state waves); hw3 issues the loads of the k rows and gates
+//            of chunk n+2 and the v rows of chunk n+1;
+//   phase 2: hw0 starts T of chunk n+1 (t_subst); hw3 and hw1 form the A
+//            fragments of chunk n+1 (rows {0, 3} and {1, 2}), and hw3 waits
+//            for its loads; hw2 issues the loads of the q rows of chunk n+2,
+//            which it waits for at the end of the next phase 1.
+// Every load thus has at least a whole phase to land.
 template <bool WITH_Q>
 GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n1, int hw, int lane) {
     const int g = lane >> 4, r = lane & 15;
@@ -767,30 +771,30 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
     lds_barrier();
     for (int n = n0; n < n1; ++n) {
         const bool more = n + 1 < n1;
-        if (hw == 0) t_chain(sm.Tf[pslot(n, n0)], tr, lane);
-        else if (more) {
-            if (hw == 1) kk(n + 1, true);
-            else if (hw == 2) kk(n + 1, false);
-            else if (WITH_Q) qk(n + 1, true);
+        const int c2 = min(n + 2, NC - 1), c1 = min(n + 1, NC - 1);
+        if (hw == 0) {
+            __builtin_amdgcn_s_setprio(3);
+            t_chain(sm.Tf[pslot(n, n0)], tr, lane);
+            __builtin_amdgcn_s_setprio(0);
+        } else if (hw == 3) {
+            // into slots whose last readers finished in the previous chunk
+            load_rows_n<16>(sm.Kb[kslot(n + 2, n0)], a.k, a.Hk, kh, b, c2, a.T, 0, lane);
+            load_gates_all(sm, pslot(n + 2, n0), a.g, b, h, a.Hv, c2, a.T, 0, lane);
+            load_gates_all(sm, pslot(n + 2, n0), a.beta, b, h, a.Hv, c2, a.T, 1, lane);
+            load_rows_n<16>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 0, lane);
+        } else if (more) {
+            kk(n + 1, hw == 1);
         }
-        lds_barrier();  // X
+        if (hw == 2) wait_vmem0();  // q rows of chunk n+1
+        lds_barrier();              // X
         if (hw == 0) {
             if (more) t_subst(sm, sm.Tf[pslot(n + 1, n0)], tr, lane);
-        } else if (hw == 1) {
-            if (WITH_Q && more) qk(n + 1, false);
+        } else if (hw == 2) {
+            // into the slot chunk n's q leaves (read in phase 1 only)
+            if (WITH_Q) load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
         } else {
-            // k (hw2) or q (hw3) rows and gates of chunk n+2, half of the v
-            // rows of chunk n+1 each; landed before the barrier
-            const int c2 = min(n + 2, NC - 1), c1 = min(n + 1, NC - 1);
-            if (hw == 2) {
-                load_rows_n<16>(sm.Kb[kslot(n + 2, n0)], a.k, a.Hk, kh, b, c2, a.T, 0, lane);
-                load_gates_all(sm, pslot(n + 2, n0), a.g, b, h, a.Hv, c2, a.T, 0, lane);
-            } else {
-                if (WITH_Q) load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
-                load_gates_all(sm, pslot(n + 2, n0), a.beta, b, h, a.Hv, c2, a.T, 1, lane);
-            }
-            load_rows_n<8>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 32 * (hw - 2), lane);
-            wait_vmem0();
+            if (WITH_Q && more) qk(n + 1, hw == 3);
+            if (hw == 3) wait_vmem0();  // k rows, gates of chunk n+2, v rows of n+1
         }
         lds_barrier();  // Y
     }
@@ -841,6 +845,8 @@ GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int 
             }
         }
         lds_barrier();  // X: T of chunk n is ready
+        // this phase bounds the chunk: its waves issue ahead of the helpers'
+        __builtin_amdgcn_s_setprio(2);
         // R = beta (V - e^G P)
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
@@ -933,6 +939,7 @@ GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int 
                 }
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         lds_barrier();  // Y
     }
 }

@@ -74,3 +74,14 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run(["python", os.path.join(REPO, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_generated_substitution_steps_up_to_date():
+    """gdn_subst_steps.inc is the output of its generator, unedited."""
+    import importlib.util
+    csrc = os.path.join(REPO, "orionsbelt_amd", "csrc")
+    spec = importlib.util.spec_from_file_location("gen_subst_steps", os.path.join(csrc, "gen_subst_steps.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    with open(os.path.join(csrc, "gdn_subst_steps.inc")) as f:
+        assert f.read() == gen.render()
