@@ -132,11 +132,14 @@ def test_prefill_positive_log_gates(L):
 def test_prefill_repeated_keys(L):
     """Degenerate chunks: every token has the same key, beta near 1, little or
     no decay (a repeated token).  M is then nearly the all-ones strictly lower
-    triangle, whose block inverse is built from powers with entries in the
-    thousands that cancel to O(1); rounding them to bf16 blows the result up
-    by many orders of magnitude.  Rank-1 keys also amplify the bf16 rounding
-    of W and v_new, so the bound here is looser than the generic one:
-    max_rel <= 4e-2 and l2_rel <= 3e-2 (measured about 2e-2)."""
+    triangle and T = (I + M)^-1 nearly the alternating bidiagonal I - shift:
+    T R is a difference of consecutive rows of R that almost cancel, so R
+    must enter the T product with more than bf16's 8 bits (the kernel uses a
+    hi + lo pair), and the diagonal blocks of T must be exact enough to
+    cancel (fp32 substitution).  Rank-1 keys also amplify the bf16 rounding
+    of T's off-diagonal blocks and of v_new, so the bound here is looser than
+    the generic one: max_rel <= 4e-2 and l2_rel <= 3e-2 (measured about
+    2e-2)."""
     for beta_v, g_v in [(1.0, 0.0), (0.9, -0.01)]:
         q, k, v, g, beta, S = prefill_inputs(41, 1, 256, 2, 1)
         k[:, :] = k[:, :1]
