@@ -244,6 +244,63 @@ def bench_prefill_f16_state(L, ob, torch, timer, lengths=(1024, 8192, 32768, 131
             "lengths": rows}
 
 
+def bench_layer_glue(L, ob, torch, timer, T=PF_T):
+    """The layer glue at the prefill shape (B=1, T=16384, Hk=16, Hv=32):
+    the gating prologue (conv output fp32 -> q, k, v bf16, g, beta) and the
+    bf16 gated RMSNorm over the T * Hv rows of the recurrence output.  Both
+    are HBM-bound; bytes are each kernel's reads plus writes."""
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(31)
+    H = 2 * HK + HV
+    x = torch.randn(T, H * 128, generator=gen, device="cuda")
+    a = torch.randn(T, HV, generator=gen, device="cuda")
+    b = torch.randn(T, HV, generator=gen, device="cuda")
+    A_log = torch.log(torch.rand(HV, generator=gen, device="cuda") * 15 + 0.5)
+    dt = torch.randn(HV, generator=gen, device="cuda")
+    q = torch.empty(T, HK, 128, dtype=torch.int16, device="cuda")
+    k = torch.empty_like(q)
+    v = torch.empty(T, HV, 128, dtype=torch.int16, device="cuda")
+    g = torch.empty(T, HV, device="cuda")
+    beta = torch.empty_like(g)
+
+    def prologue():
+        rc = L.kai_run_gdn_gating_prologue_bf16_hip(
+            x.data_ptr(), a.data_ptr(), b.data_ptr(), A_log.data_ptr(), dt.data_ptr(),
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), T, HK, HV,
+            stream)
+        if rc:
+            ob.check(rc, "gating prologue")
+
+    ms = timer.p50_ms(prologue, warmup=20, reps=30)
+    pro_bytes = T * H * 128 * 4 + 2 * T * HV * 4 + 2 * HV * 4 + T * H * 128 * 2 + 2 * T * HV * 4
+    pro = {"workload": f"gating prologue, B=1 T={T} Hk={HK} Hv={HV}: fp32 conv output -> "
+                       "L2-normalised q, k and v (bf16), g, beta",
+           "us": round(ms * 1e3, 2), "tokens_per_s": round(T / (ms * 1e-3), 1),
+           "bytes_per_launch": pro_bytes, "achieved_gbs": round(pro_bytes / (ms * 1e-3) / 1e9, 1),
+           "hbm_frac": round(pro_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del x, a, b, q, k, v, g, beta
+    rows = T * HV
+    o = torch.randn(rows, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    z = torch.randn(rows, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(128, generator=gen, device="cuda")).to(torch.bfloat16)
+    y = torch.empty_like(o)
+
+    def norm():
+        rc = L.kai_run_gdn_gated_rmsnorm_bf16_hip(o.data_ptr(), z.data_ptr(), w.data_ptr(),
+                                                  y.data_ptr(), rows, 1e-6, stream)
+        if rc:
+            ob.check(rc, "gated rmsnorm")
+
+    ms = timer.p50_ms(norm, warmup=20, reps=30)
+    rn_bytes = 3 * rows * 128 * 2 + 128 * 2
+    rn = {"workload": f"gated RMSNorm + SiLU(z), bf16, {rows} rows of 128 (B=1 T={T} Hv={HV})",
+          "us": round(ms * 1e3, 2), "tokens_per_s": round(T / (ms * 1e-3), 1),
+          "bytes_per_launch": rn_bytes, "achieved_gbs": round(rn_bytes / (ms * 1e-3) / 1e9, 1),
+          "hbm_frac": round(rn_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return pro, rn
+
+
 def cpu_prefill_baseline(budget_s=10.0):
     from oracle import oracle as orc
     from tests.gdn_inputs import prefill_inputs
@@ -325,6 +382,9 @@ def run_profile(which, L, ob, torch, timer, steps, warmup):
         log(f"prefill: {bench_prefill(L, ob, torch, timer, reps=steps)}")
     elif which == "prefill_f16":
         log(f"prefill fp16 state: {bench_prefill_f16_state(L, ob, torch, timer)}")
+    elif which == "layer":
+        pro, rn = bench_layer_glue(L, ob, torch, timer)
+        log(f"gating prologue: {pro}\ngated rmsnorm: {rn}")
     else:
         conv, decay = bench_stream(L, ob, torch, timer, reps=steps)
         log(f"{which}: {conv if which == 'conv' else decay}")
@@ -343,7 +403,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip prefill/conv/decay lines")
-    ap.add_argument("--profile", choices=["decode", "prefill", "prefill_f16", "conv", "cumdecay"],
+    ap.add_argument("--profile", choices=["decode", "prefill", "prefill_f16", "layer", "conv", "cumdecay"],
                     help="run only this workload (and a 256 MiB device copy that calibrates "
                          "HBM byte counters) for rocprofv3; prints no JSON line")
     args = ap.parse_args()
@@ -380,6 +440,10 @@ def main():
         log("conv / decay ...")
         secondary["conv"], secondary["cumdecay"] = bench_stream(L, ob, torch, timer)
         log(f"conv: {secondary['conv']}\ncumdecay: {secondary['cumdecay']}")
+        log("layer glue (gating prologue, gated RMSNorm) ...")
+        secondary["gating_prologue"], secondary["gated_rmsnorm"] = bench_layer_glue(L, ob, torch, timer)
+        log(f"gating prologue: {secondary['gating_prologue']}\n"
+            f"gated rmsnorm: {secondary['gated_rmsnorm']}")
 
     cpu = None
     if not args.no_cpu:

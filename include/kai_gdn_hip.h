@@ -135,6 +135,48 @@ int kai_run_gdn_chunk_delta_rule_bf16_f16state_hip(const uint16_t *q,
                                                    int num_k_heads, float q_scale,
                                                    void *stream);
 
+/* ---- layer glue on either side of the recurrence ------------------------
+ * No reference kai symbol: the reference's layer runs these steps in its CPU
+ * model code; the definitions are HF transformers modeling_qwen3_5.py
+ * (Qwen3_5GatedDeltaNet.forward:481-502, l2norm:242-245,
+ * Qwen3_5RMSNormGated:168-184), which the reference documents at
+ * docs/GDN_LAYER_AUDIT.md:138-163.  Head dims are 128.
+ *
+ * Gating prologue.  x [rows][(2 Hk + Hv) * 128] fp32 is the conv+SiLU output
+ * of rows = batch * seq_len tokens, channels ordered q heads, k heads, v heads
+ * (HF's torch.split of the conv output); a, b [rows][Hv] fp32 are the in_proj_a
+ * and in_proj_b outputs; A_log, dt_bias [Hv].  Writes
+ *   q, k [rows][Hk][128] = x_head / sqrt(sum x_head^2 + 1e-6)
+ *   v [rows][Hv][128]    = x_head
+ *   g [rows][Hv]    = -exp(A_log) * softplus(a + dt_bias)  (threshold 20)
+ *   beta [rows][Hv] = sigmoid(b)
+ * in the layouts the recurrence entry points read (bf16 bit patterns for the
+ * prefill, fp32 for the decode step).  The 1/sqrt(128) query scale is the
+ * recurrence's q_scale argument (HF applies it after the norm), and the GQA
+ * repeat_interleave is not materialised: value head h reads key head
+ * h / (Hv / Hk).  x, q, k, v 16-byte aligned; Hv % Hk == 0. */
+int kai_run_gdn_gating_prologue_bf16_hip(const float *x, const float *a, const float *b,
+                                         const float *A_log, const float *dt_bias,
+                                         uint16_t *q, uint16_t *k, uint16_t *v, float *g,
+                                         float *beta, size_t rows, int num_k_heads,
+                                         int num_v_heads, void *stream);
+int kai_run_gdn_gating_prologue_f32_hip(const float *x, const float *a, const float *b,
+                                        const float *A_log, const float *dt_bias, float *q,
+                                        float *k, float *v, float *g, float *beta,
+                                        size_t rows, int num_k_heads, int num_v_heads,
+                                        void *stream);
+/* Gated RMSNorm epilogue: for each of `rows` rows of 128 values (rows =
+ * batch * seq_len * num_v_heads, the recurrence output o and the in_proj_z
+ * gate z in the same layout), y = w * (o / sqrt(mean(o^2) + eps)) * silu(z).
+ * The bf16 form rounds as HF's module does in a bf16 model: the normalised
+ * row to bf16, its product with w to bf16, the final product to bf16.
+ * y is the input of out_proj.  Pointers 16-byte aligned; eps >= 0
+ * (Qwen3.5: 1e-6). */
+int kai_run_gdn_gated_rmsnorm_bf16_hip(const uint16_t *o, const uint16_t *z,
+                                       const uint16_t *w, uint16_t *y, size_t rows,
+                                       float eps, void *stream);
+int kai_run_gdn_gated_rmsnorm_f32_hip(const float *o, const float *z, const float *w,
+                                      float *y, size_t rows, float eps, void *stream);
 /* ---- library ------------------------------------------------------------ */
 
 /* Initialise the HIP runtime state of the current device (optional; every

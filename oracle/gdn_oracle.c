@@ -458,3 +458,76 @@ void orc_chunk_gdr_f64(const float *q, const float *k, const float *v,
                        float q_scale) {
     ORC_CHUNK_BODY(double, exp)
 }
+
+/* ---- layer glue: gating prologue and gated RMSNorm ------------------------ */
+
+/* Qwen3_5GatedDeltaNet.forward:497-499 and l2norm:242-245 (see header). */
+static float softplus_torch(float y) { return y > 20.f ? y : log1pf(expf(y)); }
+
+void orc_gating_prologue_f32(const float *x, const float *a, const float *b,
+                             const float *A_log, const float *dt_bias, float *q,
+                             float *k, float *v, float *g, float *beta, size_t rows,
+                             int Hk, int Hv) {
+    const int D = 128, H = 2 * Hk + Hv;
+#pragma omp parallel for schedule(static)
+    for (size_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * (size_t)H * D;
+        for (int h = 0; h < H; ++h) {
+            const float *xh = xr + (size_t)h * D;
+            float *dst = h < Hk ? q + (r * Hk + h) * D
+                       : h < 2 * Hk ? k + (r * Hk + (h - Hk)) * D
+                                    : v + (r * Hv + (h - 2 * Hk)) * D;
+            if (h < 2 * Hk) {
+                double ss = 0.0;
+                for (int i = 0; i < D; ++i) ss += (double)xh[i] * xh[i];
+                const float inv = 1.0f / sqrtf((float)ss + 1e-6f);
+                for (int i = 0; i < D; ++i) dst[i] = xh[i] * inv;
+            } else {
+                for (int i = 0; i < D; ++i) dst[i] = xh[i];
+            }
+        }
+        for (int h = 0; h < Hv; ++h) {
+            const size_t i = r * Hv + h;
+            g[i] = -expf(A_log[h]) * softplus_torch(a[i] + dt_bias[h]);
+            beta[i] = 1.0f / (1.0f + expf(-b[i]));
+        }
+    }
+}
+
+/* Qwen3_5RMSNormGated.forward:175-184 (see header). */
+static float silu_f32(float z) { return z / (1.0f + expf(-z)); }
+
+static float row_inv_rms(const float *x, int n, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < n; ++i) ss += (double)x[i] * x[i];
+    const float var = (float)ss / (float)n;
+    return 1.0f / sqrtf(var + eps);
+}
+
+void orc_gated_rmsnorm_f32(const float *o, const float *z, const float *w, float *y,
+                           size_t rows, int n, float eps) {
+#pragma omp parallel for schedule(static)
+    for (size_t r = 0; r < rows; ++r) {
+        const float *orow = o + r * n, *zrow = z + r * n;
+        const float inv = row_inv_rms(orow, n, eps);
+        for (int i = 0; i < n; ++i) {
+            const float h = orow[i] * inv;
+            y[r * n + i] = (w[i] * h) * silu_f32(zrow[i]);
+        }
+    }
+}
+
+void orc_gated_rmsnorm_bf16(const uint16_t *o, const uint16_t *z, const uint16_t *w,
+                            uint16_t *y, size_t rows, int n, float eps) {
+#pragma omp parallel for schedule(static)
+    for (size_t r = 0; r < rows; ++r) {
+        float row[n];
+        for (int i = 0; i < n; ++i) row[i] = orc_bf16_to_f32(o[r * n + i]);
+        const float inv = row_inv_rms(row, n, eps);
+        for (int i = 0; i < n; ++i) {
+            const float h = orc_bf16_to_f32(orc_f32_to_bf16(row[i] * inv));
+            const float hw = orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(w[i]) * h));
+            y[r * n + i] = orc_f32_to_bf16(hw * silu_f32(orc_bf16_to_f32(z[r * n + i])));
+        }
+    }
+}

@@ -28,6 +28,13 @@
  *                              golden vectors (tests/golden).
  *   orc_chunk_gdr_f32/_f64  -- HF torch_chunk_gated_delta_rule golden
  *                              vectors, and equality with T stepped decodes.
+ *   orc_gating_prologue_f32 -- torch golden vectors of the HF forward's
+ *                              gate expressions and HF l2norm; closed forms
+ *                              (unit norms, softplus(0) = ln 2, sigmoid(0)
+ *                              = 1/2, the softplus threshold).
+ *   orc_gated_rmsnorm_*     -- golden vectors of HF Qwen3_5RMSNormGated in
+ *                              fp32 and bf16; closed forms (constant rows,
+ *                              z = 0 gives 0, w scales linearly).
  */
 #ifndef ORC_GDN_ORACLE_H
 #define ORC_GDN_ORACLE_H
@@ -134,6 +141,35 @@ void orc_chunk_gdr_f64(const float *q, const float *k, const float *v,
                        const float *g, const float *beta, float *o, float *S,
                        int B, int T, int Hv, int Hk, int dk, int dv, int chunk,
                        float q_scale);
+
+/* Gating prologue of one GDN layer: HF transformers
+ * modeling_qwen3_5.py Qwen3_5GatedDeltaNet.forward:497-499 (gates) and
+ * l2norm:242-245 (q, k norm with eps 1e-6, use_qk_l2norm_in_kernel,
+ * :262-264).  x [rows][(2 Hk + Hv) * 128] holds the conv output of each
+ * token, q heads then k heads then v heads (the torch.split / reshape of
+ * :481-492); a, b [rows][Hv]; A_log, dt_bias [Hv].  Outputs:
+ *   q, k [rows][Hk][128] = x_head / sqrt(sum x_head^2 + 1e-6)
+ *   v [rows][Hv][128]    = x_head
+ *   g [rows][Hv]    = -exp(A_log) * softplus(a + dt_bias),
+ *                     softplus(y) = y > 20 ? y : log1p(exp(y)) (torch's)
+ *   beta [rows][Hv] = 1 / (1 + exp(-b))
+ * The sum of squares is accumulated in double and rounded once. */
+void orc_gating_prologue_f32(const float *x, const float *a, const float *b,
+                             const float *A_log, const float *dt_bias, float *q,
+                             float *k, float *v, float *g, float *beta, size_t rows,
+                             int Hk, int Hv);
+
+/* Gated RMSNorm with the SiLU gate (HF Qwen3_5RMSNormGated.forward,
+ * modeling_qwen3_5.py:175-184) over rows of n values:
+ *   fp32 model: y = (w * (o / sqrt(mean(o^2) + eps))) * silu(z)
+ *   bf16 model: h = bf16(o / sqrt(mean(o^2) + eps)), h = bf16(w * h),
+ *               y = bf16(h * silu(z))   (o, z, w, y bf16 bit patterns)
+ * with silu(z) = z / (1 + exp(-z)) in fp32 and mean(o^2) in fp32 from a
+ * double sum. */
+void orc_gated_rmsnorm_f32(const float *o, const float *z, const float *w, float *y,
+                           size_t rows, int n, float eps);
+void orc_gated_rmsnorm_bf16(const uint16_t *o, const uint16_t *z, const uint16_t *w,
+                            uint16_t *y, size_t rows, int n, float eps);
 
 /* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
 int orc_num_threads(void);

@@ -179,6 +179,45 @@ def chunk_gdr(q, k, v, g, beta, S0, B, T, Hv, Hk, dk, dv, chunk=64, q_scale=None
     return o, S
 
 
+# ---- layer glue ------------------------------------------------------------
+
+def gating_prologue(x, a, b, A_log, dt_bias, rows, Hk, Hv):
+    """HF gate expressions and q/k l2norm; returns (q [rows][Hk][128],
+    k [rows][Hk][128], v [rows][Hv][128], g [rows][Hv], beta [rows][Hv])."""
+    q = np.empty((rows, Hk, 128), np.float32)
+    k = np.empty((rows, Hk, 128), np.float32)
+    v = np.empty((rows, Hv, 128), np.float32)
+    g = np.empty((rows, Hv), np.float32)
+    beta = np.empty((rows, Hv), np.float32)
+    c = lambda t: np.ascontiguousarray(t, np.float32)  # noqa: E731
+    lib().orc_gating_prologue_f32(P(c(x)), P(c(a)), P(c(b)), P(c(A_log)), P(c(dt_bias)),
+                                  P(q), P(k), P(v), P(g), P(beta), _sz(rows), _int(Hk),
+                                  _int(Hv))
+    return q, k, v, g, beta
+
+
+def gated_rmsnorm_f32(o, z, w, eps=1e-6):
+    """HF Qwen3_5RMSNormGated in an fp32 model over the last axis."""
+    o = np.ascontiguousarray(o, np.float32)
+    n = o.shape[-1]
+    y = np.empty_like(o)
+    lib().orc_gated_rmsnorm_f32(P(o), P(np.ascontiguousarray(z, np.float32)),
+                                P(np.ascontiguousarray(w, np.float32)), P(y),
+                                _sz(o.size // n), _int(n), _flt(eps))
+    return y
+
+
+def gated_rmsnorm_bf16(o16, z16, w16, eps=1e-6):
+    """HF Qwen3_5RMSNormGated in a bf16 model (bf16 bit patterns)."""
+    o16 = np.ascontiguousarray(o16, np.uint16)
+    n = o16.shape[-1]
+    y = np.empty_like(o16)
+    lib().orc_gated_rmsnorm_bf16(P(o16), P(np.ascontiguousarray(z16, np.uint16)),
+                                 P(np.ascontiguousarray(w16, np.uint16)), P(y),
+                                 _sz(o16.size // n), _int(n), _flt(eps))
+    return y
+
+
 def num_threads() -> int:
     return lib().orc_num_threads()
 

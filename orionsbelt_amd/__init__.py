@@ -35,6 +35,10 @@ HIP_SYMBOLS = (
     "kai_run_gdn_delta_rule_decode_f16state_hip",
     "kai_run_gdn_chunk_delta_rule_bf16_f32_hip",
     "kai_run_gdn_chunk_delta_rule_bf16_f16state_hip",
+    "kai_run_gdn_gating_prologue_bf16_hip",
+    "kai_run_gdn_gating_prologue_f32_hip",
+    "kai_run_gdn_gated_rmsnorm_bf16_hip",
+    "kai_run_gdn_gated_rmsnorm_f32_hip",
     "kai_gdn_hip_init",
     "kai_gdn_hip_error_string",
     "kai_gdn_hip_check_device_error",
@@ -68,6 +72,12 @@ _SIGS = {
         (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     "kai_run_gdn_chunk_delta_rule_bf16_f16state_hip":
         (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
+    "kai_run_gdn_gating_prologue_bf16_hip":
+        (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _vp]),
+    "kai_run_gdn_gating_prologue_f32_hip":
+        (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _vp]),
+    "kai_run_gdn_gated_rmsnorm_bf16_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _f, _vp]),
+    "kai_run_gdn_gated_rmsnorm_f32_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _f, _vp]),
     "kai_gdn_hip_init": (_i, []),
     "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
     "kai_gdn_hip_check_device_error": (_i, []),

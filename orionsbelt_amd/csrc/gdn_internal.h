@@ -75,4 +75,16 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
                               void *S, int B, int T, int Hv, int Hk, float q_scale, void *carry,
                               hipStream_t st);
 
+// ---- layer glue (gdn_layer.hip) ---------------------------------------------
+
+// Gating prologue: conv output x [rows][(2 Hk + Hv) * 128] -> q, k (L2-normalised)
+// [rows][Hk][128], v [rows][Hv][128] (bf16 bit patterns or fp32), g, beta [rows][Hv].
+hipError_t launch_gating_prologue(bool bf16, const float *x, const float *a, const float *b,
+                                  const float *A_log, const float *dt_bias, void *q, void *k,
+                                  void *v, float *g, float *beta, size_t rows, int Hk, int Hv,
+                                  hipStream_t st);
+// Gated RMSNorm over rows of 128 values (bf16 bit patterns or fp32).
+hipError_t launch_gated_rmsnorm(bool bf16, const void *o, const void *z, const void *w, void *y,
+                                size_t rows, float eps, hipStream_t st);
+
 }  // namespace gdn

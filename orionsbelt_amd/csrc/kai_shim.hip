@@ -426,6 +426,71 @@ extern "C" int kai_run_gdn_chunk_delta_rule_bf16_f16state_hip(
                      q_scale, (hipStream_t)stream);
 }
 
+// ---- layer glue: gating prologue and gated RMSNorm ------------------------
+
+static int check_prologue_args(const float *x, const float *a, const float *b, const float *A_log,
+                               const float *dt_bias, const void *q, const void *k, const void *v,
+                               const float *g, const float *beta, size_t rows, int Hk, int Hv,
+                               size_t out_align) {  // 16-byte accesses to every array
+    if (Hk <= 0 || Hv <= 0 || Hv % Hk != 0) return (int)hipErrorInvalidValue;
+    if (rows == 0) return 0;
+    if (rows > 0x7FFFFFFFu) return (int)hipErrorInvalidValue;
+    if (!x || !a || !b || !A_log || !dt_bias || !q || !k || !v || !g || !beta)
+        return (int)hipErrorInvalidValue;
+    if (!aligned(x, 16) || !aligned(q, out_align) || !aligned(k, out_align) || !aligned(v, out_align))
+        return (int)hipErrorInvalidValue;
+    return 0;
+}
+
+extern "C" int kai_run_gdn_gating_prologue_bf16_hip(const float *x, const float *a, const float *b,
+                                                    const float *A_log, const float *dt_bias,
+                                                    uint16_t *q, uint16_t *k, uint16_t *v, float *g,
+                                                    float *beta, size_t rows, int num_k_heads,
+                                                    int num_v_heads, void *stream) {
+    int rc = check_prologue_args(x, a, b, A_log, dt_bias, q, k, v, g, beta, rows, num_k_heads,
+                                 num_v_heads, 16);
+    if (rc || rows == 0) return rc;
+    return (int)gdn::launch_gating_prologue(true, x, a, b, A_log, dt_bias, q, k, v, g, beta, rows,
+                                            num_k_heads, num_v_heads, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_gating_prologue_f32_hip(const float *x, const float *a, const float *b,
+                                                   const float *A_log, const float *dt_bias,
+                                                   float *q, float *k, float *v, float *g,
+                                                   float *beta, size_t rows, int num_k_heads,
+                                                   int num_v_heads, void *stream) {
+    int rc = check_prologue_args(x, a, b, A_log, dt_bias, q, k, v, g, beta, rows, num_k_heads,
+                                 num_v_heads, 16);
+    if (rc || rows == 0) return rc;
+    return (int)gdn::launch_gating_prologue(false, x, a, b, A_log, dt_bias, q, k, v, g, beta, rows,
+                                            num_k_heads, num_v_heads, (hipStream_t)stream);
+}
+
+static int check_rmsnorm_args(const void *o, const void *z, const void *w, const void *y,
+                              size_t rows, float eps, size_t align) {
+    if (!(eps >= 0.0f)) return (int)hipErrorInvalidValue;  // also rejects NaN
+    if (rows == 0) return 0;
+    if (!o || !z || !w || !y) return (int)hipErrorInvalidValue;
+    if (!aligned(o, align) || !aligned(z, align) || !aligned(w, align) || !aligned(y, align))
+        return (int)hipErrorInvalidValue;
+    return 0;
+}
+
+extern "C" int kai_run_gdn_gated_rmsnorm_bf16_hip(const uint16_t *o, const uint16_t *z,
+                                                  const uint16_t *w, uint16_t *y, size_t rows,
+                                                  float eps, void *stream) {
+    int rc = check_rmsnorm_args(o, z, w, y, rows, eps, 16);
+    if (rc || rows == 0) return rc;
+    return (int)gdn::launch_gated_rmsnorm(true, o, z, w, y, rows, eps, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_gated_rmsnorm_f32_hip(const float *o, const float *z, const float *w,
+                                                 float *y, size_t rows, float eps, void *stream) {
+    int rc = check_rmsnorm_args(o, z, w, y, rows, eps, 16);
+    if (rc || rows == 0) return rc;
+    return (int)gdn::launch_gated_rmsnorm(false, o, z, w, y, rows, eps, (hipStream_t)stream);
+}
+
 // ===========================================================================
 // Reference kai symbols (synchronous, host or device pointers)
 // ===========================================================================

@@ -4,7 +4,7 @@ installed HuggingFace transformers for the delta-rule vectors):
 
     python tests/golden/gen_golden.py
 
-Three fixture files, each a numpy .npz (no pickles):
+Four fixture files, each a numpy .npz (no pickles):
 
 kai_ref.npz     inputs and outputs of the reference kai ukernels
                 (kleidiai_submission/kai/ukernels/gdn/*.c, scalar branch),
@@ -16,6 +16,10 @@ sve_mixed.npz   the reference gdn_sve.c fp16/bf16 variants
                 (src/orionsbelt/engines/cpu/kernels/gdn_sve.c:442-766) from
                 oracle/_ref/libgdn_sve_ref.so on T=64, C=35 warm/cold gates
                 (the scenarios of test_gdn_mixed.c).
+hf_layer.npz    HuggingFace transformers (v5.15.0): the gate expressions and
+                l2norm of Qwen3_5GatedDeltaNet.forward and Qwen3_5RMSNormGated
+                (modeling_qwen3_5.py:168-184,242-245,497-499), fp32 and bf16
+                (`python tests/golden/gen_golden.py layer` rewrites only it).
 hf_gdr.npz      HuggingFace transformers (v5.15.0, third-party, not part of
                 the reference) torch_chunk_gated_delta_rule and
                 torch_recurrent_gated_delta_rule
@@ -173,10 +177,72 @@ def gen_hf():
     np.savez_compressed(os.path.join(HERE, "hf_gdr.npz"), **d)
 
 
+def gen_layer():
+    """The layer glue around the recurrence, from HF transformers v5.15.0:
+    the gate expressions of Qwen3_5GatedDeltaNet.forward
+    (modeling_qwen3_5.py:497-499), its l2norm (:242-245, applied to q and k
+    with use_qk_l2norm_in_kernel, :262-264) after the split of the conv
+    output into q, k, v heads (:481-492), and Qwen3_5RMSNormGated
+    (:168-184) in fp32 and in bf16."""
+    import torch
+    import torch.nn.functional as F
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as m
+
+    torch.set_num_threads(4)
+    rs = np.random.RandomState(77)
+    d = {}
+    rows, Hk, Hv, D = 6, 2, 4, 128
+    x = rs.randn(rows, (2 * Hk + Hv) * D).astype(np.float32)
+    x[1, :Hk * D] = 0.0                      # zero q heads: l2norm of 0 is 0
+    x[2] *= 40.0                             # large rows
+    a = rs.randn(rows, Hv).astype(np.float32) * 3
+    a[3] = [25.0, -30.0, 0.0, 19.5]          # softplus threshold (20) both sides
+    b = rs.randn(rows, Hv).astype(np.float32) * 4
+    A_log = np.log(rs.uniform(0.5, 16, Hv)).astype(np.float32)
+    dt_bias = rs.randn(Hv).astype(np.float32)
+    with torch.no_grad():
+        tx, ta, tb = (torch.from_numpy(t) for t in (x, a, b))
+        query, key, value = torch.split(tx, [Hk * D, Hk * D, Hv * D], dim=-1)
+        query = m.l2norm(query.reshape(rows, Hk, D), dim=-1, eps=1e-6)
+        key = m.l2norm(key.reshape(rows, Hk, D), dim=-1, eps=1e-6)
+        value = value.reshape(rows, Hv, D)
+        beta = tb.sigmoid()
+        g = -torch.from_numpy(A_log).float().exp() * F.softplus(ta.float() + torch.from_numpy(dt_bias))
+    d.update(gp_x=x, gp_a=a, gp_b=b, gp_A_log=A_log, gp_dt_bias=dt_bias,
+             gp_q=query.numpy(), gp_k=key.numpy(), gp_v=value.numpy(), gp_g=g.numpy(),
+             gp_beta=beta.numpy(), gp_dims=np.array([rows, Hk, Hv], np.int64))
+
+    n, nrows = 128, 9
+    o = rs.randn(nrows, n).astype(np.float32)
+    o[1] = 0.0                               # zero row: eps keeps it finite
+    o[2] *= 1e-3
+    z = (rs.randn(nrows, n) * 3).astype(np.float32)
+    z[3] = 0.0                               # silu(0) = 0
+    w = (1.0 + 0.2 * rs.randn(n)).astype(np.float32)
+    for dt, tag in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        norm = m.Qwen3_5RMSNormGated(n, eps=1e-6)
+        with torch.no_grad():
+            norm.weight.copy_(torch.from_numpy(w))
+            norm = norm.to(dt)
+            to, tz = torch.from_numpy(o).to(dt), torch.from_numpy(z).to(dt)
+            y = norm(to, tz)
+        if dt == torch.float32:
+            d.update(rn_f32_o=o, rn_f32_z=z, rn_f32_w=w, rn_f32_y=y.numpy())
+        else:
+            bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+            d.update(rn_bf16_o=bits(to), rn_bf16_z=bits(tz), rn_bf16_w=bits(norm.weight.data),
+                     rn_bf16_y=bits(y))
+    np.savez_compressed(os.path.join(HERE, "hf_layer.npz"), **d)
+
+
 if __name__ == "__main__":
     orc.build()
+    if len(sys.argv) > 1 and sys.argv[1] == "layer":
+        gen_layer()
+        sys.exit(0)
     gen_kai()
     gen_sve()
     gen_hf()
-    for f in ("kai_ref.npz", "sve_mixed.npz", "hf_gdr.npz"):
+    gen_layer()
+    for f in ("kai_ref.npz", "sve_mixed.npz", "hf_gdr.npz", "hf_layer.npz"):
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

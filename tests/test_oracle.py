@@ -403,3 +403,86 @@ def test_chunk_gate_sensitivity():
     o_nob, _ = orc.chunk_gdr(q, k, v, g, np.ones_like(beta), S0, B, T, Hv, Hk, dk, dv, 16)
     assert np.abs(o - o_nog).max() > 1e-2 * np.abs(o).max()
     assert np.abs(o - o_nob).max() > 1e-2 * np.abs(o).max()
+
+
+# --------------------------------------------------------------------------
+# layer glue: gating prologue and gated RMSNorm (hf_layer.npz)
+# --------------------------------------------------------------------------
+
+def ulp_bf16_diff(a16, b16):
+    """Distance in bf16 units in the last place between two bit arrays
+    (monotone integer mapping of the bit patterns)."""
+    def key(u):
+        u = np.asarray(u, np.uint16).astype(np.int32)
+        return np.where(u & 0x8000, 0x8000 - (u & 0x7FFF), u + 0x8000)
+    return np.abs(key(a16) - key(b16))
+
+
+def test_gating_prologue_vs_hf(golden):
+    d = golden("hf_layer.npz")
+    rows, Hk, Hv = (int(t) for t in d["gp_dims"])
+    q, k, v, g, beta = orc.gating_prologue(d["gp_x"], d["gp_a"], d["gp_b"], d["gp_A_log"],
+                                           d["gp_dt_bias"], rows, Hk, Hv)
+    np.testing.assert_allclose(q, d["gp_q"], rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(k, d["gp_k"], rtol=2e-6, atol=1e-7)
+    assert bits_equal(v, d["gp_v"])
+    np.testing.assert_allclose(g, d["gp_g"], rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(beta, d["gp_beta"], rtol=2e-6, atol=1e-7)
+
+
+def test_gating_prologue_closed_forms():
+    rows, Hk, Hv = 3, 1, 2
+    rs = np.random.RandomState(5)
+    x = rs.randn(rows, (2 * Hk + Hv) * 128).astype(np.float32)
+    x[2, :128] = 3.0                                   # constant q head
+    a = np.array([[0, 0], [30, -40], [0, 0]], np.float32)
+    b = np.array([[0, 0], [50, -50], [0, 0]], np.float32)
+    A_log = np.array([0.0, math.log(2.0)], np.float32)
+    dt = np.zeros(Hv, np.float32)
+    q, k, v, g, beta = orc.gating_prologue(x, a, b, A_log, dt, rows, Hk, Hv)
+    # unit rows (|x|^2 >> eps), v untouched and in the v channels, k from the k channels
+    np.testing.assert_allclose(np.linalg.norm(q, axis=-1), 1.0, rtol=1e-6)
+    np.testing.assert_allclose(np.linalg.norm(k, axis=-1), 1.0, rtol=1e-6)
+    assert bits_equal(v.reshape(rows, -1), x[:, 2 * Hk * 128:])
+    np.testing.assert_allclose(k[0, 0] * np.linalg.norm(x[0, 128:256]), x[0, 128:256], rtol=1e-5)
+    np.testing.assert_allclose(q[2, 0], np.full(128, 1 / math.sqrt(128), np.float32), rtol=1e-6)
+    # softplus(0) = ln 2, scaled by exp(A_log) = 1 and 2; beyond the
+    # threshold softplus(y) = y; far below, exp(y)
+    np.testing.assert_allclose(g[0], [-math.log(2.0), -2 * math.log(2.0)], rtol=1e-6)
+    assert g[1, 0] == np.float32(-30.0)
+    np.testing.assert_allclose(g[1, 1], -2 * math.exp(-40.0), rtol=1e-5)
+    np.testing.assert_allclose(beta[0], [0.5, 0.5], rtol=0)
+    assert beta[1, 0] == 1.0 and 0 < beta[1, 1] < 1e-20
+
+
+def test_gated_rmsnorm_vs_hf(golden):
+    d = golden("hf_layer.npz")
+    y = orc.gated_rmsnorm_f32(d["rn_f32_o"], d["rn_f32_z"], d["rn_f32_w"], 1e-6)
+    np.testing.assert_allclose(y, d["rn_f32_y"], rtol=3e-6, atol=1e-7)
+    y16 = orc.gated_rmsnorm_bf16(d["rn_bf16_o"], d["rn_bf16_z"], d["rn_bf16_w"], 1e-6)
+    # the three bf16 roundings of HF's bf16 module; rsqrt/exp differ by an
+    # fp32 ulp, which can move a rounding by one bf16 ulp
+    diff = ulp_bf16_diff(y16, d["rn_bf16_y"])
+    assert diff.max() <= 1 and (diff > 0).mean() < 0.02
+
+
+def test_gated_rmsnorm_closed_forms():
+    n = 128
+    w = np.linspace(0.5, 1.5, n).astype(np.float32)
+    # a constant row c: o / rms(o) = sign(c) exactly up to eps; z large -> silu(z) ~ z
+    o = np.full((2, n), 2.0, np.float32)
+    z = np.full((2, n), 30.0, np.float32)
+    z[1] = 0.0
+    y = orc.gated_rmsnorm_f32(o, z, w, 0.0)
+    np.testing.assert_allclose(y[0], w * 30.0, rtol=1e-6)
+    assert np.all(y[1] == 0)
+    # scaling o does not change the result (eps = 0); scaling w scales y
+    rs = np.random.RandomState(3)
+    o = rs.randn(4, n).astype(np.float32)
+    z = rs.randn(4, n).astype(np.float32)
+    y1 = orc.gated_rmsnorm_f32(o, z, w, 0.0)
+    np.testing.assert_allclose(orc.gated_rmsnorm_f32(o * 8, z, w, 0.0), y1, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(orc.gated_rmsnorm_f32(o, z, 2 * w, 0.0), 2 * y1, rtol=1e-6, atol=1e-7)
+    # a plain-numpy restatement in float64 (mean of squares, rsqrt, silu)
+    ref = (o / np.sqrt((o.astype(np.float64) ** 2).mean(-1, keepdims=True))) * w * (z / (1 + np.exp(-z.astype(np.float64))))
+    np.testing.assert_allclose(y1, ref, rtol=2e-6, atol=1e-7)
