@@ -177,6 +177,51 @@ int kai_run_gdn_gated_rmsnorm_bf16_hip(const uint16_t *o, const uint16_t *z,
                                        float eps, void *stream);
 int kai_run_gdn_gated_rmsnorm_f32_hip(const float *o, const float *z, const float *w,
                                       float *y, size_t rows, float eps, void *stream);
+/* ---- state formats of the prefill -> decode hand-off ----------------------
+ * No reference kai symbol.  HF keeps a GDN layer's cache as conv_state
+ * [batch][channels][4] (the last four conv inputs of each sequence, newest
+ * last, zero-padded after a prefill shorter than four tokens;
+ * transformers cache_utils.py LinearAttentionLayer.update_conv_state:
+ * 1032-1070) and the recurrent state [batch][Hv][128][128] in the model
+ * dtype.  The kai conv carries hist [3][channels] per sequence, oldest
+ * first (kai_gdn_causal_dwconv1d_f32_k4_sve.h:28-36).  Pointers to
+ * conv_state and w are 16-byte aligned; batch <= 65535. */
+
+/* HF causal_conv1d_update (modeling_qwen3_5.py:199-217) for a batch of
+ * sequences: x, out [batch][seq_len][channels] (token-major, as in_proj
+ * writes it), conv_state [batch][channels][4] updated in place, w
+ * [channels][4] (HF's conv1d.weight.squeeze(1)).  For each token:
+ *   out = ((s1*w0 + s2*w1) + s3*w2) + x*w3,  then SiLU if silu != 0,
+ *   state <- (s1, s2, s3, x)
+ * in the kai reference's order without contraction, so decode steps that
+ * continue a sequence are bit-identical to the kai conv over the whole
+ * sequence.  out may equal x. */
+int kai_run_gdn_causal_conv1d_update_f32_hip(const float *x, float *conv_state,
+                                             const float *w, float *out, int batch,
+                                             int seq_len, size_t channels, int silu,
+                                             void *stream);
+/* conv_state [batch][channels][4] after a prefill of seq_len tokens whose
+ * conv inputs are x [batch][seq_len][channels]: the last four rows, zero
+ * where seq_len < 4 (HF's prefill path of update_conv_state). */
+int kai_run_gdn_conv_state_from_inputs_f32_hip(const float *x, float *conv_state,
+                                               int batch, size_t seq_len,
+                                               size_t channels, void *stream);
+/* conv_state [batch][channels][4] -> hist [batch][3][channels] (entries
+ * 1..3, oldest first) and back.  Entry 0 of the HF state, the input four
+ * steps back, feeds no later output; hist -> state writes it as 0. */
+int kai_run_gdn_conv_state_to_hist_f32_hip(const float *conv_state, float *hist,
+                                           int batch, size_t channels, void *stream);
+int kai_run_gdn_conv_hist_to_state_f32_hip(const float *hist, float *conv_state,
+                                           int batch, size_t channels, void *stream);
+/* Element format conversion of `count` values (a recurrent state, e.g. fp32
+ * from the prefill to the fp16-state decode step): formats below, narrowing
+ * to nearest even (bf16 by the reference's rule, gdn_sve.c:81-87).  src and
+ * dst must not overlap unless they are the same array in the same format. */
+#define KAI_GDN_FMT_F32 0
+#define KAI_GDN_FMT_F16 1
+#define KAI_GDN_FMT_BF16 2
+int kai_run_gdn_state_convert_hip(const void *src, int src_format, void *dst,
+                                  int dst_format, size_t count, void *stream);
 /* ---- library ------------------------------------------------------------ */
 
 /* Initialise the HIP runtime state of the current device (optional; every

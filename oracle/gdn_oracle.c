@@ -531,3 +531,25 @@ void orc_gated_rmsnorm_bf16(const uint16_t *o, const uint16_t *z, const uint16_t
         }
     }
 }
+
+/* ---- decode-step conv on HF's state layout (see header) ------------------- */
+
+void orc_causal_conv1d_update_f32(const float *x, float *conv_state, const float *w,
+                                  float *out, int B, int T, size_t C, int silu) {
+    for (int b = 0; b < B; ++b)
+        for (size_t c = 0; c < C; ++c) {
+            float *s = conv_state + ((size_t)b * C + c) * 4;
+            const float *wc = w + c * 4;
+            for (int t = 0; t < T; ++t) {
+                const size_t i = ((size_t)b * T + t) * C + c;
+                const float cur = x[i];
+                float acc = s[1] * wc[0] + s[2] * wc[1] + s[3] * wc[2] + cur * wc[3];
+                if (silu) acc = acc / (1.0f + expf(-acc));
+                out[i] = acc;
+                s[0] = s[1];
+                s[1] = s[2];
+                s[2] = s[3];
+                s[3] = cur;
+            }
+        }
+}

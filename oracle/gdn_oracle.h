@@ -32,6 +32,10 @@
  *                              gate expressions and HF l2norm; closed forms
  *                              (unit norms, softplus(0) = ln 2, sigmoid(0)
  *                              = 1/2, the softplus threshold).
+ *   orc_causal_conv1d_update_f32 -- HF causal_conv1d_update golden vectors
+ *                              (tolerance: HF's conv sums in another order)
+ *                              and bit-identity with orc_causal_dwconv1d over
+ *                              the whole sequence (continuation).
  *   orc_gated_rmsnorm_*     -- golden vectors of HF Qwen3_5RMSNormGated in
  *                              fp32 and bf16; closed forms (constant rows,
  *                              z = 0 gives 0, w scales linearly).
@@ -170,6 +174,16 @@ void orc_gated_rmsnorm_f32(const float *o, const float *z, const float *w, float
                            size_t rows, int n, float eps);
 void orc_gated_rmsnorm_bf16(const uint16_t *o, const uint16_t *z, const uint16_t *w,
                             uint16_t *y, size_t rows, int n, float eps);
+
+/* HF causal_conv1d_update (modeling_qwen3_5.py:199-217) for B sequences
+ * of T new tokens: x, out [B][T][C], conv_state [B][C][4] (in/out; the last
+ * four inputs, newest last), w [C][4].  Per token, with the window
+ * (s1, s2, s3, x) of the state and the new input:
+ *   out = ((s1*w0 + s2*w1) + s3*w2) + x*w3   (the kai reference's order,
+ *         kai_gdn_causal_dwconv1d_f32_k4_sve.c:149-166), SiLU if silu,
+ *   state <- (s1, s2, s3, x). */
+void orc_causal_conv1d_update_f32(const float *x, float *conv_state, const float *w,
+                                  float *out, int B, int T, size_t C, int silu);
 
 /* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
 int orc_num_threads(void);

@@ -218,6 +218,45 @@ def gated_rmsnorm_bf16(o16, z16, w16, eps=1e-6):
     return y
 
 
+# ---- state hand-off formats ----------------------------------------------
+
+def causal_conv1d_update(x, conv_state, w, silu):
+    """HF causal_conv1d_update on x [B][T][C] (token-major), conv_state
+    [B][C][4], w [C][4]; returns (out [B][T][C], new conv_state)."""
+    x = np.ascontiguousarray(x, np.float32)
+    B, T, C = x.shape
+    st = np.array(conv_state, np.float32, copy=True)
+    out = np.empty_like(x)
+    lib().orc_causal_conv1d_update_f32(P(x), P(st), P(np.ascontiguousarray(w, np.float32)),
+                                       P(out), _int(B), _int(T), _sz(C), _int(int(silu)))
+    return out, st
+
+
+def conv_state_from_inputs(x):
+    """The HF conv state [B][C][4] after a prefill over x [B][T][C]: the
+    last four inputs, newest last, zero-padded when T < 4 (index work)."""
+    x = np.asarray(x, np.float32)
+    B, T, C = x.shape
+    st = np.zeros((B, C, 4), np.float32)
+    n = min(T, 4)
+    if n:
+        st[:, :, 4 - n:] = np.transpose(x[:, T - n:, :], (0, 2, 1))
+    return st
+
+
+def conv_state_to_hist(conv_state):
+    """[B][C][4] -> kai history [B][3][C] (entries 1..3, oldest first)."""
+    return np.ascontiguousarray(np.transpose(np.asarray(conv_state, np.float32)[:, :, 1:], (0, 2, 1)))
+
+
+def conv_hist_to_state(hist):
+    """kai history [B][3][C] -> [B][C][4] with entry 0 (unused) = 0."""
+    h = np.asarray(hist, np.float32)
+    st = np.zeros((h.shape[0], h.shape[2], 4), np.float32)
+    st[:, :, 1:] = np.transpose(h, (0, 2, 1))
+    return st
+
+
 def num_threads() -> int:
     return lib().orc_num_threads()
 

@@ -39,6 +39,11 @@ HIP_SYMBOLS = (
     "kai_run_gdn_gating_prologue_f32_hip",
     "kai_run_gdn_gated_rmsnorm_bf16_hip",
     "kai_run_gdn_gated_rmsnorm_f32_hip",
+    "kai_run_gdn_causal_conv1d_update_f32_hip",
+    "kai_run_gdn_conv_state_from_inputs_f32_hip",
+    "kai_run_gdn_conv_state_to_hist_f32_hip",
+    "kai_run_gdn_conv_hist_to_state_f32_hip",
+    "kai_run_gdn_state_convert_hip",
     "kai_gdn_hip_init",
     "kai_gdn_hip_error_string",
     "kai_gdn_hip_check_device_error",
@@ -49,6 +54,9 @@ _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _i = ctypes.c_int
 _f = ctypes.c_float
+
+# Element formats of kai_run_gdn_state_convert_hip (KAI_GDN_FMT_* in kai_gdn_hip.h).
+FMT_F32, FMT_F16, FMT_BF16 = 0, 1, 2
 
 _SIGS = {
     "kai_run_gdn_cumdecay_f32_sve": (None, [_vp, _vp, _sz, _sz]),
@@ -78,6 +86,11 @@ _SIGS = {
         (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _vp]),
     "kai_run_gdn_gated_rmsnorm_bf16_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _f, _vp]),
     "kai_run_gdn_gated_rmsnorm_f32_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _f, _vp]),
+    "kai_run_gdn_causal_conv1d_update_f32_hip": (_i, [_vp, _vp, _vp, _vp, _i, _i, _sz, _i, _vp]),
+    "kai_run_gdn_conv_state_from_inputs_f32_hip": (_i, [_vp, _vp, _i, _sz, _sz, _vp]),
+    "kai_run_gdn_conv_state_to_hist_f32_hip": (_i, [_vp, _vp, _i, _sz, _vp]),
+    "kai_run_gdn_conv_hist_to_state_f32_hip": (_i, [_vp, _vp, _i, _sz, _vp]),
+    "kai_run_gdn_state_convert_hip": (_i, [_vp, _i, _vp, _i, _sz, _vp]),
     "kai_gdn_hip_init": (_i, []),
     "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
     "kai_gdn_hip_check_device_error": (_i, []),

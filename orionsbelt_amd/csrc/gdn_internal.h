@@ -87,4 +87,18 @@ hipError_t launch_gating_prologue(bool bf16, const float *x, const float *a, con
 hipError_t launch_gated_rmsnorm(bool bf16, const void *o, const void *z, const void *w, void *y,
                                 size_t rows, float eps, hipStream_t st);
 
+// ---- state hand-off formats and the decode-step conv (gdn_state.hip) -------
+
+// HF causal_conv1d_update on x, out [B][T][C], conv_state [B][C][4], w [C][4].
+hipError_t launch_conv_update(const float *x, float *conv_state, const float *w, float *out, int B,
+                              int T, size_t C, bool silu, hipStream_t st);
+// conv_state [B][C][4] from the last four rows of x [B][T][C] (zero-padded).
+hipError_t launch_conv_state_from_inputs(const float *x, float *conv_state, int B, size_t T, size_t C,
+                                         hipStream_t st);
+// hist [B][3][C] <-> conv_state [B][C][4].
+hipError_t launch_conv_hist_state(bool to_hist, float *hist, float *conv_state, int B, size_t C,
+                                  hipStream_t st);
+// Element conversion between kF32, kF16 and kBF16 arrays.
+hipError_t launch_convert(const void *src, int sf, void *dst, int df, size_t n, hipStream_t st);
+
 }  // namespace gdn

@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <vector>
 
@@ -489,6 +490,69 @@ extern "C" int kai_run_gdn_gated_rmsnorm_f32_hip(const float *o, const float *z,
     int rc = check_rmsnorm_args(o, z, w, y, rows, eps, 16);
     if (rc || rows == 0) return rc;
     return (int)gdn::launch_gated_rmsnorm(false, o, z, w, y, rows, eps, (hipStream_t)stream);
+}
+
+// ---- state hand-off formats and the decode-step conv -----------------------
+
+static int check_conv_state_args(int B, size_t C, const void *state, std::initializer_list<const void *> others) {
+    if (B < 0 || B > 65535) return (int)hipErrorInvalidValue;
+    if (B == 0 || C == 0) return 0;
+    if (C > ((size_t)1 << 40)) return (int)hipErrorInvalidValue;
+    if (!state || !aligned(state, 16)) return (int)hipErrorInvalidValue;
+    for (const void *p : others)
+        if (!p) return (int)hipErrorInvalidValue;
+    return 0;
+}
+
+extern "C" int kai_run_gdn_causal_conv1d_update_f32_hip(const float *x, float *conv_state,
+                                                        const float *w, float *out, int batch,
+                                                        int seq_len, size_t channels, int silu,
+                                                        void *stream) {
+    if (seq_len < 0) return (int)hipErrorInvalidValue;
+    int rc = check_conv_state_args(batch, channels, conv_state, {x, w, out});
+    if (rc || batch == 0 || channels == 0 || seq_len == 0) return rc;
+    if (!aligned(w, 16)) return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_conv_update(x, conv_state, w, out, batch, seq_len, channels, silu != 0,
+                                        (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_conv_state_from_inputs_f32_hip(const float *x, float *conv_state,
+                                                          int batch, size_t seq_len,
+                                                          size_t channels, void *stream) {
+    int rc = check_conv_state_args(batch, channels, conv_state, {seq_len ? x : conv_state});
+    if (rc || batch == 0 || channels == 0) return rc;
+    return (int)gdn::launch_conv_state_from_inputs(x, conv_state, batch, seq_len, channels,
+                                                   (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_conv_state_to_hist_f32_hip(const float *conv_state, float *hist,
+                                                      int batch, size_t channels, void *stream) {
+    int rc = check_conv_state_args(batch, channels, conv_state, {hist});
+    if (rc || batch == 0 || channels == 0) return rc;
+    return (int)gdn::launch_conv_hist_state(true, hist, const_cast<float *>(conv_state), batch,
+                                            channels, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_conv_hist_to_state_f32_hip(const float *hist, float *conv_state,
+                                                      int batch, size_t channels, void *stream) {
+    int rc = check_conv_state_args(batch, channels, conv_state, {hist});
+    if (rc || batch == 0 || channels == 0) return rc;
+    return (int)gdn::launch_conv_hist_state(false, const_cast<float *>(hist), conv_state, batch,
+                                            channels, (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_state_convert_hip(const void *src, int src_format, void *dst,
+                                             int dst_format, size_t count, void *stream) {
+    auto ok = [](int f) { return f == gdn::kF32 || f == gdn::kF16 || f == gdn::kBF16; };
+    if (!ok(src_format) || !ok(dst_format)) return (int)hipErrorInvalidValue;
+    if (count == 0) return 0;
+    if (!src || !dst) return (int)hipErrorInvalidValue;
+    const size_t sb = count * (src_format == gdn::kF32 ? 4 : 2);
+    const size_t db = count * (dst_format == gdn::kF32 ? 4 : 2);
+    const uintptr_t s0 = (uintptr_t)src, d0 = (uintptr_t)dst;
+    const bool same = s0 == d0 && src_format == dst_format;
+    if (!same && s0 < d0 + db && d0 < s0 + sb) return (int)hipErrorInvalidValue;  // overlap
+    return (int)gdn::launch_convert(src, src_format, dst, dst_format, count, (hipStream_t)stream);
 }
 
 // ===========================================================================

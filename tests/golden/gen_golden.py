@@ -4,7 +4,7 @@ installed HuggingFace transformers for the delta-rule vectors):
 
     python tests/golden/gen_golden.py
 
-Four fixture files, each a numpy .npz (no pickles):
+Five fixture files, each a numpy .npz (no pickles):
 
 kai_ref.npz     inputs and outputs of the reference kai ukernels
                 (kleidiai_submission/kai/ukernels/gdn/*.c, scalar branch),
@@ -19,7 +19,12 @@ sve_mixed.npz   the reference gdn_sve.c fp16/bf16 variants
 hf_layer.npz    HuggingFace transformers (v5.15.0): the gate expressions and
                 l2norm of Qwen3_5GatedDeltaNet.forward and Qwen3_5RMSNormGated
                 (modeling_qwen3_5.py:168-184,242-245,497-499), fp32 and bf16
-                (`python tests/golden/gen_golden.py layer` rewrites only it).
+                (`python tests/golden/gen_golden.py layer` rewrites only
+                it and hf_state.npz).
+hf_state.npz    HuggingFace transformers (v5.15.0): causal_conv1d_update
+                (modeling_qwen3_5.py:199-217) and the conv cache of
+                LinearAttentionLayer.update_conv_state (cache_utils.py:
+                1032-1070).
 hf_gdr.npz      HuggingFace transformers (v5.15.0, third-party, not part of
                 the reference) torch_chunk_gated_delta_rule and
                 torch_recurrent_gated_delta_rule
@@ -235,14 +240,48 @@ def gen_layer():
     np.savez_compressed(os.path.join(HERE, "hf_layer.npz"), **d)
 
 
+def gen_state():
+    """The decode-step conv and the conv cache of HF transformers v5.15.0:
+    causal_conv1d_update (modeling_qwen3_5.py:199-217, torch fallback) and
+    LinearAttentionLayer.update_conv_state (cache_utils.py:1032-1070) after a
+    prefill, on small shapes.  Tensors are stored token-major ([B][T][C]) as
+    the kernels take them; HF's own calls use [B][C][T]."""
+    import torch
+    from transformers import cache_utils
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as m
+
+    rs = np.random.RandomState(91)
+    d = {}
+    for name, B, T, C, silu in (("cu_t1", 3, 1, 40, True), ("cu_t3", 2, 3, 24, False)):
+        x = rs.randn(B, T, C).astype(np.float32)
+        st = rs.randn(B, C, 4).astype(np.float32)
+        w = (0.5 * rs.randn(C, 4)).astype(np.float32)
+        ts = torch.from_numpy(st.copy())
+        with torch.no_grad():
+            out = m.causal_conv1d_update(torch.from_numpy(x).transpose(1, 2).contiguous(), ts,
+                                         torch.from_numpy(w), None, "silu" if silu else None)
+        d.update({f"{name}_x": x, f"{name}_state0": st, f"{name}_w": w,
+                  f"{name}_out": out.transpose(1, 2).contiguous().numpy(),
+                  f"{name}_state": ts.numpy(), f"{name}_silu": np.array(int(silu))})
+    for name, B, T, C in (("cs_t2", 2, 2, 16), ("cs_t7", 2, 7, 16)):
+        x = rs.randn(B, T, C).astype(np.float32)
+        layer = cache_utils.LinearAttentionLayer()
+        layer.update_conv_state(torch.from_numpy(x).transpose(1, 2).contiguous(), 0,
+                                conv_kernel_size=4)
+        d.update({f"{name}_x": x, f"{name}_state": layer.conv_states[0].numpy().copy()})
+    np.savez_compressed(os.path.join(HERE, "hf_state.npz"), **d)
+
+
 if __name__ == "__main__":
     orc.build()
     if len(sys.argv) > 1 and sys.argv[1] == "layer":
         gen_layer()
+        gen_state()
         sys.exit(0)
     gen_kai()
     gen_sve()
     gen_hf()
     gen_layer()
-    for f in ("kai_ref.npz", "sve_mixed.npz", "hf_gdr.npz", "hf_layer.npz"):
+    gen_state()
+    for f in ("kai_ref.npz", "sve_mixed.npz", "hf_gdr.npz", "hf_layer.npz", "hf_state.npz"):
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

@@ -486,3 +486,54 @@ def test_gated_rmsnorm_closed_forms():
     # a plain-numpy restatement in float64 (mean of squares, rsqrt, silu)
     ref = (o / np.sqrt((o.astype(np.float64) ** 2).mean(-1, keepdims=True))) * w * (z / (1 + np.exp(-z.astype(np.float64))))
     np.testing.assert_allclose(y1, ref, rtol=2e-6, atol=1e-7)
+
+
+# --------------------------------------------------------------------------
+# state hand-off formats (hf_state.npz)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["cu_t1", "cu_t3"])
+def test_conv_update_vs_hf(golden, name):
+    d = golden("hf_state.npz")
+    out, st = orc.causal_conv1d_update(d[f"{name}_x"], d[f"{name}_state0"], d[f"{name}_w"],
+                                       bool(d[f"{name}_silu"]))
+    # HF's F.conv1d sums the four taps in its own order: a few fp32 ulps
+    np.testing.assert_allclose(out, d[f"{name}_out"], rtol=1e-5, atol=1e-6)
+    assert bits_equal(st, d[f"{name}_state"])   # the state is a pure shift
+
+
+def test_conv_update_continues_kai_conv():
+    """A sequence prefilled by the kai conv and continued by decode steps on
+    the HF state layout is bit-identical to the kai conv over the whole
+    sequence (both in the reference's tap order)."""
+    rs = np.random.RandomState(12)
+    T, N, C = 37, 5, 19
+    x = rs.randn(T + N, C).astype(np.float32)
+    w_kai = rs.randn(4, C).astype(np.float32)          # kai layout [4][C]
+    full, _ = orc.conv_f32(x.ravel(), w_kai.ravel(), np.zeros(3 * C, np.float32), T + N, C, silu=True)
+    pre, hist = orc.conv_f32(x[:T].ravel(), w_kai.ravel(), np.zeros(3 * C, np.float32), T, C, silu=True)
+    st = orc.conv_hist_to_state(hist.reshape(1, 3, C))
+    expect = orc.conv_state_from_inputs(x[None, :T])
+    expect[:, :, 0] = 0.0                      # the dead entry hist -> state writes
+    assert bits_equal(st, expect)
+    outs = []
+    for t in range(T, T + N):
+        o, st = orc.causal_conv1d_update(x[None, t:t + 1], st, np.ascontiguousarray(w_kai.T), True)
+        outs.append(o[0, 0])
+    assert bits_equal(np.concatenate([pre.reshape(T, C), np.stack(outs)]), full.reshape(T + N, C))
+
+
+@pytest.mark.parametrize("name", ["cs_t2", "cs_t7"])
+def test_conv_state_from_inputs_vs_hf_cache(golden, name):
+    d = golden("hf_state.npz")
+    assert bits_equal(orc.conv_state_from_inputs(d[f"{name}_x"]), d[f"{name}_state"])
+
+
+def test_conv_hist_state_round_trip():
+    rs = np.random.RandomState(4)
+    st = rs.randn(3, 11, 4).astype(np.float32)
+    hist = orc.conv_state_to_hist(st)
+    assert hist.shape == (3, 3, 11) and bits_equal(hist[:, 0, :], st[:, :, 1])
+    assert bits_equal(hist[:, 2, :], st[:, :, 3])
+    back = orc.conv_hist_to_state(hist)
+    assert bits_equal(back[:, :, 1:], st[:, :, 1:]) and np.all(back[:, :, 0] == 0)
