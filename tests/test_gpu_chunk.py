@@ -118,6 +118,31 @@ def test_prefill_segments_vs_oracle(L):
         check(Sg, S_ref, T, f"state T={T}")
 
 
+@pytest.mark.parametrize("gate", ["weak", "strong", "extreme", "mixed"])
+def test_prefill_decay_regimes(L, gate):
+    """Decay regimes, as per-token log-gates: weak -0.01 (the state is kept
+    for thousands of tokens), strong -1.2 (each chunk decays by about
+    e^-77), extreme -5 (e^G underflows to 0 inside a chunk: the state and
+    the transitions are forgotten), mixed: chunks alternating between -0.6
+    and -0.05.  T = 1000 (16 chunks, one segment) and T = 1600 at 32 heads
+    (segments whose start states are composed from those transitions)."""
+    for T, Hv, Hk in ((1000, 2, 1), (1600, 32, 16)):
+        q, k, v, g, beta, S = prefill_inputs(77, 1, T, Hv, Hk)
+        if gate == "weak":
+            g[:] = -0.01
+        elif gate == "strong":
+            g[:] = -1.2
+        elif gate == "extreme":
+            g[:] = -5.0
+        else:
+            chunk = np.arange(T) // 64
+            g[:] = np.where(chunk % 2 == 0, -0.6, -0.05)[None, :, None]
+        o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+        o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, T, Hv, Hk, 128, 128, 64)
+        check(o, o_ref, T, f"{gate} T={T} output")
+        check(Sg, S_ref, T, f"{gate} T={T} state")
+
+
 def test_prefill_positive_log_gates(L):
     """Log-gates of either sign (the kernel must not assume g <= 0): the
     Gamma factors exp(G_i - G_j) then exceed 1 inside a chunk."""
