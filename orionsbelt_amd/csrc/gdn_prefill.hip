@@ -75,6 +75,7 @@ constexpr int D = kHeadDim;   // 128
 constexpr int NW = 8;         // waves per workgroup
 constexpr int NT = 64 * NW;   // threads per workgroup
 constexpr int NSW = 4;        // state waves (the first four)
+constexpr int kMaxSegs = 64;  // segments of one sequence
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
@@ -693,7 +694,8 @@ struct SegArgs {
     uint16_t *o;
     void *S;          // initial state in, final state out
     float *carry;
-    int T, Hv, Hk, NC, L, P;
+    int T, Hv, Hk, NC, P;
+    int bnd[kMaxSegs + 1];  // segment p covers chunks [bnd[p], bnd[p+1])
     float q_scale;
 };
 
@@ -1160,7 +1162,7 @@ __global__ __launch_bounds__(NT) void prefill_pass1_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
     const int h = head_of(blockIdx.x, a.Hv), p = blockIdx.y, b = blockIdx.z;
-    const int n0 = p * a.L, n1 = min(a.NC, n0 + a.L);
+    const int n0 = a.bnd[p], n1 = a.bnd[p + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int g = lane >> 4, r = lane & 15;
     if (p == 0) {
@@ -1205,7 +1207,7 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
     const int h = head_of(blockIdx.x, a.Hv), p = blockIdx.y + 1, b = blockIdx.z;
-    const int n0 = p * a.L, n1 = min(a.NC, n0 + a.L);
+    const int n0 = a.bnd[p], n1 = a.bnd[p + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int g = lane >> 4, r = lane & 15;
     f32x4_t S[8][2];
@@ -1226,33 +1228,108 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
     }
 }
 
-// Segments: enough middle segments that a pass fills the device (about 256
-// workgroups), at least kMinSegChunks chunks each; P = 2 would only
-// serialise, so it falls back to 1.
+// Segments.  P: enough that a pass fills the device (about 256 workgroups),
+// at least kMinSegChunks chunks per segment on average, at most kMaxSegs;
+// P = 2 would only serialise, so it falls back to 1.  Lengths: segment 0
+// runs with outputs in pass 1 only; segments 1 .. P-2 run their transition
+// in pass 1 (kCostTrans per chunk, relative to a chunk with outputs) and
+// rerun with outputs in pass 2 after composing their start state
+// (kCostPrologue + kCostStep per transition composed); segment P-1 runs in
+// pass 2 only.  The lengths minimise the modelled pass 1 + pass 2 time:
+// transitions share one cap M, segment 0 takes kCostTrans * M, and the
+// pass-2 segments shrink with their composition cost.  The costs are
+// measured per-chunk times of the kernels (shader-clock counters).
 constexpr int kMinSegChunks = 8;
 constexpr int kTargetWgs = 256;
+constexpr double kCostTrans = 1.17, kCostStep = 1.12, kCostPrologue = 0.5;
 
-void plan_segments(int B, int Hv, int NC, int &P, int &L) {
-    const int bh = B * Hv;
-    int want = 1 + (kTargetWgs + bh - 1) / bh;
-    const int cap = NC / kMinSegChunks;
-    if (want > cap) want = cap;
-    if (want < 3) want = 1;
-    P = want;
-    L = (NC + P - 1) / P;
-    P = (NC + L - 1) / L;  // drop empty trailing segments
-    if (P < 3) {
-        P = 1;
-        L = NC;
+struct SegPlan {
+    int P;
+    int bnd[kMaxSegs + 1];
+};
+
+// Lengths of pass-2 segments p = 1 .. P-1 under the pass-2 bound X, the
+// transitions capped at M: len[p] = clamp(floor(X - prologue(p)), 1, M).
+int pass2_lengths(int P, int M, double X, int *len) {
+    int sum = 0;
+    for (int p = 1; p < P; ++p) {
+        int l = (int)floor(X - kCostPrologue - kCostStep * (p - 1));
+        if (p < P - 1 && l > M) l = M;
+        if (l < 1) l = 1;
+        len[p] = l;
+        sum += l;
     }
+    return sum;
+}
+
+double plan_cost(int P, const int *len) {
+    double t1 = len[0], t2 = 0.0;
+    for (int p = 1; p < P; ++p) {
+        if (p < P - 1) t1 = fmax(t1, kCostTrans * len[p]);
+        t2 = fmax(t2, kCostPrologue + kCostStep * (p - 1) + len[p]);
+    }
+    return t1 + t2;
+}
+
+void plan_segments(int B, int Hv, int NC, SegPlan &pl) {
+    const int bh = B * Hv;
+    int P = 1 + (kTargetWgs + bh - 1) / bh;
+    P = min(P, NC / kMinSegChunks);
+    P = min(P, kMaxSegs);
+    if (P < 3) {
+        pl.P = 1;
+        pl.bnd[0] = 0;
+        pl.bnd[1] = NC;
+        return;
+    }
+    int best[kMaxSegs], len[kMaxSegs];
+    double best_cost = 1e30;
+    const int m_max = min(NC, 2 * NC / (P - 1) + 1);  // the cap is near NC / (P - 1)
+    for (int M = 1; M <= m_max; ++M) {
+        len[0] = min(NC - (P - 1), (int)floor(kCostTrans * M));
+        const int rem = NC - len[0];
+        if (rem < P - 1 || pass2_lengths(P, M, 1e9, len) < rem) continue;
+        double lo = 0.0, hi = NC + kCostPrologue + kCostStep * P;  // pass-2 bound X
+        for (int it = 0; it < 40; ++it) {
+            const double mid = 0.5 * (lo + hi);
+            (pass2_lengths(P, M, mid, len) >= rem ? hi : lo) = mid;
+        }
+        int sum = pass2_lengths(P, M, hi, len);
+        for (int p = P - 1; p >= 1 && sum > rem; --p) {  // trim the excess from the end
+            const int cut = min(sum - rem, len[p] - 1);
+            len[p] -= cut;
+            sum -= cut;
+        }
+        if (sum != rem) continue;
+        const double cost = plan_cost(P, len);
+        if (cost < best_cost) {
+            best_cost = cost;
+            for (int p = 0; p < P; ++p) best[p] = len[p];
+        }
+    }
+    pl.P = P;
+    pl.bnd[0] = 0;
+    for (int p = 0; p < P; ++p) pl.bnd[p + 1] = pl.bnd[p] + best[p];
+}
+
+// The plan of the last shape asked for on this thread (a layer calls the
+// prefill with one shape over and over).
+const SegPlan &cached_plan(int B, int Hv, int NC) {
+    thread_local int key_bh = -1, key_nc = -1;
+    thread_local SegPlan plan;
+    if (key_bh != B * Hv || key_nc != NC) {
+        plan_segments(B, Hv, NC, plan);
+        key_bh = B * Hv;
+        key_nc = NC;
+    }
+    return plan;
 }
 
 }  // namespace
 
 size_t prefill_carry_bytes(int B, int T, int Hv) {
     const int NC = (T + C - 1) / C;
-    int P, L;
-    plan_segments(B, Hv, NC, P, L);
+    const int P = cached_plan(B, Hv, NC).P;
     return P > 1 ? (size_t)B * Hv * P * 3 * D * D * sizeof(float) : 0;
 }
 
@@ -1277,7 +1354,11 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
     a.Hk = Hk;
     a.NC = NC;
     a.q_scale = q_scale;
-    plan_segments(B, Hv, NC, a.P, a.L);
+    {
+        const SegPlan &pl = cached_plan(B, Hv, NC);
+        a.P = pl.P;
+        for (int p = 0; p <= pl.P; ++p) a.bnd[p] = pl.bnd[p];
+    }
     if (a.P > 1 && !carry) return hipErrorInvalidValue;
     static_assert(sizeof(CombSmem) <= sizeof(Smem), "the start-state staging reuses the chunk LDS");
     static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget");
