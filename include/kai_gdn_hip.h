@@ -222,6 +222,27 @@ int kai_run_gdn_conv_hist_to_state_f32_hip(const float *hist, float *conv_state,
 #define KAI_GDN_FMT_BF16 2
 int kai_run_gdn_state_convert_hip(const void *src, int src_format, void *dst,
                                   int dst_format, size_t count, void *stream);
+/* ---- matmuls of the hybrid decode loop ------------------------------------
+ * int8 weight-only matmul, fp16 activations, per-output-channel symmetric
+ * weight scales: the reference's INT8_WEIGHTS matmul (gdn_e2e_decode.c:
+ * quantize_weight:175-199, gemv_int8_neon:296-359), with the weights stored
+ * output-major (Wq[N][K], row n = output channel n) so that MFMA operands
+ * are contiguous bytes.
+ *   y[m][n] = scale[n] * sum_k x[m][k] * Wq[n][k]      (fp32 accumulation)
+ * x [M][K] fp16 bit patterns, y [M][N] fp32, 1 <= M <= 16 (the batch),
+ * N % 16 == 0, K % 256 == 0, pointers 16-byte aligned.  Narrow layers split
+ * k across blocks into `workspace` (at least
+ * kai_gdn_w8a16_gemm_workspace_bytes(M, N, K) bytes, 0 = none needed) and
+ * reduce it in a fixed order: results are deterministic. */
+size_t kai_gdn_w8a16_gemm_workspace_bytes(int M, int N, int K);
+int kai_run_gdn_w8a16_gemm_hip(const uint16_t *x, const int8_t *Wq, const float *scale,
+                               float *y, int M, int N, int K, void *workspace,
+                               size_t workspace_bytes, void *stream);
+/* Quantise W[N][K] fp32 per output channel (row): scale[n] = max|W[n]|/127
+ * (1 for an all-zero row), Wq = clamp(round_half_away(W * (1/scale)),
+ * -128, 127), as the reference's quantize_weight does per column. */
+int kai_run_gdn_w8_quantize_hip(const float *W, int8_t *Wq, float *scale, int N, int K,
+                                void *stream);
 /* ---- library ------------------------------------------------------------ */
 
 /* Initialise the HIP runtime state of the current device (optional; every

@@ -553,3 +553,40 @@ void orc_causal_conv1d_update_f32(const float *x, float *conv_state, const float
             }
         }
 }
+
+/* ---- int8 weight-only matmul (see header) --------------------------------- */
+
+void orc_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K) {
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n) {
+        const float *row = W + (size_t)n * K;
+        float max_abs = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const float v = fabsf(row[k]);
+            if (v > max_abs) max_abs = v;
+        }
+        const float s = max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
+        const float inv = 1.0f / s;
+        scale[n] = s;
+        for (int k = 0; k < K; ++k) {
+            long vi = lroundf(row[k] * inv);
+            if (vi > 127) vi = 127;
+            if (vi < -128) vi = -128;
+            Wq[(size_t)n * K + k] = (int8_t)vi;
+        }
+    }
+}
+
+static float f16_bits_to_float(uint16_t h) { return orc_f16_to_f32(h); }
+
+void orc_w8_gemm(const uint16_t *x, const int8_t *Wq, const float *scale, float *y, int M,
+                 int N, int K) {
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n)
+        for (int m = 0; m < M; ++m) {
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k)
+                acc += (double)f16_bits_to_float(x[(size_t)m * K + k]) * Wq[(size_t)n * K + k];
+            y[(size_t)m * N + n] = (float)acc * scale[n];
+        }
+}

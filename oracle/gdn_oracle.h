@@ -36,6 +36,9 @@
  *                              (tolerance: HF's conv sums in another order)
  *                              and bit-identity with orc_causal_dwconv1d over
  *                              the whole sequence (continuation).
+ *   orc_w8_quantize, orc_w8_gemm -- closed forms (the largest weight maps
+ *                              to +-127, halves round away from zero, zero
+ *                              rows); a float64 numpy restatement.
  *   orc_gated_rmsnorm_*     -- golden vectors of HF Qwen3_5RMSNormGated in
  *                              fp32 and bf16; closed forms (constant rows,
  *                              z = 0 gives 0, w scales linearly).
@@ -184,6 +187,18 @@ void orc_gated_rmsnorm_bf16(const uint16_t *o, const uint16_t *z, const uint16_t
  *   state <- (s1, s2, s3, x). */
 void orc_causal_conv1d_update_f32(const float *x, float *conv_state, const float *w,
                                   float *out, int B, int T, size_t C, int silu);
+
+/* int8 weight-only matmul of the hybrid decode loop (the reference's
+ * INT8_WEIGHTS path, gdn_e2e_decode.c).  orc_w8_quantize restates
+ * quantize_weight (:175-199) on the rows of W[N][K] (the reference quantises
+ * the columns of its [K][N] layout): scale = max|w| / 127 (1 for a zero
+ * row), q = clamp(lroundf(w * (1 / scale)), -128, 127).  orc_w8_gemm:
+ * y[m][n] = scale[n] * sum_k x[m][k] q[n][k] with x fp16 bit patterns, the
+ * sum in double, rounded to fp32 once, then scaled (gemv_int8_neon
+ * (:296-359) sums in fp32 and scales per column). */
+void orc_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K);
+void orc_w8_gemm(const uint16_t *x, const int8_t *Wq, const float *scale, float *y, int M,
+                 int N, int K);
 
 /* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
 int orc_num_threads(void);

@@ -257,6 +257,33 @@ def conv_hist_to_state(hist):
     return st
 
 
+# ---- hybrid decode loop matmuls ----------------------------------------------
+
+_i8p = ctypes.POINTER(ctypes.c_int8)
+
+
+def w8_quantize(W):
+    """Per-output-channel symmetric int8 of W [N][K] fp32 -> (Wq int8, scale)."""
+    W = np.ascontiguousarray(W, np.float32)
+    N, K = W.shape
+    Wq = np.empty((N, K), np.int8)
+    sc = np.empty(N, np.float32)
+    lib().orc_w8_quantize(P(W), Wq.ctypes.data_as(_i8p), P(sc), _int(N), _int(K))
+    return Wq, sc
+
+
+def w8_gemm(x16, Wq, scale):
+    """y [M][N] fp32 from x [M][K] fp16 bits, Wq [N][K] int8, scale [N]."""
+    x16 = np.ascontiguousarray(x16, np.uint16)
+    Wq = np.ascontiguousarray(Wq, np.int8)
+    M, K = x16.shape
+    N = Wq.shape[0]
+    y = np.empty((M, N), np.float32)
+    lib().orc_w8_gemm(P(x16), Wq.ctypes.data_as(_i8p), P(np.ascontiguousarray(scale, np.float32)),
+                      P(y), _int(M), _int(N), _int(K))
+    return y
+
+
 def num_threads() -> int:
     return lib().orc_num_threads()
 

@@ -44,6 +44,9 @@ HIP_SYMBOLS = (
     "kai_run_gdn_conv_state_to_hist_f32_hip",
     "kai_run_gdn_conv_hist_to_state_f32_hip",
     "kai_run_gdn_state_convert_hip",
+    "kai_gdn_w8a16_gemm_workspace_bytes",
+    "kai_run_gdn_w8a16_gemm_hip",
+    "kai_run_gdn_w8_quantize_hip",
     "kai_gdn_hip_init",
     "kai_gdn_hip_error_string",
     "kai_gdn_hip_check_device_error",
@@ -91,6 +94,9 @@ _SIGS = {
     "kai_run_gdn_conv_state_to_hist_f32_hip": (_i, [_vp, _vp, _i, _sz, _vp]),
     "kai_run_gdn_conv_hist_to_state_f32_hip": (_i, [_vp, _vp, _i, _sz, _vp]),
     "kai_run_gdn_state_convert_hip": (_i, [_vp, _i, _vp, _i, _sz, _vp]),
+    "kai_gdn_w8a16_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kai_run_gdn_w8a16_gemm_hip": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "kai_run_gdn_w8_quantize_hip": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "kai_gdn_hip_init": (_i, []),
     "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
     "kai_gdn_hip_check_device_error": (_i, []),

@@ -101,4 +101,15 @@ hipError_t launch_conv_hist_state(bool to_hist, float *hist, float *conv_state, 
 // Element conversion between kF32, kF16 and kBF16 arrays.
 hipError_t launch_convert(const void *src, int sf, void *dst, int df, size_t n, hipStream_t st);
 
+// ---- hybrid decode loop matmuls (gdn_model.hip) ------------------------------
+
+// y[M][N] fp32 = scale[N] * (x[M][K] fp16 . Wq[N][K]^T int8), M <= 16,
+// N % 16 == 0, K % 256 == 0; `workspace` holds w8_workspace_bytes(M, N, K).
+int w8_splits(int N, int K);
+size_t w8_workspace_bytes(int M, int N, int K);
+hipError_t launch_w8_gemm(const uint16_t *x, const int8_t *W, const float *scale, float *y, int M,
+                          int N, int K, float *workspace, hipStream_t st);
+// Per-output-channel symmetric int8 quantisation of W[N][K] fp32.
+hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K, hipStream_t st);
+
 }  // namespace gdn

@@ -555,6 +555,36 @@ extern "C" int kai_run_gdn_state_convert_hip(const void *src, int src_format, vo
     return (int)gdn::launch_convert(src, src_format, dst, dst_format, count, (hipStream_t)stream);
 }
 
+// ---- hybrid decode loop: int8 weight-only matmul ---------------------------
+
+extern "C" size_t kai_gdn_w8a16_gemm_workspace_bytes(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || N % 16 || K % 256) return 0;
+    return gdn::w8_workspace_bytes(M, N, K);
+}
+
+extern "C" int kai_run_gdn_w8a16_gemm_hip(const uint16_t *x, const int8_t *Wq, const float *scale,
+                                          float *y, int M, int N, int K, void *workspace,
+                                          size_t workspace_bytes, void *stream) {
+    if (M < 0 || M > 16 || N < 0 || K <= 0 || N % 16 || K % 256) return (int)hipErrorInvalidValue;
+    if (M == 0 || N == 0) return 0;
+    if (!x || !Wq || !scale || !y) return (int)hipErrorInvalidValue;
+    if (!aligned(x, 16) || !aligned(Wq, 16) || !aligned(scale, 16) || !aligned(y, 16))
+        return (int)hipErrorInvalidValue;
+    const size_t need = gdn::w8_workspace_bytes(M, N, K);
+    if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
+        return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_w8_gemm(x, Wq, scale, y, M, N, K, static_cast<float *>(workspace),
+                                    (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_w8_quantize_hip(const float *W, int8_t *Wq, float *scale, int N, int K,
+                                           void *stream) {
+    if (N < 0 || K < 0) return (int)hipErrorInvalidValue;
+    if (N == 0 || K == 0) return 0;
+    if (!W || !Wq || !scale) return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_w8_quantize(W, Wq, scale, N, K, (hipStream_t)stream);
+}
+
 // ===========================================================================
 // Reference kai symbols (synchronous, host or device pointers)
 // ===========================================================================

@@ -537,3 +537,38 @@ def test_conv_hist_state_round_trip():
     assert bits_equal(hist[:, 2, :], st[:, :, 3])
     back = orc.conv_hist_to_state(hist)
     assert bits_equal(back[:, :, 1:], st[:, :, 1:]) and np.all(back[:, :, 0] == 0)
+
+
+# --------------------------------------------------------------------------
+# int8 weight-only matmul of the hybrid decode loop
+# --------------------------------------------------------------------------
+
+def test_w8_quantize_closed_forms():
+    W = np.array([[0.5, -1.0, 0.25, 0.0],      # max 1 -> scale 1/127
+                  [0.0, 0.0, 0.0, 0.0],        # zero row -> scale 1, q = 0
+                  [3.0, -3.0, 1.5, 0.01]], np.float32)
+    q, s = orc.w8_quantize(W)
+    assert s[1] == 1.0 and np.all(q[1] == 0)
+    assert q[0, 1] == -127 and q[2, 0] == 127 and q[2, 1] == -127
+    assert s[0] == np.float32(1.0) / np.float32(127.0)
+    # 0.5 * 127 = 63.5 rounds away from zero (lroundf), 0.25 * 127 = 31.75 -> 32
+    assert q[0, 0] == 64 and q[0, 2] == 32
+    assert q[2, 2] == 64                        # 1.5 / (3/127) = 63.5 -> 64
+    rs = np.random.RandomState(2)
+    W = rs.randn(40, 96).astype(np.float32)
+    q, s = orc.w8_quantize(W)
+    assert np.all(np.abs(q).max(axis=1) == 127)
+    np.testing.assert_allclose(q * s[:, None], W, atol=0.5 * s.max() * 1.0001)
+
+
+def test_w8_gemm_vs_numpy():
+    rs = np.random.RandomState(3)
+    M, N, K = 5, 48, 256
+    x = rs.randn(M, K).astype(np.float16)
+    W = rs.randn(N, K).astype(np.float32)
+    q, s = orc.w8_quantize(W)
+    y = orc.w8_gemm(x.view(np.uint16), q, s)
+    ref = (x.astype(np.float64) @ q.astype(np.float64).T).astype(np.float32) * s
+    assert np.array_equal(y, ref)
+    # a transposed operand or a dropped scale fails
+    assert not np.allclose(y, (x.astype(np.float64) @ q.astype(np.float64).T).astype(np.float32))
