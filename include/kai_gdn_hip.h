@@ -243,6 +243,22 @@ int kai_run_gdn_w8a16_gemm_hip(const uint16_t *x, const int8_t *Wq, const float 
  * -128, 127), as the reference's quantize_weight does per column. */
 int kai_run_gdn_w8_quantize_hip(const float *W, int8_t *Wq, float *scale, int N, int K,
                                 void *stream);
+/* Attention decode of the hybrid loop's full-attention layers (HF
+ * Qwen3_5Attention with a KV cache, modeling_qwen3_5.py:629-701, and
+ * eager_attention_forward:606-627; the reference's GQA attention,
+ * gdn_e2e_decode.c:1532-1634): one new token per sequence,
+ *   out[b][h] = softmax_t(scaling * q[b][h] . K[b][kv][t]) . V[b][kv][t],
+ *   t < length, kv = h / (num_q_heads / num_kv_heads)
+ * q [batch][num_q_heads][256] fp16 (after q_norm and RoPE), k_cache, v_cache
+ * [batch][num_kv_heads][max_len][256] fp16, out fp32; softmax and sums in
+ * fp32.  num_q_heads / num_kv_heads <= 4.  `workspace` holds at least
+ * kai_gdn_attn_decode_workspace_bytes(batch, num_q_heads, length) bytes. */
+size_t kai_gdn_attn_decode_workspace_bytes(int batch, int num_q_heads, int length);
+int kai_run_gdn_attn_decode_f16kv_hip(const uint16_t *q, const uint16_t *k_cache,
+                                      const uint16_t *v_cache, float *out, int batch,
+                                      int num_q_heads, int num_kv_heads, int max_len,
+                                      int length, float scaling, void *workspace,
+                                      size_t workspace_bytes, void *stream);
 /* ---- library ------------------------------------------------------------ */
 
 /* Initialise the HIP runtime state of the current device (optional; every

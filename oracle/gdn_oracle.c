@@ -590,3 +590,35 @@ void orc_w8_gemm(const uint16_t *x, const int8_t *Wq, const float *scale, float 
             y[(size_t)m * N + n] = (float)acc * scale[n];
         }
 }
+
+/* ---- attention decode (see header) ---------------------------------------- */
+
+void orc_attn_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out, int B,
+                     int Hq, int Hkv, int Tmax, int L, int D, float scaling) {
+    const int rep = Hq / Hkv;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < Hq; ++h) {
+            const int kv = h / rep;
+            const uint16_t *qh = q + ((size_t)b * Hq + h) * D;
+            const size_t base = ((size_t)b * Hkv + kv) * Tmax;
+            double *s = malloc(sizeof(double) * L), mx = -1e300, sum = 0.0;
+            for (int t = 0; t < L; ++t) {
+                double dot = 0.0;
+                for (int d = 0; d < D; ++d)
+                    dot += (double)orc_f16_to_f32(qh[d]) * orc_f16_to_f32(k[(base + t) * D + d]);
+                s[t] = dot * scaling;
+                if (s[t] > mx) mx = s[t];
+            }
+            for (int t = 0; t < L; ++t) {
+                s[t] = exp(s[t] - mx);
+                sum += s[t];
+            }
+            for (int d = 0; d < D; ++d) {
+                double acc = 0.0;
+                for (int t = 0; t < L; ++t) acc += s[t] * orc_f16_to_f32(v[(base + t) * D + d]);
+                out[((size_t)b * Hq + h) * D + d] = (float)(acc / sum);
+            }
+            free(s);
+        }
+}

@@ -39,6 +39,10 @@
  *   orc_w8_quantize, orc_w8_gemm -- closed forms (the largest weight maps
  *                              to +-127, halves round away from zero, zero
  *                              rows); a float64 numpy restatement.
+ *   orc_attn_decode         -- closed forms (one position returns its v; equal
+ *                              scores average the values; a dominant score
+ *                              selects one value) and a float64 numpy
+ *                              restatement of softmax(q K^T) V.
  *   orc_gated_rmsnorm_*     -- golden vectors of HF Qwen3_5RMSNormGated in
  *                              fp32 and bf16; closed forms (constant rows,
  *                              z = 0 gives 0, w scales linearly).
@@ -199,6 +203,13 @@ void orc_causal_conv1d_update_f32(const float *x, float *conv_state, const float
 void orc_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K);
 void orc_w8_gemm(const uint16_t *x, const int8_t *Wq, const float *scale, float *y, int M,
                  int N, int K);
+
+/* Attention decode over an fp16 KV cache (HF eager_attention_forward with
+ * repeat_kv, modeling_qwen3_5.py:606-627): q [B][Hq][D], k, v
+ * [B][Hkv][Tmax][D] fp16 bits, out [B][Hq][D] fp32; softmax and sums in
+ * double. */
+void orc_attn_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out, int B,
+                     int Hq, int Hkv, int Tmax, int L, int D, float scaling);
 
 /* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
 int orc_num_threads(void);

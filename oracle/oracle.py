@@ -284,6 +284,20 @@ def w8_gemm(x16, Wq, scale):
     return y
 
 
+def attn_decode(q16, k16, v16, L, scaling):
+    """softmax(scaling q K^T) V over the first L positions; q [B][Hq][D],
+    k, v [B][Hkv][Tmax][D] fp16 bits -> out [B][Hq][D] fp32."""
+    q16 = np.ascontiguousarray(q16, np.uint16)
+    k16 = np.ascontiguousarray(k16, np.uint16)
+    v16 = np.ascontiguousarray(v16, np.uint16)
+    B, Hq, D = q16.shape
+    Hkv, Tmax = k16.shape[1], k16.shape[2]
+    out = np.empty((B, Hq, D), np.float32)
+    lib().orc_attn_decode(P(q16), P(k16), P(v16), P(out), _int(B), _int(Hq), _int(Hkv), _int(Tmax),
+                          _int(L), _int(D), _flt(scaling))
+    return out
+
+
 def num_threads() -> int:
     return lib().orc_num_threads()
 

@@ -47,6 +47,8 @@ HIP_SYMBOLS = (
     "kai_gdn_w8a16_gemm_workspace_bytes",
     "kai_run_gdn_w8a16_gemm_hip",
     "kai_run_gdn_w8_quantize_hip",
+    "kai_gdn_attn_decode_workspace_bytes",
+    "kai_run_gdn_attn_decode_f16kv_hip",
     "kai_gdn_hip_init",
     "kai_gdn_hip_error_string",
     "kai_gdn_hip_check_device_error",
@@ -97,6 +99,9 @@ _SIGS = {
     "kai_gdn_w8a16_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
     "kai_run_gdn_w8a16_gemm_hip": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "kai_run_gdn_w8_quantize_hip": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "kai_gdn_attn_decode_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kai_run_gdn_attn_decode_f16kv_hip":
+        (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "kai_gdn_hip_init": (_i, []),
     "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
     "kai_gdn_hip_check_device_error": (_i, []),

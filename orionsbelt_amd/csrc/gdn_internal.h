@@ -111,5 +111,11 @@ hipError_t launch_w8_gemm(const uint16_t *x, const int8_t *W, const float *scale
                           int N, int K, float *workspace, hipStream_t st);
 // Per-output-channel symmetric int8 quantisation of W[N][K] fp32.
 hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K, hipStream_t st);
+// Attention decode over an fp16 KV cache (head_dim 256, Hq / Hkv <= 4):
+// out [B][Hq][256] fp32; `workspace` holds attn_workspace_bytes(B, Hq, L).
+size_t attn_workspace_bytes(int B, int Hq, int L);
+hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
+                              int B, int Hq, int Hkv, int Tmax, int L, float scaling, float *workspace,
+                              hipStream_t st);
 
 }  // namespace gdn

@@ -177,4 +177,195 @@ hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, i
     return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// Attention decode (HF Qwen3_5Attention with a KV cache, one new token per
+// sequence; eager_attention_forward, modeling_qwen3_5.py:606-627): for query
+// head h of sequence b, with kv = h / (Hq / Hkv) (repeat_kv),
+//   o[b][h] = softmax_t(scaling * q[b][h] . K[b][kv][t]) . V[b][kv][t],  t < L
+// q [B][Hq][256] fp16, K, V [B][Hkv][Tmax][256] fp16, fp32 softmax and sums.
+// Split over the sequence: block (span, kv, b) takes positions [256 span,
+// 256 span + 256) and every query head of kv; wave w takes 64 of them in
+// groups of 16.  Scores on fp16 MFMA 16x16x32 (A = 16 key rows, B = the
+// group's query heads as columns); online softmax per head in exp2; P.V on
+// the VALU, lane l holding dims 4l .. 4l+3 of every head's output.  The
+// block's four waves merge through LDS into one partial (max, sum, o) per
+// head; attn_combine_kernel merges the spans.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kAttD = 256;
+constexpr int kAttSpan = 256;   // positions per block
+constexpr int kAttRepMax = 4;   // query heads per kv head handled (Hq / Hkv <= 4)
+constexpr int kAttPart = kAttD + 2;
+
+__global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__restrict__ q,
+                                                          const uint16_t *__restrict__ Kc,
+                                                          const uint16_t *__restrict__ Vc,
+                                                          float *__restrict__ part, int Hq, int Hkv,
+                                                          int Tmax, int L, int nspan, float sc_log2) {
+    __shared__ float s_m[4][kAttRepMax], s_l[4][kAttRepMax];
+    __shared__ float s_o[4][kAttRepMax][kAttD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int span = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
+    const int rep = Hq / Hkv;
+    const size_t kvrow = ((size_t)b * Hkv + kv) * Tmax;  // row of position 0
+    // B operand: query head r of the group (zero columns past rep), dims
+    // 32 j + 8 g .. +7
+    f16x8_t qb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        u32x4_t u = {0u, 0u, 0u, 0u};
+        if (r < rep) u = *reinterpret_cast<const u32x4_t *>(q + ((size_t)b * Hq + kv * rep + r) * kAttD + 32 * j + 8 * g);
+        qb[j] = __builtin_bit_cast(f16x8_t, u);
+    }
+    float m[kAttRepMax], l[kAttRepMax], o[kAttRepMax][4];
+#pragma unroll
+    for (int h = 0; h < kAttRepMax; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[h][i] = 0.f;
+    }
+    const int t_begin = span * kAttSpan + wave * 64;
+    for (int grp = 0; grp < 4; ++grp) {
+        const int t0 = t_begin + 16 * grp;
+        if (t0 >= L) break;  // uniform over the wave
+        const int tr = min(t0 + r, L - 1);  // key row of this lane (clamped; masked below)
+        const uint16_t *kp = Kc + (kvrow + tr) * kAttD + 8 * g;
+        f32x4_t acc = zero4();
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(f16x8_t, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(kp + 32 * j))),
+                qb[j], acc, 0, 0, 0);
+        // lane (g, r): scores of positions t0 + 4g + e for head r, in log2 units
+        float s[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] = (t0 + 4 * g + e < L) ? acc[e] * sc_log2 : -INFINITY;
+        float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // per head r (all lanes of column r agree); the new running max
+        float p[4], mrow = -INFINITY;
+#pragma unroll
+        for (int h = 0; h < kAttRepMax; ++h)
+            if (h == r) mrow = m[h];
+        const float mnew = fmaxf(mrow, mx);
+        float ps = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(s[e] - mnew);
+            ps += p[e];
+        }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);  // 0 on the first group
+        // every lane: the running state of each head from lane h
+#pragma unroll
+        for (int h = 0; h < kAttRepMax; ++h) {
+            if (h >= rep) break;
+            const float a_h = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
+            const float mn_h = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mnew), h));
+            const float ps_h = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ps), h));
+            m[h] = mn_h;
+            l[h] = l[h] * a_h + ps_h;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[h][i] *= a_h;
+        }
+        // P.V: position t0 + 4gg + e, head h: p in lane 16 gg + h, element e
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = t0 + 4 * gg + e;
+                if (t >= L) continue;  // uniform
+                const uint2 vv = *reinterpret_cast<const uint2 *>(Vc + (kvrow + t) * kAttD + 4 * lane);
+                const float v[4] = {f16_to_f32((uint16_t)(vv.x & 0xFFFFu)), f16_to_f32((uint16_t)(vv.x >> 16)),
+                                    f16_to_f32((uint16_t)(vv.y & 0xFFFFu)), f16_to_f32((uint16_t)(vv.y >> 16))};
+#pragma unroll
+                for (int h = 0; h < kAttRepMax; ++h) {
+                    if (h >= rep) break;
+                    const float ph = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[e]), 16 * gg + h));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o[h][i] += ph * v[i];
+                }
+            }
+    }
+    // merge the four waves (each may have seen no position: m = -inf, l = 0)
+    if (lane == 0)
+#pragma unroll
+        for (int h = 0; h < kAttRepMax; ++h) {
+            s_m[wave][h] = m[h];
+            s_l[wave][h] = l[h];
+        }
+#pragma unroll
+    for (int h = 0; h < kAttRepMax; ++h)
+        *reinterpret_cast<float4 *>(&s_o[wave][h][4 * lane]) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+    __syncthreads();
+    // thread (h, d): h = tid / 64, dims 4 (tid % 64) .. +3
+    const int h = threadIdx.x >> 6;
+    if (h >= rep) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][h]);
+    float lsum = 0.f, acc4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float f = s_m[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w][h] - M);
+        lsum += f * s_l[w][h];
+        const float4 ow = *reinterpret_cast<const float4 *>(&s_o[w][h][4 * lane]);
+        acc4[0] += f * ow.x;
+        acc4[1] += f * ow.y;
+        acc4[2] += f * ow.z;
+        acc4[3] += f * ow.w;
+    }
+    float *pp = part + (((size_t)b * Hq + kv * rep + h) * nspan + span) * kAttPart;
+    *reinterpret_cast<float4 *>(pp + 4 * lane) = make_float4(acc4[0], acc4[1], acc4[2], acc4[3]);
+    if (lane == 0) {
+        pp[kAttD] = M;
+        pp[kAttD + 1] = lsum;
+    }
+}
+
+// o[b][h][d] = sum_s e^{m_s - M} o_s[d] / sum_s e^{m_s - M} l_s (log2 units).
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part,
+                                                           float *__restrict__ out, int nspan) {
+    const size_t bh = blockIdx.x;
+    const float *pp = part + bh * nspan * kAttPart;
+    const int d = threadIdx.x;
+    float M = -INFINITY;
+    for (int s = 0; s < nspan; ++s) M = fmaxf(M, pp[s * kAttPart + kAttD]);
+    float lsum = 0.f, acc = 0.f;
+    for (int s = 0; s < nspan; ++s) {
+        const float ms = pp[s * kAttPart + kAttD];
+        const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+        lsum += f * pp[s * kAttPart + kAttD + 1];
+        acc += f * pp[s * kAttPart + d];
+    }
+    out[bh * kAttD + d] = acc / lsum;
+}
+
+}  // namespace
+
+size_t attn_workspace_bytes(int B, int Hq, int L) {
+    const int nspan = (L + kAttSpan - 1) / kAttSpan;
+    return (size_t)B * Hq * nspan * kAttPart * sizeof(float);
+}
+
+hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
+                              int B, int Hq, int Hkv, int Tmax, int L, float scaling, float *workspace,
+                              hipStream_t st) {
+    if (B == 0) return hipSuccess;
+    const int nspan = (L + kAttSpan - 1) / kAttSpan;
+    const float sc_log2 = scaling * 1.4426950408889634f;
+    attn_decode_kernel<<<dim3(nspan, Hkv, B), 256, 0, st>>>(q, Kc, Vc, workspace, Hq, Hkv, Tmax, L, nspan,
+                                                            sc_log2);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    attn_combine_kernel<<<dim3(B * Hq), kAttD, 0, st>>>(workspace, out, nspan);
+    return hipGetLastError();
+}
+
 }  // namespace gdn

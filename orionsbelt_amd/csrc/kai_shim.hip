@@ -585,6 +585,32 @@ extern "C" int kai_run_gdn_w8_quantize_hip(const float *W, int8_t *Wq, float *sc
     return (int)gdn::launch_w8_quantize(W, Wq, scale, N, K, (hipStream_t)stream);
 }
 
+extern "C" size_t kai_gdn_attn_decode_workspace_bytes(int batch, int num_q_heads, int length) {
+    if (batch <= 0 || num_q_heads <= 0 || length <= 0) return 0;
+    return gdn::attn_workspace_bytes(batch, num_q_heads, length);
+}
+
+extern "C" int kai_run_gdn_attn_decode_f16kv_hip(const uint16_t *q, const uint16_t *k_cache,
+                                                 const uint16_t *v_cache, float *out, int batch,
+                                                 int num_q_heads, int num_kv_heads, int max_len,
+                                                 int length, float scaling, void *workspace,
+                                                 size_t workspace_bytes, void *stream) {
+    if (batch < 0 || batch > 65535 || num_kv_heads <= 0 || num_q_heads <= 0 ||
+        num_q_heads % num_kv_heads || num_q_heads / num_kv_heads > 4 || num_kv_heads > 65535)
+        return (int)hipErrorInvalidValue;
+    if (length <= 0 || length > max_len) return (int)hipErrorInvalidValue;
+    if (batch == 0) return 0;
+    if (!q || !k_cache || !v_cache || !out || !workspace) return (int)hipErrorInvalidValue;
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 16) ||
+        !aligned(workspace, 16))
+        return (int)hipErrorInvalidValue;
+    if (workspace_bytes < gdn::attn_workspace_bytes(batch, num_q_heads, length))
+        return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_attn_decode(q, k_cache, v_cache, out, batch, num_q_heads, num_kv_heads,
+                                        max_len, length, scaling, static_cast<float *>(workspace),
+                                        (hipStream_t)stream);
+}
+
 // ===========================================================================
 // Reference kai symbols (synchronous, host or device pointers)
 // ===========================================================================

@@ -86,3 +86,76 @@ def test_w8a16_gemm_rejects_bad_args(L):
     off = ctypes.c_void_p(t.data_ptr() + 8)
     assert fn(off, P(t), P(t), P(t), 1, 32, 256, P(t), 1 << 20, stream()) != 0    # misaligned x
     assert fn(None, None, None, None, 0, 32, 256, None, 0, stream()) == 0         # nothing to do
+
+
+# ---- attention decode --------------------------------------------------------
+
+def gpu_attn(L, q16, k16, v16, length, scaling):
+    torch = torch_mod()
+    B, Hq, D = q16.shape
+    Hkv, Tmax = k16.shape[1], k16.shape[2]
+    dq, dk, dv = (dev(a.view(np.int16)) for a in (q16, k16, v16))
+    out = empty((B, Hq, D), torch.float32)
+    nb = L.kai_gdn_attn_decode_workspace_bytes(B, Hq, length)
+    ws = empty((nb // 4,), torch.float32)
+    rc = L.kai_run_gdn_attn_decode_f16kv_hip(P(dq), P(dk), P(dv), P(out), B, Hq, Hkv, Tmax, length,
+                                              scaling, P(ws), nb, stream())
+    assert rc == 0, rc
+    return host(out)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Tmax,length", [(1, 4, 1, 64, 1), (2, 16, 4, 300, 300),
+                                                   (3, 8, 4, 1000, 777), (1, 16, 4, 4096, 4096),
+                                                   (16, 16, 4, 640, 513)])
+def test_attn_decode_vs_oracle(L, B, Hq, Hkv, Tmax, length):
+    rs = np.random.RandomState(length + B)
+    D = 256
+    q = (rs.randn(B, Hq, D) * 0.5).astype(np.float16)
+    k = rs.randn(B, Hkv, Tmax, D).astype(np.float16)
+    v = rs.randn(B, Hkv, Tmax, D).astype(np.float16)
+    k[:, :, length:] = np.float16(1e4)                            # past the length: must not count
+    out = gpu_attn(L, q.view(np.uint16), k.view(np.uint16), v.view(np.uint16), length, 1 / 16)
+    ref = orc.attn_decode(q.view(np.uint16), k.view(np.uint16), v.view(np.uint16), length, 1 / 16)
+    np.testing.assert_allclose(out, ref, rtol=2e-5, atol=2e-5)
+
+
+def test_attn_decode_peaked_and_long(L):
+    """A dominant key selects its value (the softmax's max tracking across
+    spans and waves), at 32K positions."""
+    torch = torch_mod()
+    B, Hq, Hkv, T, D = 1, 16, 4, 32768, 256
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    k = (torch.randn(B, Hkv, T, D, generator=gen, device="cuda") * 0.1).half()
+    v = torch.randn(B, Hkv, T, D, generator=gen, device="cuda").half()
+    q = torch.zeros(B, Hq, D, device="cuda").half()
+    q[:, :, :] = 1.0
+    hot = [123, 20000, 32767, 5]                                 # one per kv head
+    for kv, t in enumerate(hot):
+        k[0, kv, t] = 2.0
+    out = torch.empty(B, Hq, D, device="cuda")
+    nb = L.kai_gdn_attn_decode_workspace_bytes(B, Hq, T)
+    ws = torch.empty(nb // 4, device="cuda")
+    assert L.kai_run_gdn_attn_decode_f16kv_hip(P(q), P(k), P(v), P(out), B, Hq, Hkv, T, T, 1 / 16,
+                                               P(ws), nb, stream()) == 0
+    torch.cuda.synchronize()
+    for h in range(Hq):
+        kv = h // 4
+        assert torch.allclose(out[0, h], v[0, kv, hot[kv]].float(), rtol=1e-3, atol=1e-3)
+
+
+def test_attn_decode_rejects_bad_args(L):
+    torch = torch_mod()
+    t = empty((1 << 16,), torch.float32)
+    fn = L.kai_run_gdn_attn_decode_f16kv_hip
+    args = [P(t), P(t), P(t), P(t), 1, 16, 4, 64, 64, 0.0625, P(t), 1 << 18, stream()]
+    bad = list(args); bad[5] = 15                                 # Hq % Hkv
+    assert fn(*bad) != 0
+    bad = list(args); bad[5] = 32                                 # Hq / Hkv > 4
+    assert fn(*bad) != 0
+    bad = list(args); bad[8] = 65                                 # length > max_len
+    assert fn(*bad) != 0
+    bad = list(args); bad[11] = 16                                # workspace short
+    assert fn(*bad) != 0
+    bad = list(args); bad[4] = 0                                  # nothing to do
+    assert fn(*bad) == 0

@@ -572,3 +572,27 @@ def test_w8_gemm_vs_numpy():
     assert np.array_equal(y, ref)
     # a transposed operand or a dropped scale fails
     assert not np.allclose(y, (x.astype(np.float64) @ q.astype(np.float64).T).astype(np.float32))
+
+
+def test_attn_decode_closed_forms():
+    rs = np.random.RandomState(6)
+    B, Hq, Hkv, T, D = 1, 4, 2, 5, 16
+    q = rs.randn(B, Hq, D).astype(np.float16)
+    k = rs.randn(B, Hkv, T, D).astype(np.float16)
+    v = rs.randn(B, Hkv, T, D).astype(np.float16)
+    bits = lambda a: a.view(np.uint16)  # noqa: E731
+    # one position: the output is its value row (each query head's own kv head)
+    o = orc.attn_decode(bits(q), bits(k), bits(v), 1, 0.25)
+    np.testing.assert_allclose(o[0, 0], v[0, 0, 0].astype(np.float32), rtol=1e-6)
+    np.testing.assert_allclose(o[0, 3], v[0, 1, 0].astype(np.float32), rtol=1e-6)
+    # equal scores (zero keys): the mean of the values
+    o = orc.attn_decode(bits(q), bits(np.zeros_like(k)), bits(v), T, 0.25)
+    np.testing.assert_allclose(o[0, 1], v[0, 0].astype(np.float64).mean(0), rtol=1e-6)
+    # float64 numpy restatement
+    o = orc.attn_decode(bits(q), bits(k), bits(v), T, 0.25)
+    kk = np.repeat(k.astype(np.float64), Hq // Hkv, axis=1)
+    vv = np.repeat(v.astype(np.float64), Hq // Hkv, axis=1)
+    s = np.einsum("bhd,bhtd->bht", q.astype(np.float64), kk) * 0.25
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    np.testing.assert_allclose(o, np.einsum("bht,bhtd->bhd", p, vv), rtol=1e-6, atol=1e-7)
