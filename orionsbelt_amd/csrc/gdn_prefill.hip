@@ -785,7 +785,9 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
             load_gates_all(sm, pslot(n + 2, n0), a.beta, b, h, a.Hv, c2, a.T, 1, lane);
             load_rows_n<16>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 0, lane);
         } else if (more) {
+            __builtin_amdgcn_s_setprio(2);
             kk(n + 1, hw == 1);
+            __builtin_amdgcn_s_setprio(0);
         }
         if (hw == 2) wait_vmem0();  // q rows of chunk n+1
         lds_barrier();              // X
