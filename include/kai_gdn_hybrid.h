@@ -1,0 +1,79 @@
+/*
+ * kai_gdn_hybrid.h -- the end-to-end hybrid decode loop of libkai_gdn_hip.so
+ * (gfx950): a random-init, Qwen3.5-shaped model of Gated DeltaNet and full
+ * attention layers with int8 per-output-channel weights and fp16
+ * activations, decoded one token per sequence per step.
+ *
+ * No reference kai symbol: the reference's loop is the C program
+ * src/orionsbelt/engines/cpu/kernels/gdn_e2e_decode.c (:1921-2865), which
+ * uses a simplified GDN and produces no logits.  The layer definitions
+ * followed here are HF transformers modeling_qwen3_5.py
+ * (Qwen3_5DecoderLayer:740-794: pre-norm, mixer, residual, post-norm,
+ * SwiGLU MLP, residual; Qwen3_5GatedDeltaNet:387-543; Qwen3_5Attention:
+ * 629-701 with q/k norm, partial rotary embedding and the sigmoid output
+ * gate; Qwen3_5RMSNorm:720-737, whose weight enters as 1 + w), with the
+ * residual stream kept in fp32 and every matmul input rounded to fp16.
+ *
+ * Weights, norms and gate parameters are drawn from a counter-based hash of
+ * (seed, tensor, index), so a CPU restatement draws the same model; matmul
+ * weights are quantised per output channel as the reference's
+ * quantize_weight does.  A context of `context` tokens is represented by
+ * states drawn the same way (KV caches, recurrent and conv states), which
+ * is what a prefill of that length leaves behind for the decode steps to
+ * read; a context of 0 starts empty, and tokens fed through
+ * kai_gdn_hybrid_step build the context for real.
+ *
+ * All functions return 0 or a hipError_t code (kai_gdn_hip_error_string).
+ */
+#ifndef KAI_GDN_HYBRID_H
+#define KAI_GDN_HYBRID_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kai_gdn_hybrid kai_gdn_hybrid;
+
+typedef struct {
+    int layers;      /* 32 */
+    int attn_every;  /* 4: layer i is full attention iff (i + 1) % attn_every == 0 */
+    int hidden;      /* 2560 (% 256 == 0) */
+    int inter;       /* 9216 (% 256 == 0) */
+    int vocab;       /* 151936 (% 16 == 0) */
+    int gdn_k_heads; /* 16; key and value head dims are 128 */
+    int gdn_v_heads; /* 32 (% 16 == 0, a multiple of gdn_k_heads) */
+    int attn_q_heads;  /* 16; head dim 256 */
+    int attn_kv_heads; /* 4 (q_heads / kv_heads <= 4) */
+    int max_batch;   /* <= 16 */
+    int max_context; /* KV cache length */
+    float rope_theta; /* 1e7 */
+    float rms_eps;    /* 1e-6 */
+} kai_gdn_hybrid_config;
+
+/* The Qwen3.5-4B shape of the benchmark, with the given
+ * batch and context limits. */
+kai_gdn_hybrid_config kai_gdn_hybrid_qwen35_4b(int max_batch, int max_context);
+
+/* Allocate the model on the current device and draw its weights. */
+int kai_gdn_hybrid_create(const kai_gdn_hybrid_config *cfg, unsigned long long seed,
+                          kai_gdn_hybrid **out);
+/* Start `batch` sequences at position `context`, with drawn states for the
+ * context (0: empty states).  batch <= max_batch, context < max_context. */
+int kai_gdn_hybrid_reset(kai_gdn_hybrid *m, int batch, int context, unsigned long long seed);
+/* One decode step on `stream`: tokens [batch] int32 (device) in, the next
+ * tokens by greedy argmax (device, may be NULL) and the logits [batch][vocab]
+ * fp32 (device, may be NULL) out.  The position advances by one. */
+int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits,
+                        void *stream);
+/* Current position (context + steps taken) and device bytes held. */
+int kai_gdn_hybrid_position(const kai_gdn_hybrid *m);
+size_t kai_gdn_hybrid_device_bytes(const kai_gdn_hybrid *m);
+/* Weight bytes a step reads (int8 matrices + scales), for bandwidth figures. */
+size_t kai_gdn_hybrid_weight_bytes(const kai_gdn_hybrid *m);
+void kai_gdn_hybrid_destroy(kai_gdn_hybrid *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KAI_GDN_HYBRID_H */

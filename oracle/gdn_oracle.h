@@ -211,6 +211,23 @@ void orc_w8_gemm(const uint16_t *x, const int8_t *Wq, const float *scale, float 
 void orc_attn_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out, int B,
                      int Hq, int Hkv, int Tmax, int L, int D, float scaling);
 
+/* ---- hybrid decode loop (gdn_hybrid_oracle.c) ---------------------------
+ * The CPU model of include/kai_gdn_hybrid.h: same configuration fields in
+ * the same order, same drawn weights and states, same step (see the file
+ * header for the layer definitions and how it is pinned). */
+typedef struct {
+    int layers, attn_every, hidden, inter, vocab, gdn_k_heads, gdn_v_heads, attn_q_heads,
+        attn_kv_heads, max_batch, max_context;
+    float rope_theta, rms_eps;
+} orc_hybrid_config;
+typedef struct orc_hybrid orc_hybrid;
+orc_hybrid *orc_hybrid_create(const orc_hybrid_config *cfg, uint64_t seed);
+void orc_hybrid_reset(orc_hybrid *m, int batch, int context, uint64_t seed);
+void orc_hybrid_step(orc_hybrid *m, const int32_t *tokens, int32_t *next, float *logits);
+int orc_hybrid_position(const orc_hybrid *m);
+long orc_hybrid_tensor(const orc_hybrid *m, int layer, int id, float *dst);
+void orc_hybrid_destroy(orc_hybrid *m);
+
 /* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
 int orc_num_threads(void);
 

@@ -302,6 +302,79 @@ def num_threads() -> int:
     return lib().orc_num_threads()
 
 
+# ---- hybrid decode loop ----------------------------------------------------
+
+class HybridConfig(ctypes.Structure):
+    """orc_hybrid_config (field order of kai_gdn_hybrid_config)."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "layers", "attn_every", "hidden", "inter", "vocab", "gdn_k_heads", "gdn_v_heads",
+        "attn_q_heads", "attn_kv_heads", "max_batch", "max_context")] + [
+        ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
+# Tensor ids of orc_hybrid_tensor: per layer, and model-level (layer -1).
+HYBRID_LAYER_TENSORS = {
+    "input_layernorm": 0, "post_attention_layernorm": 1, "in_proj_qkv": 2, "in_proj_z": 3,
+    "in_proj_b": 4, "in_proj_a": 5, "out_proj": 6, "conv1d": 7, "dt_bias": 8, "A_log": 9,
+    "norm": 10, "q_proj": 11, "k_proj": 12, "v_proj": 13, "o_proj": 14, "q_norm": 15,
+    "k_norm": 16, "gate_proj": 17, "up_proj": 18, "down_proj": 19}
+HYBRID_MODEL_TENSORS = {"embed_tokens": 1, "norm": 2, "lm_head": 3}
+
+
+class HybridModel:
+    """The CPU restatement of the hybrid decode model (gdn_hybrid_oracle.c)."""
+
+    def __init__(self, cfg: HybridConfig, seed: int):
+        self._h = None
+        L = lib()
+        L.orc_hybrid_create.restype = ctypes.c_void_p
+        L.orc_hybrid_create.argtypes = [ctypes.POINTER(HybridConfig), ctypes.c_uint64]
+        L.orc_hybrid_reset.argtypes = [ctypes.c_void_p, _int, _int, ctypes.c_uint64]
+        L.orc_hybrid_step.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _f32p]
+        L.orc_hybrid_position.argtypes = [ctypes.c_void_p]
+        L.orc_hybrid_tensor.restype = ctypes.c_long
+        L.orc_hybrid_tensor.argtypes = [ctypes.c_void_p, _int, _int, _f32p]
+        L.orc_hybrid_destroy.argtypes = [ctypes.c_void_p]
+        self.cfg = cfg
+        self._h = L.orc_hybrid_create(ctypes.byref(cfg), ctypes.c_uint64(seed))
+        self.batch = cfg.max_batch
+
+    def reset(self, batch: int, context: int, seed: int) -> None:
+        lib().orc_hybrid_reset(self._h, batch, context, ctypes.c_uint64(seed))
+        self.batch = batch
+
+    def step(self, tokens):
+        """-> (next tokens [batch] int32, logits [batch][vocab] fp32)."""
+        tok = np.ascontiguousarray(tokens, np.int32)
+        assert tok.shape == (self.batch,)
+        nxt = np.empty(self.batch, np.int32)
+        logits = np.empty((self.batch, self.cfg.vocab), np.float32)
+        lib().orc_hybrid_step(self._h, tok.ctypes.data, nxt.ctypes.data, P(logits))
+        return nxt, logits
+
+    @property
+    def position(self) -> int:
+        return lib().orc_hybrid_position(self._h)
+
+    def tensor(self, layer: int, name: str) -> np.ndarray | None:
+        """A drawn tensor as fp32 (matrices dequantised), None if absent."""
+        tid = HYBRID_MODEL_TENSORS[name] if layer < 0 else HYBRID_LAYER_TENSORS[name]
+        n = lib().orc_hybrid_tensor(self._h, layer, tid, None)
+        if n < 0:
+            return None
+        out = np.empty(n, np.float32)
+        lib().orc_hybrid_tensor(self._h, layer, tid, P(out))
+        return out
+
+    def close(self) -> None:
+        if self._h:
+            lib().orc_hybrid_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
 # ---- narrow-format helpers -------------------------------------------------
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:

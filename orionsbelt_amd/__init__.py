@@ -1,7 +1,8 @@
 """orionsbelt_amd -- MI355X (gfx950) implementation of the OrionsBelt GDN hot path.
 
 The product is the C-ABI library ``orionsbelt_amd/lib/libkai_gdn_hip.so``
-(declared in ``include/kai/ukernels/gdn/*.h`` and ``include/kai_gdn_hip.h``).
+(declared in ``include/kai/ukernels/gdn/*.h``, ``include/kai_gdn_hip.h`` and
+``include/kai_gdn_hybrid.h``).
 This module only loads it through ctypes so Python tests and the benchmark
 can call the same entry points a C caller would.  There is no fallback: if the
 library is missing, :func:`lib` raises.
@@ -49,6 +50,14 @@ HIP_SYMBOLS = (
     "kai_run_gdn_w8_quantize_hip",
     "kai_gdn_attn_decode_workspace_bytes",
     "kai_run_gdn_attn_decode_f16kv_hip",
+    "kai_gdn_hybrid_qwen35_4b",
+    "kai_gdn_hybrid_create",
+    "kai_gdn_hybrid_reset",
+    "kai_gdn_hybrid_step",
+    "kai_gdn_hybrid_position",
+    "kai_gdn_hybrid_device_bytes",
+    "kai_gdn_hybrid_weight_bytes",
+    "kai_gdn_hybrid_destroy",
     "kai_gdn_hip_init",
     "kai_gdn_hip_error_string",
     "kai_gdn_hip_check_device_error",
@@ -59,6 +68,16 @@ _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _i = ctypes.c_int
 _f = ctypes.c_float
+
+
+
+class HybridConfig(ctypes.Structure):
+    """kai_gdn_hybrid_config (include/kai_gdn_hybrid.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "layers", "attn_every", "hidden", "inter", "vocab", "gdn_k_heads", "gdn_v_heads",
+        "attn_q_heads", "attn_kv_heads", "max_batch", "max_context")] + [
+        ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
 
 # Element formats of kai_run_gdn_state_convert_hip (KAI_GDN_FMT_* in kai_gdn_hip.h).
 FMT_F32, FMT_F16, FMT_BF16 = 0, 1, 2
@@ -102,6 +121,15 @@ _SIGS = {
     "kai_gdn_attn_decode_workspace_bytes": (_sz, [_i, _i, _i]),
     "kai_run_gdn_attn_decode_f16kv_hip":
         (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
+    "kai_gdn_hybrid_qwen35_4b": (HybridConfig, [_i, _i]),
+    "kai_gdn_hybrid_create": (_i, [ctypes.POINTER(HybridConfig), ctypes.c_ulonglong,
+                                   ctypes.POINTER(_vp)]),
+    "kai_gdn_hybrid_reset": (_i, [_vp, _i, _i, ctypes.c_ulonglong]),
+    "kai_gdn_hybrid_step": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "kai_gdn_hybrid_position": (_i, [_vp]),
+    "kai_gdn_hybrid_device_bytes": (_sz, [_vp]),
+    "kai_gdn_hybrid_weight_bytes": (_sz, [_vp]),
+    "kai_gdn_hybrid_destroy": (None, [_vp]),
     "kai_gdn_hip_init": (_i, []),
     "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
     "kai_gdn_hip_check_device_error": (_i, []),

@@ -1,0 +1,549 @@
+// gdn_hybrid.hip -- the end-to-end hybrid decode loop (include/kai_gdn_hybrid.h)
+// for gfx950: model construction, drawn states, and one decode step as a
+// sequence of this library's kernels on one stream.
+//
+// Per step, batch B, residual stream h [B][hidden] fp32:
+//   h = embed(tokens)
+//   per layer: x = rmsnorm(h) fp16; mixer(x) -> d; h += d; x = rmsnorm(h);
+//              h += down(silu(gate(x)) * up(x))
+//     GDN mixer: in_proj_qkv/z/b/a (int8 GEMM) -> conv update on HF's cache
+//                -> gating prologue -> delta-rule decode step (fp32 state)
+//                -> gated RMSNorm with z -> out_proj
+//     attention: q_proj (q and output gate per head), k_proj, v_proj ->
+//                q/k RMSNorm, partial rotary embedding, KV append -> decode
+//                attention over the cache -> o * sigmoid(gate) -> o_proj
+//   logits = lm_head(rmsnorm(h)), next = argmax
+// The residual add is fused into the following RMSNorm.  Everything a matmul
+// reads is fp16 (the model's activation dtype), everything it writes fp32.
+#include <cmath>
+#include <vector>
+
+#include "gdn_common.h"
+#include "gdn_internal.h"
+#include "../../include/kai_gdn_hybrid.h"
+
+namespace gdn {
+namespace {
+
+#define GDN_HD __host__ __device__ __forceinline__
+
+// ---- drawn values: counter-based hash, identical on host and device --------
+GDN_HD uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// (2u - 1) * amp + center, u in [0, 1) from 24 hash bits; the arithmetic
+// is exact up to the final product and sum (no contraction).
+GDN_HD float hash_value(uint64_t seed, uint64_t stream, uint64_t i, float amp, float center) {
+#pragma clang fp contract(off)
+    const uint64_t h = mix64(mix64(seed ^ (stream * 0x100000001B3ull)) + i);
+    const float u = (float)(h >> 40) * (1.0f / 16777216.0f);
+    return (u * 2.0f - 1.0f) * amp + center;
+}
+
+__global__ __launch_bounds__(256) void fill_f32_kernel(float *dst, size_t n, uint64_t seed,
+                                                       uint64_t stream, float amp, float center) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = hash_value(seed, stream, i, amp, center);
+}
+__global__ __launch_bounds__(256) void fill_f16_kernel(uint16_t *dst, size_t n, uint64_t seed,
+                                                       uint64_t stream, float amp, float center) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = f32_to_f16_rne(hash_value(seed, stream, i, amp, center));
+}
+// K/V cache rows [rows][Tmax][256], positions < len drawn, the rest zero.
+__global__ __launch_bounds__(256) void fill_cache_kernel(uint16_t *dst, size_t rows, int Tmax, int len,
+                                                         uint64_t seed, uint64_t stream, float amp) {
+    const size_t n = rows * (size_t)Tmax * 256;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const int t = (int)((i / 256) % Tmax);
+        dst[i] = t < len ? f32_to_f16_rne(hash_value(seed, stream, i, amp, 0.f)) : 0;
+    }
+}
+unsigned fill_blocks(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
+
+// ---- step kernels ------------------------------------------------------------
+
+GDN_DEV float block_sum(float x, float *red) {  // 256 threads
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return s;
+}
+
+// h[b] = embed[token[b]] (token ids clamped into the vocabulary).
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t *tokens, const uint16_t *table,
+                                                    float *h, int H, int vocab) {
+    const int b = blockIdx.x;
+    const int t = min(max(tokens[b], 0), vocab - 1);
+    for (int i = threadIdx.x; i < H; i += 256) h[(size_t)b * H + i] = f16_to_f32(table[(size_t)t * H + i]);
+}
+
+// Qwen3_5RMSNorm (modeling_qwen3_5.py:720-737) with the residual add fused:
+// h += d (when d), out = fp16(h / sqrt(mean(h^2) + eps) * (1 + w)).
+__global__ __launch_bounds__(256) void addnorm_kernel(float *h, const float *d, const float *w,
+                                                      uint16_t *out, int H, float eps) {
+    __shared__ float red[4];
+    const size_t b = blockIdx.x;
+    float *hr = h + b * H;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < H; i += 256) {
+        float x = hr[i];
+        if (d) {
+            x += d[b * H + i];
+            hr[i] = x;
+        }
+        ss += x * x;
+    }
+    const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+    for (int i = threadIdx.x; i < H; i += 256) out[b * H + i] = f32_to_f16_rne(hr[i] * inv * (1.0f + w[i]));
+}
+
+// Attention prologue (Qwen3_5Attention.forward:656-681): block (slot, b),
+// 256 threads = the head's dims.  Slots [0, Hq): query heads from qg
+// [B][Hq][512] (q = dims 0..255, gate = 256..511) -> q_norm -> rotary ->
+// q16; [Hq, Hq + Hkv): key heads -> k_norm -> rotary -> K cache at pos;
+// [Hq + Hkv, Hq + 2 Hkv): value heads -> V cache at pos.  Norm outputs are
+// rounded to fp16 (type_as) before the rotary embedding, which acts on dims
+// 0..63 with inv_freq[i] = 1 / theta^(2i / 64) and rotate_half.
+__global__ __launch_bounds__(256) void attn_prologue_kernel(
+    const float *qg, const float *kx, const float *vx, const float *q_norm, const float *k_norm,
+    uint16_t *q16, uint16_t *Kc, uint16_t *Vc, int Hq, int Hkv, int Tmax, int pos, float theta,
+    float eps) {
+    __shared__ float red[4];
+    __shared__ float rot[64];
+    const int slot = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    if (slot >= Hq + Hkv) {  // value head: copy into the cache
+        const int kv = slot - Hq - Hkv;
+        Vc[(((size_t)b * Hkv + kv) * Tmax + pos) * 256 + d] = f32_to_f16_rne(vx[((size_t)b * Hkv + kv) * 256 + d]);
+        return;
+    }
+    const bool is_q = slot < Hq;
+    const float x = is_q ? qg[((size_t)b * Hq + slot) * 512 + d] : kx[((size_t)b * Hkv + (slot - Hq)) * 256 + d];
+    const float *wn = is_q ? q_norm : k_norm;
+    const float inv = 1.0f / sqrtf(block_sum(x * x, red) / 256.0f + eps);
+    const float xn = f16_to_f32(f32_to_f16_rne(x * inv * (1.0f + wn[d])));
+    float y = xn;
+    if (d < 64) rot[d] = xn;
+    __syncthreads();
+    if (d < 64) {
+        const int i = d & 31;
+        const float inv_freq = 1.0f / powf(theta, (float)(2 * i) / 64.0f);
+        const float f = inv_freq * (float)pos;
+        const float c = cosf(f), s = sinf(f);
+        y = d < 32 ? xn * c - rot[d + 32] * s : xn * c + rot[d - 32] * s;
+    }
+    const uint16_t o = f32_to_f16_rne(y);
+    if (is_q) q16[((size_t)b * Hq + slot) * 256 + d] = o;
+    else Kc[(((size_t)b * Hkv + (slot - Hq)) * Tmax + pos) * 256 + d] = o;
+}
+
+// o16 = fp16(attn * sigmoid(gate)), gate = dims 256..511 of qg's head.
+__global__ __launch_bounds__(256) void attn_post_kernel(const float *ao, const float *qg, uint16_t *o16,
+                                                        int Hq) {
+    const size_t bh = blockIdx.x;  // b * Hq + h
+    const int d = threadIdx.x;
+    const float gt = qg[bh * 512 + 256 + d];
+    o16[bh * 256 + d] = f32_to_f16_rne(ao[bh * 256 + d] * (1.0f / (1.0f + expf(-gt))));
+}
+
+// Qwen3_5MLP (modeling_qwen3_5.py:704-717): act = fp16(silu(gate) * up).
+__global__ __launch_bounds__(256) void swiglu_kernel(const float *gate, const float *up, uint16_t *out,
+                                                     size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const float g = gate[i];
+        out[i] = f32_to_f16_rne(g / (1.0f + expf(-g)) * up[i]);
+    }
+}
+
+// next[b] = the first index of the largest logit of row b.
+__global__ __launch_bounds__(256) void argmax_kernel(const float *logits, int32_t *next, int V) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    const float *row = logits + (size_t)blockIdx.x * V;
+    float best = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < V; i += 256) {
+        const float v = row[i];
+        if (v > best) {  // first occurrence within the thread's stride
+            best = v;
+            bi = i;
+        }
+    }
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = 128; s >= 1; s >>= 1) {
+        if (threadIdx.x < s) {
+            const float v2 = sv[threadIdx.x + s];
+            const int i2 = si[threadIdx.x + s];
+            if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
+                sv[threadIdx.x] = v2;
+                si[threadIdx.x] = i2;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) next[blockIdx.x] = si[0];
+}
+
+// ---- model -------------------------------------------------------------------
+
+// Tensor streams of the hash: per layer 64 ids from 64 (l + 1); global 0..63;
+// drawn states 1 << 20 onwards.
+enum : int {
+    kLnIn = 0, kLnPost, kQkv, kZ, kBp, kAp, kOut, kConvW, kDtBias, kALog, kNormW,
+    kQp, kKp, kVp, kOp, kQn, kKn, kGate, kUp, kDown,
+};
+enum : int { kEmbed = 1, kFinalNorm = 2, kLmHead = 3 };
+enum : int { kStConv = 0, kStS = 1, kStK = 2, kStV = 3 };
+constexpr float kWAmp = 0.034641016f;  // uniform amplitude of std 0.02
+
+struct Mat {
+    int8_t *q = nullptr;
+    float *s = nullptr;
+    int N = 0, K = 0;
+};
+
+struct Layer {
+    bool attn = false;
+    float *ln_in = nullptr, *ln_post = nullptr;
+    Mat qkv, z, bp, ap, out;  // GDN
+    float *conv_w = nullptr, *dt_bias = nullptr, *A_log = nullptr, *norm_w = nullptr;
+    Mat qp, kp, vp, op;  // attention
+    float *q_norm = nullptr, *k_norm = nullptr;
+    Mat gate, up, down;
+    float *S = nullptr, *conv_state = nullptr;  // [B][Hv][128][128], [B][conv_dim][4]
+    uint16_t *Kc = nullptr, *Vc = nullptr;      // [B][Hkv][Tmax][256]
+};
+
+}  // namespace
+}  // namespace gdn
+
+struct kai_gdn_hybrid {
+    kai_gdn_hybrid_config cfg{};
+    int conv_dim = 0, value_dim = 0;
+    std::vector<gdn::Layer> layers;
+    uint16_t *embed = nullptr;
+    float *final_norm = nullptr;
+    gdn::Mat lm;
+    // step buffers
+    float *h = nullptr, *mix = nullptr, *mlp = nullptr, *big0 = nullptr, *big1 = nullptr;
+    float *qkv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr, *qb = nullptr, *kb = nullptr,
+          *vb = nullptr, *gb = nullptr, *betab = nullptr, *ob = nullptr, *yb = nullptr;
+    float *qg = nullptr, *kx = nullptr, *vx = nullptr, *ao = nullptr, *logits = nullptr;
+    int32_t *next = nullptr;
+    uint16_t *x16 = nullptr, *q16 = nullptr;
+    float *gemm_ws = nullptr, *attn_ws = nullptr;
+    size_t gemm_ws_bytes = 0, attn_ws_bytes = 0;
+    std::vector<void *> allocs;
+    size_t bytes = 0, weight_bytes = 0;
+    int batch = 0, pos = 0;
+};
+
+namespace gdn {
+namespace {
+
+hipError_t alloc(kai_gdn_hybrid *m, void **p, size_t n) {
+    if (n == 0) n = 16;
+    hipError_t e = hipMalloc(p, n);
+    if (e != hipSuccess) return e;
+    m->allocs.push_back(*p);
+    m->bytes += n;
+    return hipSuccess;
+}
+template <typename T> hipError_t alloc_t(kai_gdn_hybrid *m, T **p, size_t count) {
+    return alloc(m, reinterpret_cast<void **>(p), count * sizeof(T));
+}
+
+hipError_t fill(float *dst, size_t n, uint64_t seed, uint64_t stream, float amp, float center) {
+    fill_f32_kernel<<<fill_blocks(n), 256>>>(dst, n, seed, stream, amp, center);
+    return hipGetLastError();
+}
+
+// A drawn int8 matrix [N][K] with per-output-channel scales.
+hipError_t make_mat(kai_gdn_hybrid *m, Mat &w, int N, int K, uint64_t seed, uint64_t stream, float *tmp) {
+    w.N = N;
+    w.K = K;
+    hipError_t e;
+    if ((e = alloc_t(m, &w.q, (size_t)N * K)) != hipSuccess) return e;
+    if ((e = alloc_t(m, &w.s, (size_t)N)) != hipSuccess) return e;
+    if ((e = fill(tmp, (size_t)N * K, seed, stream, kWAmp, 0.f)) != hipSuccess) return e;
+    if ((e = launch_w8_quantize(tmp, w.q, w.s, N, K, nullptr)) != hipSuccess) return e;
+    m->weight_bytes += (size_t)N * K + (size_t)N * 4;
+    return hipSuccess;
+}
+
+hipError_t make_vec(kai_gdn_hybrid *m, float **v, size_t n, uint64_t seed, uint64_t stream, float amp,
+                    float center) {
+    hipError_t e = alloc_t(m, v, n);
+    return e != hipSuccess ? e : fill(*v, n, seed, stream, amp, center);
+}
+
+hipError_t gemm(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *y, hipStream_t st) {
+    return launch_w8_gemm(x, w.q, w.s, y, m->batch, w.N, w.K, m->gemm_ws, st);
+}
+
+#define TRY(x)                              \
+    do {                                    \
+        hipError_t e_ = (x);                \
+        if (e_ != hipSuccess) return e_;    \
+    } while (0)
+
+hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
+    const kai_gdn_hybrid_config &c = m->cfg;
+    const int H = c.hidden, I = c.inter, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads, Hq = c.attn_q_heads,
+              Hkv = c.attn_kv_heads, Bm = c.max_batch;
+    m->conv_dim = 2 * Hk * 128 + Hv * 128;
+    m->value_dim = Hv * 128;
+    // the largest drawn matrix, fp32 staging for the quantiser
+    size_t tmp_n = (size_t)c.vocab * H;
+    tmp_n = std::max(tmp_n, (size_t)I * H);
+    tmp_n = std::max(tmp_n, (size_t)m->conv_dim * H);
+    tmp_n = std::max(tmp_n, (size_t)Hq * 512 * H);
+    float *tmp = nullptr;
+    TRY(hipMalloc(&tmp, tmp_n * 4));
+    auto run = [&]() -> hipError_t {
+        m->layers.resize(c.layers);
+        for (int l = 0; l < c.layers; ++l) {
+            Layer &L = m->layers[l];
+            const uint64_t base = 64ull * (l + 1);
+            L.attn = (l + 1) % c.attn_every == 0;
+            TRY(make_vec(m, &L.ln_in, H, seed, base + kLnIn, 0.1f, 0.f));
+            TRY(make_vec(m, &L.ln_post, H, seed, base + kLnPost, 0.1f, 0.f));
+            if (!L.attn) {
+                TRY(make_mat(m, L.qkv, m->conv_dim, H, seed, base + kQkv, tmp));
+                TRY(make_mat(m, L.z, m->value_dim, H, seed, base + kZ, tmp));
+                TRY(make_mat(m, L.bp, Hv, H, seed, base + kBp, tmp));
+                TRY(make_mat(m, L.ap, Hv, H, seed, base + kAp, tmp));
+                TRY(make_mat(m, L.out, H, m->value_dim, seed, base + kOut, tmp));
+                TRY(make_vec(m, &L.conv_w, (size_t)m->conv_dim * 4, seed, base + kConvW, 0.5f, 0.f));
+                TRY(make_vec(m, &L.dt_bias, Hv, seed, base + kDtBias, 0.5f, 1.0f));
+                TRY(make_vec(m, &L.A_log, Hv, seed, base + kALog, 1.3862944f, 1.3862944f));  // U(0, ln 16)
+                TRY(make_vec(m, &L.norm_w, 128, seed, base + kNormW, 0.1f, 1.0f));
+                TRY(alloc_t(m, &L.S, (size_t)Bm * Hv * 128 * 128));
+                TRY(alloc_t(m, &L.conv_state, (size_t)Bm * m->conv_dim * 4));
+            } else {
+                TRY(make_mat(m, L.qp, Hq * 512, H, seed, base + kQp, tmp));
+                TRY(make_mat(m, L.kp, Hkv * 256, H, seed, base + kKp, tmp));
+                TRY(make_mat(m, L.vp, Hkv * 256, H, seed, base + kVp, tmp));
+                TRY(make_mat(m, L.op, H, Hq * 256, seed, base + kOp, tmp));
+                TRY(make_vec(m, &L.q_norm, 256, seed, base + kQn, 0.1f, 0.f));
+                TRY(make_vec(m, &L.k_norm, 256, seed, base + kKn, 0.1f, 0.f));
+                TRY(alloc_t(m, &L.Kc, (size_t)Bm * Hkv * c.max_context * 256));
+                TRY(alloc_t(m, &L.Vc, (size_t)Bm * Hkv * c.max_context * 256));
+            }
+            TRY(make_mat(m, L.gate, I, H, seed, base + kGate, tmp));
+            TRY(make_mat(m, L.up, I, H, seed, base + kUp, tmp));
+            TRY(make_mat(m, L.down, H, I, seed, base + kDown, tmp));
+        }
+        TRY(alloc_t(m, &m->embed, (size_t)c.vocab * H));
+        fill_f16_kernel<<<fill_blocks((size_t)c.vocab * H), 256>>>(m->embed, (size_t)c.vocab * H, seed, kEmbed,
+                                                                   1.0f, 0.f);
+        TRY(hipGetLastError());
+        TRY(make_vec(m, &m->final_norm, H, seed, kFinalNorm, 0.1f, 0.f));
+        TRY(make_mat(m, m->lm, c.vocab, H, seed, kLmHead, tmp));
+        // step buffers
+        const size_t wide = std::max({(size_t)m->conv_dim, (size_t)I, (size_t)Hq * 512, (size_t)H,
+                                      (size_t)m->value_dim});
+        TRY(alloc_t(m, &m->h, (size_t)Bm * H));
+        TRY(alloc_t(m, &m->mix, (size_t)Bm * H));
+        TRY(alloc_t(m, &m->mlp, (size_t)Bm * H));
+        TRY(alloc_t(m, &m->big0, (size_t)Bm * wide));
+        TRY(alloc_t(m, &m->big1, (size_t)Bm * wide));
+        TRY(alloc_t(m, &m->zb, (size_t)Bm * m->value_dim));
+        TRY(alloc_t(m, &m->ab, (size_t)Bm * Hv));
+        TRY(alloc_t(m, &m->bb, (size_t)Bm * Hv));
+        TRY(alloc_t(m, &m->qb, (size_t)Bm * Hk * 128));
+        TRY(alloc_t(m, &m->kb, (size_t)Bm * Hk * 128));
+        TRY(alloc_t(m, &m->vb, (size_t)Bm * Hv * 128));
+        TRY(alloc_t(m, &m->gb, (size_t)Bm * Hv));
+        TRY(alloc_t(m, &m->betab, (size_t)Bm * Hv));
+        TRY(alloc_t(m, &m->ob, (size_t)Bm * Hv * 128));
+        TRY(alloc_t(m, &m->yb, (size_t)Bm * m->value_dim));
+        TRY(alloc_t(m, &m->kx, (size_t)Bm * Hkv * 256));
+        TRY(alloc_t(m, &m->vx, (size_t)Bm * Hkv * 256));
+        TRY(alloc_t(m, &m->ao, (size_t)Bm * Hq * 256));
+        TRY(alloc_t(m, &m->logits, (size_t)Bm * c.vocab));
+        TRY(alloc_t(m, &m->next, (size_t)Bm));
+        TRY(alloc_t(m, &m->x16, (size_t)Bm * wide));
+        TRY(alloc_t(m, &m->q16, (size_t)Bm * Hq * 256));
+        m->qkv = m->big0;
+        m->qg = m->big0;
+        // GEMM split-K workspace: the largest over the model's shapes
+        const int shapes[][2] = {{m->conv_dim, H}, {m->value_dim, H}, {Hv, H}, {H, m->value_dim},
+                                 {Hq * 512, H}, {Hkv * 256, H}, {H, Hq * 256}, {I, H}, {H, I},
+                                 {c.vocab, H}};
+        for (auto &s : shapes) m->gemm_ws_bytes = std::max(m->gemm_ws_bytes, w8_workspace_bytes(Bm, s[0], s[1]));
+        TRY(alloc(m, reinterpret_cast<void **>(&m->gemm_ws), m->gemm_ws_bytes));
+        m->attn_ws_bytes = attn_workspace_bytes(Bm, Hq, c.max_context);
+        TRY(alloc(m, reinterpret_cast<void **>(&m->attn_ws), m->attn_ws_bytes));
+        return hipDeviceSynchronize();
+    };
+    const hipError_t e = run();
+    (void)hipFree(tmp);
+    return e;
+}
+
+hipError_t gdn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
+    const kai_gdn_hybrid_config &c = m->cfg;
+    const int B = m->batch, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads;
+    TRY(gemm(m, m->x16, L.qkv, m->qkv, st));
+    TRY(gemm(m, m->x16, L.z, m->zb, st));
+    TRY(gemm(m, m->x16, L.bp, m->bb, st));
+    TRY(gemm(m, m->x16, L.ap, m->ab, st));
+    TRY(launch_conv_update(m->qkv, L.conv_state, L.conv_w, m->big1, B, 1, m->conv_dim, true, st));
+    TRY(launch_gating_prologue(false, m->big1, m->ab, m->bb, L.A_log, L.dt_bias, m->qb, m->kb, m->vb, m->gb,
+                               m->betab, B, Hk, Hv, st));
+    TRY(launch_delta_decode(kF32, L.S, m->qb, m->kb, m->vb, m->gb, m->betab, m->ob, B, Hv, Hk, 128, 128,
+                            1.0f / sqrtf(128.0f), st));
+    TRY(launch_gated_rmsnorm(false, m->ob, m->zb, L.norm_w, m->yb, (size_t)B * Hv, c.rms_eps, st));
+    TRY(launch_convert(m->yb, kF32, m->x16, kF16, (size_t)B * m->value_dim, st));
+    return gemm(m, m->x16, L.out, m->mix, st);
+}
+
+hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
+    const kai_gdn_hybrid_config &c = m->cfg;
+    const int B = m->batch, Hq = c.attn_q_heads, Hkv = c.attn_kv_heads;
+    TRY(gemm(m, m->x16, L.qp, m->qg, st));
+    TRY(gemm(m, m->x16, L.kp, m->kx, st));
+    TRY(gemm(m, m->x16, L.vp, m->vx, st));
+    attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, B), 256, 0, st>>>(m->qg, m->kx, m->vx, L.q_norm, L.k_norm, m->q16,
+                                                                 L.Kc, L.Vc, Hq, Hkv, c.max_context, m->pos,
+                                                                 c.rope_theta, c.rms_eps);
+    TRY(hipGetLastError());
+    TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, m->ao, B, Hq, Hkv, c.max_context, m->pos + 1, 1.0f / 16.0f,
+                           m->attn_ws, st));
+    attn_post_kernel<<<B * Hq, 256, 0, st>>>(m->ao, m->qg, m->x16, Hq);
+    TRY(hipGetLastError());
+    return gemm(m, m->x16, L.op, m->mix, st);
+}
+
+hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits, hipStream_t st) {
+    const kai_gdn_hybrid_config &c = m->cfg;
+    const int B = m->batch, H = c.hidden;
+    embed_kernel<<<B, 256, 0, st>>>(tokens, m->embed, m->h, H, c.vocab);
+    TRY(hipGetLastError());
+    const float *pending = nullptr;
+    for (Layer &L : m->layers) {
+        addnorm_kernel<<<B, 256, 0, st>>>(m->h, pending, L.ln_in, m->x16, H, c.rms_eps);
+        TRY(hipGetLastError());
+        TRY(L.attn ? attn_mixer(m, L, st) : gdn_mixer(m, L, st));
+        addnorm_kernel<<<B, 256, 0, st>>>(m->h, m->mix, L.ln_post, m->x16, H, c.rms_eps);
+        TRY(hipGetLastError());
+        TRY(gemm(m, m->x16, L.gate, m->big0, st));
+        TRY(gemm(m, m->x16, L.up, m->big1, st));
+        const size_t n = (size_t)B * c.inter;
+        swiglu_kernel<<<fill_blocks(n), 256, 0, st>>>(m->big0, m->big1, m->x16, n);
+        TRY(hipGetLastError());
+        TRY(gemm(m, m->x16, L.down, m->mlp, st));
+        pending = m->mlp;
+    }
+    addnorm_kernel<<<B, 256, 0, st>>>(m->h, pending, m->final_norm, m->x16, H, c.rms_eps);
+    TRY(hipGetLastError());
+    float *lg = logits ? logits : m->logits;
+    TRY(gemm(m, m->x16, m->lm, lg, st));
+    argmax_kernel<<<B, 256, 0, st>>>(lg, next ? next : m->next, c.vocab);
+    TRY(hipGetLastError());
+    ++m->pos;
+    return hipSuccess;
+}
+
+hipError_t reset(kai_gdn_hybrid *m, int batch, int context, uint64_t seed) {
+    const kai_gdn_hybrid_config &c = m->cfg;
+    m->batch = batch;
+    m->pos = context;
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+        Layer &L = m->layers[l];
+        const uint64_t base = (1ull << 20) + 16ull * l;
+        if (!L.attn) {
+            const size_t ns = (size_t)batch * c.gdn_v_heads * 128 * 128, nc = (size_t)batch * m->conv_dim * 4;
+            if (context > 0) {
+                TRY(fill(L.S, ns, seed, base + kStS, 0.034641016f, 0.f));
+                TRY(fill(L.conv_state, nc, seed, base + kStConv, 1.0f, 0.f));
+            } else {
+                TRY(hipMemset(L.S, 0, ns * 4));
+                TRY(hipMemset(L.conv_state, 0, nc * 4));
+            }
+        } else {
+            const size_t rows = (size_t)batch * c.attn_kv_heads;
+            const size_t n = rows * c.max_context * 256;
+            fill_cache_kernel<<<fill_blocks(n), 256>>>(L.Kc, rows, c.max_context, context, seed, base + kStK, 1.0f);
+            fill_cache_kernel<<<fill_blocks(n), 256>>>(L.Vc, rows, c.max_context, context, seed, base + kStV, 1.0f);
+            TRY(hipGetLastError());
+        }
+    }
+    return hipDeviceSynchronize();
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" kai_gdn_hybrid_config kai_gdn_hybrid_qwen35_4b(int max_batch, int max_context) {
+    kai_gdn_hybrid_config c{};
+    c.layers = 32;
+    c.attn_every = 4;
+    c.hidden = 2560;
+    c.inter = 9216;
+    c.vocab = 151936;
+    c.gdn_k_heads = 16;
+    c.gdn_v_heads = 32;
+    c.attn_q_heads = 16;
+    c.attn_kv_heads = 4;
+    c.max_batch = max_batch;
+    c.max_context = max_context;
+    c.rope_theta = 1.0e7f;
+    c.rms_eps = 1e-6f;
+    return c;
+}
+
+extern "C" void kai_gdn_hybrid_destroy(kai_gdn_hybrid *m) {
+    if (!m) return;
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+extern "C" int kai_gdn_hybrid_create(const kai_gdn_hybrid_config *cfg, unsigned long long seed,
+                                     kai_gdn_hybrid **out) {
+    if (!cfg || !out) return (int)hipErrorInvalidValue;
+    const kai_gdn_hybrid_config &c = *cfg;
+    const bool ok = c.layers > 0 && c.attn_every > 0 && c.hidden > 0 && c.hidden % 256 == 0 && c.inter > 0 &&
+                    c.inter % 256 == 0 && c.vocab > 0 && c.vocab % 16 == 0 && c.gdn_k_heads > 0 &&
+                    c.gdn_v_heads % 16 == 0 && c.gdn_v_heads % c.gdn_k_heads == 0 && c.gdn_v_heads > 0 &&
+                    c.attn_kv_heads > 0 && c.attn_q_heads % c.attn_kv_heads == 0 &&
+                    c.attn_q_heads / c.attn_kv_heads <= 4 && c.max_batch >= 1 && c.max_batch <= 16 &&
+                    c.max_context >= 1 && c.rms_eps >= 0.f && c.rope_theta > 0.f;
+    if (!ok) return (int)hipErrorInvalidValue;
+    kai_gdn_hybrid *m = new kai_gdn_hybrid;
+    m->cfg = c;
+    const hipError_t e = gdn::build(m, seed);
+    if (e != hipSuccess) {
+        kai_gdn_hybrid_destroy(m);
+        return (int)e;
+    }
+    m->batch = c.max_batch;
+    *out = m;
+    return 0;
+}
+
+extern "C" int kai_gdn_hybrid_reset(kai_gdn_hybrid *m, int batch, int context, unsigned long long seed) {
+    if (!m || batch < 1 || batch > m->cfg.max_batch || context < 0 || context >= m->cfg.max_context)
+        return (int)hipErrorInvalidValue;
+    return (int)gdn::reset(m, batch, context, seed);
+}
+
+extern "C" int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits,
+                                   void *stream) {
+    if (!m || !tokens) return (int)hipErrorInvalidValue;
+    if (m->pos >= m->cfg.max_context) return (int)hipErrorInvalidValue;  // the KV cache is full
+    return (int)gdn::step(m, tokens, next, logits, (hipStream_t)stream);
+}
+
+extern "C" int kai_gdn_hybrid_position(const kai_gdn_hybrid *m) { return m ? m->pos : -1; }
+extern "C" size_t kai_gdn_hybrid_device_bytes(const kai_gdn_hybrid *m) { return m ? m->bytes : 0; }
+extern "C" size_t kai_gdn_hybrid_weight_bytes(const kai_gdn_hybrid *m) { return m ? m->weight_bytes : 0; }

@@ -272,16 +272,82 @@ def gen_state():
     np.savez_compressed(os.path.join(HERE, "hf_state.npz"), **d)
 
 
+# The tiny hybrid model of the logits fixture: every shape constraint of the
+# device model holds (hidden, inter % 256; vocab, projections % 16), layer 3
+# is full attention, and the GDN and attention head dims are the real ones.
+HYBRID_TINY = dict(layers=4, attn_every=4, hidden=256, inter=512, vocab=1024, gdn_k_heads=8,
+                   gdn_v_heads=16, attn_q_heads=4, attn_kv_heads=1, max_batch=2, max_context=64,
+                   rope_theta=1.0e7, rms_eps=1e-6)
+HYBRID_SEED = 20260
+HYBRID_T = 12
+
+
+def gen_hybrid():
+    """HF Qwen3_5ForCausalLM (fp32, eager attention, no cache) on the
+    dequantised weights of the oracle's drawn tiny model: logits of every
+    position of two token sequences, run over the whole sequence at once
+    (chunked GDN form, causal-masked attention)."""
+    import torch
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5ForCausalLM
+
+    c = HYBRID_TINY
+    m = orc.HybridModel(orc.HybridConfig(*[c[f] for f, _ in orc.HybridConfig._fields_]), HYBRID_SEED)
+    cfg = Qwen3_5TextConfig(
+        vocab_size=c["vocab"], hidden_size=c["hidden"], intermediate_size=c["inter"],
+        num_hidden_layers=c["layers"], num_attention_heads=c["attn_q_heads"],
+        num_key_value_heads=c["attn_kv_heads"], head_dim=256, rms_norm_eps=c["rms_eps"],
+        linear_num_key_heads=c["gdn_k_heads"], linear_num_value_heads=c["gdn_v_heads"],
+        linear_key_head_dim=128, linear_value_head_dim=128, linear_conv_kernel_dim=4,
+        full_attention_interval=c["attn_every"], tie_word_embeddings=False,
+        rope_parameters={"rope_type": "default", "rope_theta": c["rope_theta"],
+                         "partial_rotary_factor": 0.25, "mrope_section": [11, 11, 10],
+                         "mrope_interleaved": True},
+        max_position_embeddings=c["max_context"])
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    hf = Qwen3_5ForCausalLM(cfg).float().eval()
+    sd = {}
+    for name, t in hf.state_dict().items():
+        parts = name.split(".")
+        if parts[1] == "layers":
+            layer = int(parts[2])
+            key = parts[4] if parts[3] in ("linear_attn", "self_attn", "mlp") else parts[3]
+            if parts[3] in ("linear_attn", "self_attn") and parts[4] == "norm":
+                key = "norm"
+            v = m.tensor(layer, key)
+        elif parts[0] == "lm_head":
+            v = m.tensor(-1, "lm_head")
+        else:
+            v = m.tensor(-1, parts[1])
+        assert v is not None and v.size == t.numel(), (name, None if v is None else v.size, t.shape)
+        sd[name] = torch.from_numpy(v.reshape(t.shape).copy())
+    hf.load_state_dict(sd)
+    rs = np.random.RandomState(5)
+    tokens = rs.randint(0, c["vocab"], size=(2, HYBRID_T)).astype(np.int32)
+    with torch.no_grad():
+        logits = hf(input_ids=torch.from_numpy(tokens.astype(np.int64)), use_cache=False).logits
+    d = {"tokens": tokens, "logits": logits.float().numpy(), "seed": np.int64(HYBRID_SEED)}
+    for k, v in c.items():
+        d["cfg_" + k] = np.asarray(v)
+    np.savez_compressed(os.path.join(HERE, "hf_hybrid.npz"), **d)
+
+
 if __name__ == "__main__":
     orc.build()
     if len(sys.argv) > 1 and sys.argv[1] == "layer":
         gen_layer()
         gen_state()
         sys.exit(0)
+    if len(sys.argv) > 1 and sys.argv[1] == "hybrid":
+        gen_hybrid()
+        sys.exit(0)
     gen_kai()
     gen_sve()
     gen_hf()
     gen_layer()
     gen_state()
-    for f in ("kai_ref.npz", "sve_mixed.npz", "hf_gdr.npz", "hf_layer.npz", "hf_state.npz"):
+    gen_hybrid()
+    for f in ("kai_ref.npz", "sve_mixed.npz", "hf_gdr.npz", "hf_layer.npz", "hf_state.npz",
+              "hf_hybrid.npz"):
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

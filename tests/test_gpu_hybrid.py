@@ -1,0 +1,180 @@
+"""GPU parity of the hybrid decode loop (include/kai_gdn_hybrid.h) through the
+C-ABI, against the oracle's CPU model (oracle/gdn_hybrid_oracle.c) drawn from
+the same seed, and against the HF Qwen3_5ForCausalLM logits fixture.
+
+Tolerance: 1e-3 of the step's largest |logit| (the device sums the int8
+matmuls in fp32 where the oracle sums in double and uses hardware exp and
+rsqrt; an fp16 rounding of an activation that lands the other side of a
+rounding boundary moves a logit by about 1e-4 of the largest), and the
+greedy token wherever the oracle's top-2 margin exceeds 2e-3 of it.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.gpu_util import dev, empty, host, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def hb():
+    torch = torch_mod()
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from orionsbelt_amd import hybrid
+    return hybrid
+
+
+@pytest.fixture(scope="module")
+def fixture(golden):
+    d = golden("hf_hybrid.npz")
+    fields = {f: d["cfg_" + f].item() for f, _ in orc.HybridConfig._fields_}
+    return d, fields
+
+
+def models(hb, fields, seed, **over):
+    f = dict(fields, **over)
+    return hb.HybridModel(hb.config(**f), seed), orc.HybridModel(
+        orc.HybridConfig(*[f[n] for n, _ in orc.HybridConfig._fields_]), seed)
+
+
+def step(gm, tokens, vocab):
+    torch = torch_mod()
+    nxt = empty((gm.batch,), torch.int32)
+    logits = empty((gm.batch, vocab), torch.float32)
+    gm.step(dev(np.asarray(tokens, np.int32)), nxt, logits)
+    return host(nxt), host(logits)
+
+
+def assert_close(lg, ref, what):
+    scale = np.abs(ref).max()
+    err = np.abs(lg - ref).max()
+    print(f"{what}: max |dlogit| {err:.3e} = {err / scale:.2e} of the largest")
+    assert err <= TOL * scale, what
+
+
+def assert_greedy(nxt, lg, ref):
+    # the device's token is its own logits' first maximum, exactly
+    assert np.array_equal(nxt, lg.argmax(1))
+    top2 = np.sort(ref, 1)[:, -2:]
+    clear = top2[:, 1] - top2[:, 0] > 2e-3 * np.abs(ref).max()
+    assert np.array_equal(nxt[clear], ref.argmax(1)[clear])
+
+
+def test_hybrid_teacher_forced_matches_oracle_and_hf(hb, fixture):
+    d, fields = fixture
+    gm, om = models(hb, fields, int(d["seed"]))
+    gm.reset(2, 0, 0)
+    om.reset(2, 0, 0)
+    tokens = d["tokens"]
+    for t in range(tokens.shape[1]):
+        nxt, lg = step(gm, tokens[:, t], fields["vocab"])
+        onxt, olg = om.step(tokens[:, t])
+        assert_close(lg, olg, f"step {t} vs oracle")
+        assert_close(lg, d["logits"][:, t], f"step {t} vs HF")
+        assert_greedy(nxt, lg, olg)
+    assert gm.position == tokens.shape[1]
+
+
+def test_hybrid_greedy_loop_on_device(hb, fixture):
+    """Tokens fed back on the device for 10 steps; the oracle replays the
+    device's tokens (teacher-forced) and checks each step's logits."""
+    d, fields = fixture
+    torch = torch_mod()
+    gm, om = models(hb, fields, int(d["seed"]))
+    gm.reset(2, 0, 0)
+    om.reset(2, 0, 0)
+    tok = dev(d["tokens"][:, 0].astype(np.int32))
+    logits = empty((2, fields["vocab"]), torch.float32)
+    for t in range(10):
+        fed = host(tok).copy()
+        nxt = empty((2,), torch.int32)
+        gm.step(tok, nxt, logits)
+        lg = host(logits)
+        _, olg = om.step(fed)
+        assert_close(lg, olg, f"greedy step {t}")
+        assert_greedy(host(nxt), lg, olg)
+        tok = nxt
+
+
+def test_hybrid_drawn_context_two_spans(hb, fixture):
+    """Three sequences after a drawn 300-token context (the attention decode
+    reads two 256-position spans and combines them)."""
+    d, fields = fixture
+    gm, om = models(hb, fields, 77, max_batch=3, max_context=320)
+    gm.reset(3, 300, 9)
+    om.reset(3, 300, 9)
+    rs = np.random.RandomState(2)
+    for t in range(3):
+        tok = rs.randint(0, fields["vocab"], 3)
+        nxt, lg = step(gm, tok, fields["vocab"])
+        _, olg = om.step(tok)
+        assert_close(lg, olg, f"context 300 step {t}")
+        assert_greedy(nxt, lg, olg)
+    assert gm.position == 303
+
+
+def test_hybrid_batch_rows_independent_and_deterministic(hb, fixture):
+    d, fields = fixture
+    gm, _ = models(hb, fields, int(d["seed"]))
+    tokens = d["tokens"]
+    gm.reset(2, 0, 0)
+    both = [step(gm, tokens[:, t], fields["vocab"])[1] for t in range(4)]
+    gm.reset(1, 0, 0)
+    one = [step(gm, tokens[1:, t], fields["vocab"])[1] for t in range(4)]
+    gm.reset(2, 0, 0)
+    again = [step(gm, tokens[:, t], fields["vocab"])[1] for t in range(4)]
+    for a, b, c in zip(both, one, again):
+        assert np.array_equal(a[1], b[0])
+        assert np.array_equal(a, c)
+
+
+def test_hybrid_rejects_bad_arguments(hb, fixture):
+    d, fields = fixture
+    from orionsbelt_amd import HipError
+    gm = hb.HybridModel(hb.config(**dict(fields, max_context=4)), 1)
+    with pytest.raises(HipError):
+        gm.reset(3, 0, 0)   # batch above max_batch
+    with pytest.raises(HipError):
+        gm.reset(1, 4, 0)   # context must leave room for a step
+    gm.reset(1, 3, 0)
+    step(gm, [5], fields["vocab"])
+    with pytest.raises(HipError):
+        step(gm, [5], fields["vocab"])  # the KV cache is full
+    with pytest.raises(HipError):
+        hb.HybridModel(hb.config(**dict(fields, hidden=200)), 1)   # hidden % 256
+    with pytest.raises(HipError):
+        hb.HybridModel(hb.config(**dict(fields, attn_q_heads=8)), 1)   # 8 q heads per kv head
+
+
+def test_hybrid_qwen35_4b_shape(hb):
+    """The full Qwen3.5-4B shape at batch 2 after a drawn 4000-token context,
+    three greedy steps: finite logits, in-range tokens, bit-identical on a
+    replay from the same reset."""
+    torch = torch_mod()
+    cfg = hb.qwen35_4b(2, 4096)
+    assert (cfg.layers, cfg.hidden, cfg.inter, cfg.vocab) == (32, 2560, 9216, 151936)
+    gm = hb.HybridModel(cfg, 12345)
+    assert gm.weight_bytes > 3.9e9
+    outs = []
+    for _ in range(2):
+        gm.reset(2, 4000, 7)
+        nxt = empty((2,), torch.int32)
+        logits = empty((2, cfg.vocab), torch.float32)
+        run = []
+        tok = dev(np.array([17, 151935], np.int32))
+        for _t in range(3):
+            gm.step(tok, nxt, logits)
+            run.append((host(nxt).copy(), host(logits).copy()))
+            tok = nxt.clone()
+        outs.append(run)
+    for (n1, l1), (n2, l2) in zip(*outs):
+        assert np.isfinite(l1).all()
+        assert ((n1 >= 0) & (n1 < cfg.vocab)).all()
+        assert np.array_equal(n1, l1.argmax(1))
+        assert np.array_equal(l1, l2) and np.array_equal(n1, n2)
+    assert gm.position == 4003
+    gm.close()

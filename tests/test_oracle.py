@@ -596,3 +596,66 @@ def test_attn_decode_closed_forms():
     p = np.exp(s - s.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
     np.testing.assert_allclose(o, np.einsum("bht,bhtd->bhd", p, vv), rtol=1e-6, atol=1e-7)
+
+
+# ---- hybrid decode loop ----------------------------------------------------
+
+def _hybrid_fixture(golden):
+    d = golden("hf_hybrid.npz")
+    cfg = orc.HybridConfig(*[d["cfg_" + f].item() for f, _ in orc.HybridConfig._fields_])
+    return d, cfg
+
+
+def test_hybrid_oracle_matches_hf_logits(golden):
+    """Teacher-forced decode steps of the oracle model from an empty context
+    against HF Qwen3_5ForCausalLM (fp32, eager attention) run over the whole
+    sequence at once on the same dequantised weights.  The oracle rounds
+    every matmul input and the KV cache to fp16, HF keeps fp32: 1e-3 of the
+    largest logit bounds that (observed 2.6e-4); a flipped rotary sign, a
+    missing output gate, a dropped q scale or a short attention window each
+    move the logits by more than 2e-2 of it."""
+    d, cfg = _hybrid_fixture(golden)
+    m = orc.HybridModel(cfg, int(d["seed"]))
+    m.reset(2, 0, 0)
+    tokens, ref = d["tokens"], d["logits"]
+    for t in range(tokens.shape[1]):
+        nxt, lg = m.step(tokens[:, t])
+        r = ref[:, t]
+        assert np.abs(lg - r).max() <= 1e-3 * np.abs(r).max(), t
+        top2 = np.sort(r, 1)[:, -2:]
+        clear = top2[:, 1] - top2[:, 0] > 2e-3 * np.abs(r).max()
+        assert np.array_equal(nxt[clear], r.argmax(1)[clear])
+    assert m.position == tokens.shape[1]
+
+
+def test_hybrid_oracle_batch_rows_independent(golden):
+    """A sequence's logits do not depend on the other rows of the batch, and
+    reset(context=0) restores the empty state exactly."""
+    d, cfg = _hybrid_fixture(golden)
+    m = orc.HybridModel(cfg, int(d["seed"]))
+    tokens = d["tokens"]
+    m.reset(2, 0, 0)
+    both = [m.step(tokens[:, t])[1] for t in range(4)]
+    m.reset(1, 0, 0)
+    one = [m.step(tokens[1:, t])[1] for t in range(4)]
+    for a, b in zip(both, one):
+        assert np.array_equal(a[1], b[0])
+    m.reset(2, 0, 0)
+    again = [m.step(tokens[:, t])[1] for t in range(4)]
+    for a, b in zip(both, again):
+        assert np.array_equal(a, b)
+
+
+def test_hybrid_oracle_drawn_context(golden):
+    """reset(context > 0) draws the states for the context deterministically
+    from the seed; different seeds give different continuations."""
+    d, cfg = _hybrid_fixture(golden)
+    m = orc.HybridModel(cfg, int(d["seed"]))
+    tok = d["tokens"][:, 0]
+    m.reset(2, 20, 3)
+    a = m.step(tok)[1]
+    assert m.position == 21
+    m.reset(2, 20, 3)
+    assert np.array_equal(a, m.step(tok)[1])
+    m.reset(2, 20, 4)
+    assert not np.allclose(a, m.step(tok)[1])
