@@ -38,7 +38,7 @@ typedef struct kai_gdn_hybrid kai_gdn_hybrid;
 typedef struct {
     int layers;      /* 32 */
     int attn_every;  /* 4: layer i is full attention iff (i + 1) % attn_every == 0 */
-    int hidden;      /* 2560 (% 256 == 0) */
+    int hidden;      /* 2560 (% 256 == 0, <= 8192) */
     int inter;       /* 9216 (% 256 == 0) */
     int vocab;       /* 151936 (% 16 == 0) */
     int gdn_k_heads; /* 16; key and value head dims are 128 */

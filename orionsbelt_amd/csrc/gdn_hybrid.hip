@@ -85,23 +85,55 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t *tokens, const
 }
 
 // Qwen3_5RMSNorm (modeling_qwen3_5.py:720-737) with the residual add fused:
-// h += d (when d), out = fp16(h / sqrt(mean(h^2) + eps) * (1 + w)).
-__global__ __launch_bounds__(256) void addnorm_kernel(float *h, const float *d, const float *w,
-                                                      uint16_t *out, int H, float eps) {
+// h += d (when d), out = fp16(h / sqrt(mean(h^2) + eps) * (1 + w)).  One
+// block per row; thread t holds the float4 chunks t, t + 256, ... (H / 4 <=
+// 256 kNormChunks), all loaded before any arithmetic.
+constexpr int kNormChunks = 8;
+__global__ __launch_bounds__(256) void addnorm_kernel(float *__restrict__ h, const float *__restrict__ d,
+                                                      const float *__restrict__ w, uint16_t *__restrict__ out,
+                                                      int H, float eps) {
     __shared__ float red[4];
     const size_t b = blockIdx.x;
-    float *hr = h + b * H;
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < H; i += 256) {
-        float x = hr[i];
-        if (d) {
-            x += d[b * H + i];
-            hr[i] = x;
+    float4 *hr = reinterpret_cast<float4 *>(h + b * H);
+    const int n4 = H / 4;
+    float4 x[kNormChunks], dv[kNormChunks];
+#pragma unroll
+    for (int j = 0; j < kNormChunks; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n4) {
+            x[j] = hr[i];
+            if (d) dv[j] = reinterpret_cast<const float4 *>(d + b * H)[i];
         }
-        ss += x * x;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormChunks; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n4) {
+            if (d) {
+                x[j].x += dv[j].x;
+                x[j].y += dv[j].y;
+                x[j].z += dv[j].z;
+                x[j].w += dv[j].w;
+                hr[i] = x[j];
+            }
+            ss += x[j].x * x[j].x + x[j].y * x[j].y + x[j].z * x[j].z + x[j].w * x[j].w;
+        }
     }
     const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
-    for (int i = threadIdx.x; i < H; i += 256) out[b * H + i] = f32_to_f16_rne(hr[i] * inv * (1.0f + w[i]));
+#pragma unroll
+    for (int j = 0; j < kNormChunks; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n4) {
+            const float4 wv = reinterpret_cast<const float4 *>(w)[i];
+            uint2 o;
+            o.x = (uint32_t)f32_to_f16_rne(x[j].x * inv * (1.0f + wv.x)) |
+                  ((uint32_t)f32_to_f16_rne(x[j].y * inv * (1.0f + wv.y)) << 16);
+            o.y = (uint32_t)f32_to_f16_rne(x[j].z * inv * (1.0f + wv.z)) |
+                  ((uint32_t)f32_to_f16_rne(x[j].w * inv * (1.0f + wv.w)) << 16);
+            reinterpret_cast<uint2 *>(out + b * H)[i] = o;
+        }
+    }
 }
 
 // Attention prologue (Qwen3_5Attention.forward:656-681): block (slot, b),
@@ -143,15 +175,6 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     else Kc[(((size_t)b * Hkv + (slot - Hq)) * Tmax + pos) * 256 + d] = o;
 }
 
-// o16 = fp16(attn * sigmoid(gate)), gate = dims 256..511 of qg's head.
-__global__ __launch_bounds__(256) void attn_post_kernel(const float *ao, const float *qg, uint16_t *o16,
-                                                        int Hq) {
-    const size_t bh = blockIdx.x;  // b * Hq + h
-    const int d = threadIdx.x;
-    const float gt = qg[bh * 512 + 256 + d];
-    o16[bh * 256 + d] = f32_to_f16_rne(ao[bh * 256 + d] * (1.0f / (1.0f + expf(-gt))));
-}
-
 // Qwen3_5MLP (modeling_qwen3_5.py:704-717): act = fp16(silu(gate) * up).
 __global__ __launch_bounds__(256) void swiglu_kernel(const float *gate, const float *up, uint16_t *out,
                                                      size_t n) {
@@ -161,35 +184,65 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float *gate, const fl
     }
 }
 
-// next[b] = the first index of the largest logit of row b.
-__global__ __launch_bounds__(256) void argmax_kernel(const float *logits, int32_t *next, int V) {
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    const float *row = logits + (size_t)blockIdx.x * V;
+// next[b] = the first index of the largest logit of row b.  Block (j, b)
+// scans slice j of the row into part[b][j] = (value, index); the last block
+// of row b to finish (counter cnt[b], left at 0 for the next launch) merges
+// the slices: the largest value, the smallest index among equals, so the
+// result does not depend on the order the blocks finish.
+constexpr int kArgBlocks = 64;
+GDN_DEV void arg_merge(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+GDN_DEV void arg_block(float &v, int &i, float *sv, int *si) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) arg_merge(v, i, __shfl_xor(v, o), __shfl_xor(i, o));
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = v;
+        si[threadIdx.x >> 6] = i;
+    }
+    __syncthreads();
+    v = sv[0];
+    i = si[0];
+    for (int k = 1; k < 4; ++k) arg_merge(v, i, sv[k], si[k]);
+}
+__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int32_t *__restrict__ next,
+                                                     int V, uint64_t *__restrict__ part, uint32_t *__restrict__ cnt) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    __shared__ bool last;
+    const int b = blockIdx.y, j = blockIdx.x;
+    const int per = (V + kArgBlocks - 1) / kArgBlocks;
+    const int lo = j * per, hi = min(V, lo + per);
+    const float *row = logits + (size_t)b * V;
     float best = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < V; i += 256) {
-        const float v = row[i];
-        if (v > best) {  // first occurrence within the thread's stride
-            best = v;
-            bi = i;
-        }
+    for (int i = lo + threadIdx.x; i < hi; i += 256) arg_merge(best, bi, row[i], i);
+    arg_block(best, bi, sv, si);
+    if (threadIdx.x == 0) {
+        part[b * kArgBlocks + j] = ((uint64_t)__float_as_uint(best) << 32) | (uint32_t)bi;
+        __threadfence();
+        last = atomicAdd(&cnt[b], 1u) == kArgBlocks - 1;
     }
-    sv[threadIdx.x] = best;
-    si[threadIdx.x] = bi;
     __syncthreads();
-    for (int s = 128; s >= 1; s >>= 1) {
-        if (threadIdx.x < s) {
-            const float v2 = sv[threadIdx.x + s];
-            const int i2 = si[threadIdx.x + s];
-            if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
-                sv[threadIdx.x] = v2;
-                si[threadIdx.x] = i2;
-            }
-        }
-        __syncthreads();
+    if (!last) return;
+    __threadfence();
+    float v = -INFINITY;
+    int i = 0x7FFFFFFF;
+    if (threadIdx.x < kArgBlocks) {
+        const uint64_t pv = __hip_atomic_load(&part[b * kArgBlocks + threadIdx.x], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+        v = __uint_as_float((uint32_t)(pv >> 32));
+        i = (int)(uint32_t)pv;
     }
-    if (threadIdx.x == 0) next[blockIdx.x] = si[0];
+    __syncthreads();
+    arg_block(v, i, sv, si);
+    if (threadIdx.x == 0) {
+        next[b] = i;
+        __hip_atomic_store(&cnt[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ---- model -------------------------------------------------------------------
@@ -236,8 +289,10 @@ struct kai_gdn_hybrid {
     float *h = nullptr, *mix = nullptr, *mlp = nullptr, *big0 = nullptr, *big1 = nullptr;
     float *qkv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr, *qb = nullptr, *kb = nullptr,
           *vb = nullptr, *gb = nullptr, *betab = nullptr, *ob = nullptr, *yb = nullptr;
-    float *qg = nullptr, *kx = nullptr, *vx = nullptr, *ao = nullptr, *logits = nullptr;
+    float *qg = nullptr, *kx = nullptr, *vx = nullptr, *logits = nullptr;
     int32_t *next = nullptr;
+    uint64_t *arg_part = nullptr;  // [max_batch][kArgBlocks]
+    uint32_t *arg_cnt = nullptr;   // [max_batch], zero between launches
     uint16_t *x16 = nullptr, *q16 = nullptr;
     float *gemm_ws = nullptr, *attn_ws = nullptr;
     size_t gemm_ws_bytes = 0, attn_ws_bytes = 0;
@@ -368,9 +423,11 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         TRY(alloc_t(m, &m->yb, (size_t)Bm * m->value_dim));
         TRY(alloc_t(m, &m->kx, (size_t)Bm * Hkv * 256));
         TRY(alloc_t(m, &m->vx, (size_t)Bm * Hkv * 256));
-        TRY(alloc_t(m, &m->ao, (size_t)Bm * Hq * 256));
         TRY(alloc_t(m, &m->logits, (size_t)Bm * c.vocab));
         TRY(alloc_t(m, &m->next, (size_t)Bm));
+        TRY(alloc_t(m, &m->arg_part, (size_t)Bm * kArgBlocks));
+        TRY(alloc_t(m, &m->arg_cnt, (size_t)Bm));
+        TRY(hipMemset(m->arg_cnt, 0, (size_t)Bm * sizeof(uint32_t)));
         TRY(alloc_t(m, &m->x16, (size_t)Bm * wide));
         TRY(alloc_t(m, &m->q16, (size_t)Bm * Hq * 256));
         m->qkv = m->big0;
@@ -417,10 +474,9 @@ hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
                                                                  L.Kc, L.Vc, Hq, Hkv, c.max_context, m->pos,
                                                                  c.rope_theta, c.rms_eps);
     TRY(hipGetLastError());
-    TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, m->ao, B, Hq, Hkv, c.max_context, m->pos + 1, 1.0f / 16.0f,
-                           m->attn_ws, st));
-    attn_post_kernel<<<B * Hq, 256, 0, st>>>(m->ao, m->qg, m->x16, Hq);
-    TRY(hipGetLastError());
+    // o * sigmoid(gate) -> fp16 in the span combine; gate = dims 256..511 of each qg head
+    TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, nullptr, B, Hq, Hkv, c.max_context, m->pos + 1, 1.0f / 16.0f,
+                           m->attn_ws, st, m->qg + 256, 512, m->x16));
     return gemm(m, m->x16, L.op, m->mix, st);
 }
 
@@ -448,7 +504,8 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
     TRY(hipGetLastError());
     float *lg = logits ? logits : m->logits;
     TRY(gemm(m, m->x16, m->lm, lg, st));
-    argmax_kernel<<<B, 256, 0, st>>>(lg, next ? next : m->next, c.vocab);
+    argmax_kernel<<<dim3(kArgBlocks, B), 256, 0, st>>>(lg, next ? next : m->next, c.vocab, m->arg_part,
+                                                       m->arg_cnt);
     TRY(hipGetLastError());
     ++m->pos;
     return hipSuccess;
@@ -512,7 +569,8 @@ extern "C" int kai_gdn_hybrid_create(const kai_gdn_hybrid_config *cfg, unsigned 
                                      kai_gdn_hybrid **out) {
     if (!cfg || !out) return (int)hipErrorInvalidValue;
     const kai_gdn_hybrid_config &c = *cfg;
-    const bool ok = c.layers > 0 && c.attn_every > 0 && c.hidden > 0 && c.hidden % 256 == 0 && c.inter > 0 &&
+    const bool ok = c.layers > 0 && c.attn_every > 0 && c.hidden > 0 && c.hidden % 256 == 0 &&
+                    c.hidden <= 4 * 256 * gdn::kNormChunks && c.inter > 0 &&
                     c.inter % 256 == 0 && c.vocab > 0 && c.vocab % 16 == 0 && c.gdn_k_heads > 0 &&
                     c.gdn_v_heads % 16 == 0 && c.gdn_v_heads % c.gdn_k_heads == 0 && c.gdn_v_heads > 0 &&
                     c.attn_kv_heads > 0 && c.attn_q_heads % c.attn_kv_heads == 0 &&

@@ -113,9 +113,12 @@ hipError_t launch_w8_gemm(const uint16_t *x, const int8_t *W, const float *scale
 hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K, hipStream_t st);
 // Attention decode over an fp16 KV cache (head_dim 256, Hq / Hkv <= 4):
 // out [B][Hq][256] fp32; `workspace` holds attn_workspace_bytes(B, Hq, L).
+// With `gate` (non-null), the output is instead out16 [B][Hq][256] fp16 =
+// fp16(o * sigmoid(gate[(b * Hq + h) * gate_stride + d])).
 size_t attn_workspace_bytes(int B, int Hq, int L);
 hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
                               int B, int Hq, int Hkv, int Tmax, int L, float scaling, float *workspace,
-                              hipStream_t st);
+                              hipStream_t st, const float *gate = nullptr, int gate_stride = 0,
+                              uint16_t *out16 = nullptr);
 
 }  // namespace gdn

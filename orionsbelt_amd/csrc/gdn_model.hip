@@ -228,18 +228,34 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__rest
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[h][i] = 0.f;
     }
+    // Groups of 16 positions, double-buffered: the K rows and V rows of
+    // group n + 1 are in flight while group n is scored and accumulated.
+    // Rows past L are clamped to L - 1 (in bounds; masked by p = 0).
     const int t_begin = span * kAttSpan + wave * 64;
+    u32x4_t kbuf[2][8];
+    u32x2_t vbuf[2][16];
+    auto load_group = [&](int t0, u32x4_t (&kb)[8], u32x2_t (&vb)[16]) {
+        const uint16_t *kp = Kc + (kvrow + min(t0 + r, L - 1)) * kAttD + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            kb[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(kp + 32 * j));
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            vb[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x2_t *>(Vc + (kvrow + min(t0 + i, L - 1)) * kAttD + 4 * lane));
+    };
+    if (t_begin < L) load_group(t_begin, kbuf[0], vbuf[0]);
+#pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
         const int t0 = t_begin + 16 * grp;
         if (t0 >= L) break;  // uniform over the wave
-        const int tr = min(t0 + r, L - 1);  // key row of this lane (clamped; masked below)
-        const uint16_t *kp = Kc + (kvrow + tr) * kAttD + 8 * g;
+        if (grp < 3 && t0 + 16 < L) load_group(t0 + 16, kbuf[(grp + 1) & 1], vbuf[(grp + 1) & 1]);
+        const u32x4_t(&kb)[8] = kbuf[grp & 1];
+        const u32x2_t(&vb)[16] = vbuf[grp & 1];
         f32x4_t acc = zero4();
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                __builtin_bit_cast(f16x8_t, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(kp + 32 * j))),
-                qb[j], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, kb[j]), qb[j], acc, 0, 0, 0);
         // lane (g, r): scores of positions t0 + 4g + e for head r, in log2 units
         float s[4];
 #pragma unroll
@@ -275,15 +291,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__rest
             for (int i = 0; i < 4; ++i) o[h][i] *= a_h;
         }
         // P.V: position t0 + 4gg + e, head h: p in lane 16 gg + h, element e
+        // (p = 0 for positions past L)
 #pragma unroll
         for (int gg = 0; gg < 4; ++gg)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int t = t0 + 4 * gg + e;
-                if (t >= L) continue;  // uniform
-                const uint2 vv = *reinterpret_cast<const uint2 *>(Vc + (kvrow + t) * kAttD + 4 * lane);
-                const float v[4] = {f16_to_f32((uint16_t)(vv.x & 0xFFFFu)), f16_to_f32((uint16_t)(vv.x >> 16)),
-                                    f16_to_f32((uint16_t)(vv.y & 0xFFFFu)), f16_to_f32((uint16_t)(vv.y >> 16))};
+                const u32x2_t vv = vb[4 * gg + e];
+                const float v[4] = {f16_to_f32((uint16_t)(vv[0] & 0xFFFFu)), f16_to_f32((uint16_t)(vv[0] >> 16)),
+                                    f16_to_f32((uint16_t)(vv[1] & 0xFFFFu)), f16_to_f32((uint16_t)(vv[1] >> 16))};
 #pragma unroll
                 for (int h = 0; h < kAttRepMax; ++h) {
                     if (h >= rep) break;
@@ -329,22 +344,56 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__rest
     }
 }
 
-// o[b][h][d] = sum_s e^{m_s - M} o_s[d] / sum_s e^{m_s - M} l_s (log2 units).
+// o[b][h][d] = sum_s e^{m_s - M} o_s[d] / sum_s e^{m_s - M} l_s (log2 units),
+// one block per (b, h): wave j takes the spans s = j mod 4, lane l dims
+// 4l .. 4l+3; the four waves merge in a fixed order.  With `gate`, the
+// output is fp16(o * sigmoid(gate[bh * gate_stride + d])) into out16
+// (the sigmoid output gate of Qwen3_5Attention), else fp32 into out.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part,
-                                                           float *__restrict__ out, int nspan) {
+                                                           float *__restrict__ out, const float *__restrict__ gate,
+                                                           int gate_stride, uint16_t *__restrict__ out16,
+                                                           int nspan) {
+    __shared__ float s_red[4];
+    __shared__ float s_l[4];
+    __shared__ float4 s_o[4][64];
     const size_t bh = blockIdx.x;
     const float *pp = part + bh * nspan * kAttPart;
-    const int d = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float M = -INFINITY;
-    for (int s = 0; s < nspan; ++s) M = fmaxf(M, pp[s * kAttPart + kAttD]);
-    float lsum = 0.f, acc = 0.f;
-    for (int s = 0; s < nspan; ++s) {
-        const float ms = pp[s * kAttPart + kAttD];
+    for (int s = tid; s < nspan; s += 256) M = fmaxf(M, pp[s * kAttPart + kAttD]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    if (lane == 0) s_red[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float lsum = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int s = wave; s < nspan; s += 4) {
+        const float *ps = pp + s * kAttPart;
+        const float ms = ps[kAttD];
         const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-        lsum += f * pp[s * kAttPart + kAttD + 1];
-        acc += f * pp[s * kAttPart + d];
+        lsum += f * ps[kAttD + 1];
+        const float4 v = *reinterpret_cast<const float4 *>(ps + 4 * lane);
+        acc.x += f * v.x;
+        acc.y += f * v.y;
+        acc.z += f * v.z;
+        acc.w += f * v.w;
     }
-    out[bh * kAttD + d] = acc / lsum;
+    s_o[wave][lane] = acc;
+    if (lane == 0) s_l[wave] = lsum;
+    __syncthreads();
+    const int d = tid;
+    const float *so = reinterpret_cast<const float *>(s_o);
+    const float num = ((so[d] + so[256 + d]) + so[512 + d]) + so[768 + d];
+    const float den = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
+    const float y = num / den;
+    if (gate) {
+        const float gt = gate[bh * gate_stride + d];
+        out16[bh * kAttD + d] = f32_to_f16_rne(y * (1.0f / (1.0f + expf(-gt))));
+    } else {
+        out[bh * kAttD + d] = y;
+    }
 }
 
 }  // namespace
@@ -356,7 +405,7 @@ size_t attn_workspace_bytes(int B, int Hq, int L) {
 
 hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
                               int B, int Hq, int Hkv, int Tmax, int L, float scaling, float *workspace,
-                              hipStream_t st) {
+                              hipStream_t st, const float *gate, int gate_stride, uint16_t *out16) {
     if (B == 0) return hipSuccess;
     const int nspan = (L + kAttSpan - 1) / kAttSpan;
     const float sc_log2 = scaling * 1.4426950408889634f;
@@ -364,7 +413,7 @@ hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint1
                                                             sc_log2);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_combine_kernel<<<dim3(B * Hq), kAttD, 0, st>>>(workspace, out, nspan);
+    attn_combine_kernel<<<dim3(B * Hq), kAttD, 0, st>>>(workspace, out, gate, gate_stride, out16, nspan);
     return hipGetLastError();
 }
 
