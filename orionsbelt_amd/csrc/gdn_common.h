@@ -93,3 +93,31 @@ template <bool NT> GDN_DEV void store_u2(void *p, u32x2_t v) {
     if constexpr (NT) __builtin_nontemporal_store(v, q);
     else *q = v;
 }
+
+// ---- device-wide hand-off between the blocks of one launch -----------------
+// The "last block finishes the reduction" pattern.  An agent-scope fence
+// (__threadfence) writes back and invalidates this XCD's whole L2 on gfx950,
+// so the data that crosses blocks travels by agent-scope relaxed atomics
+// instead (stores written through, loads from the coherence point): a block
+// stores its partials with store_agent, waits for their acknowledgement
+// (stores_done), then bumps the counter with an agent-scope
+// atomic; the block that sees the last count reads every partial with
+// load_agent.  Ordinary loads and stores keep their caches.
+GDN_DEV void store_agent(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GDN_DEV void store_agent(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+GDN_DEV float load_agent(float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GDN_DEV uint64_t load_agent(uint64_t *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// This wave's stores acknowledged before what follows (a workgroup-scope
+// release emits no wait for global stores on gfx950, an agent-scope one
+// writes back the L2).
+GDN_DEV void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Increment the counter; true for the caller that brings it to `total` (it
+// also returns the counter to 0 for the next launch).
+GDN_DEV bool arrive_last(uint32_t *cnt, uint32_t total) {
+    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old != total - 1) return false;
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}

@@ -13,9 +13,14 @@
 //                q/k RMSNorm, partial rotary embedding, KV append -> decode
 //                attention over the cache -> o * sigmoid(gate) -> o_proj
 //   logits = lm_head(rmsnorm(h)), next = argmax
-// The residual add is fused into the following RMSNorm.  Everything a matmul
-// reads is fp16 (the model's activation dtype), everything it writes fp32.
+// The residual add is fused into the following RMSNorm, the projections that
+// share an input are one int8 GEMM launch (qkv|z|b|a; q|k|v; gate|up with
+// the SiLU product in its epilogue), and the output gate is applied in the
+// attention's span combine.  Everything a matmul reads is fp16 (the model's
+// activation dtype), everything it writes fp32 (the MLP activation fp16).
+#include <algorithm>
 #include <cmath>
+#include <initializer_list>
 #include <vector>
 
 #include "gdn_common.h"
@@ -175,18 +180,9 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     else Kc[(((size_t)b * Hkv + (slot - Hq)) * Tmax + pos) * 256 + d] = o;
 }
 
-// Qwen3_5MLP (modeling_qwen3_5.py:704-717): act = fp16(silu(gate) * up).
-__global__ __launch_bounds__(256) void swiglu_kernel(const float *gate, const float *up, uint16_t *out,
-                                                     size_t n) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        const float g = gate[i];
-        out[i] = f32_to_f16_rne(g / (1.0f + expf(-g)) * up[i]);
-    }
-}
-
 // next[b] = the first index of the largest logit of row b.  Block (j, b)
 // scans slice j of the row into part[b][j] = (value, index); the last block
-// of row b to finish (counter cnt[b], left at 0 for the next launch) merges
+// of row b to finish (counter cnt[b], returned to 0 for the next launch) merges
 // the slices: the largest value, the smallest index among equals, so the
 // result does not depend on the order the blocks finish.
 constexpr int kArgBlocks = 64;
@@ -222,27 +218,22 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ l
     for (int i = lo + threadIdx.x; i < hi; i += 256) arg_merge(best, bi, row[i], i);
     arg_block(best, bi, sv, si);
     if (threadIdx.x == 0) {
-        part[b * kArgBlocks + j] = ((uint64_t)__float_as_uint(best) << 32) | (uint32_t)bi;
-        __threadfence();
-        last = atomicAdd(&cnt[b], 1u) == kArgBlocks - 1;
+        store_agent(&part[b * kArgBlocks + j], ((uint64_t)__float_as_uint(best) << 32) | (uint32_t)bi);
+        stores_done();
+        last = arrive_last(&cnt[b], kArgBlocks);
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     float v = -INFINITY;
     int i = 0x7FFFFFFF;
     if (threadIdx.x < kArgBlocks) {
-        const uint64_t pv = __hip_atomic_load(&part[b * kArgBlocks + threadIdx.x], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t pv = load_agent(&part[b * kArgBlocks + threadIdx.x]);
         v = __uint_as_float((uint32_t)(pv >> 32));
         i = (int)(uint32_t)pv;
     }
     __syncthreads();
     arg_block(v, i, sv, si);
-    if (threadIdx.x == 0) {
-        next[b] = i;
-        __hip_atomic_store(&cnt[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (threadIdx.x == 0) next[b] = i;
 }
 
 // ---- model -------------------------------------------------------------------
@@ -257,6 +248,12 @@ enum : int { kEmbed = 1, kFinalNorm = 2, kLmHead = 3 };
 enum : int { kStConv = 0, kStS = 1, kStK = 2, kStV = 3 };
 constexpr float kWAmp = 0.034641016f;  // uniform amplitude of std 0.02
 
+// An int8 weight matrix [N][K] with per-output-channel scales.  The
+// matrices of a layer that read the same input are one Mat, their rows
+// concatenated (GDN: in_proj_qkv | in_proj_z | in_proj_b | in_proj_a;
+// attention: q_proj | k_proj | v_proj) or interleaved (MLP: gate_proj and
+// up_proj in alternating groups of 8 rows), zero rows padding N to a
+// multiple of 64.
 struct Mat {
     int8_t *q = nullptr;
     float *s = nullptr;
@@ -266,14 +263,30 @@ struct Mat {
 struct Layer {
     bool attn = false;
     float *ln_in = nullptr, *ln_post = nullptr;
-    Mat qkv, z, bp, ap, out;  // GDN
+    Mat in, out;  // GDN: [qkv | z | b | a], out_proj; attention: [q | k | v], o_proj
     float *conv_w = nullptr, *dt_bias = nullptr, *A_log = nullptr, *norm_w = nullptr;
-    Mat qp, kp, vp, op;  // attention
     float *q_norm = nullptr, *k_norm = nullptr;
-    Mat gate, up, down;
+    Mat gate_up, down;
     float *S = nullptr, *conv_state = nullptr;  // [B][Hv][128][128], [B][conv_dim][4]
     uint16_t *Kc = nullptr, *Vc = nullptr;      // [B][Hkv][Tmax][256]
 };
+
+// Rows of the interleaved gate/up matrix: row R takes row 8 (R / 16) + R % 8
+// of gate (R % 16 < 8) or of up.
+__global__ __launch_bounds__(256) void interleave_rows_kernel(const int8_t *__restrict__ ga,
+                                                              const int8_t *__restrict__ up,
+                                                              const float *__restrict__ sg,
+                                                              const float *__restrict__ su,
+                                                              int8_t *__restrict__ out, float *__restrict__ so,
+                                                              int K) {
+    const int R = blockIdx.x;
+    const int w = R & 15;
+    const int n = (R >> 4) * 8 + (w & 7);
+    const int8_t *src = (w < 8 ? ga : up) + (size_t)n * K;
+    for (int i = threadIdx.x * 16; i < K; i += 256 * 16)
+        *reinterpret_cast<uint4 *>(out + (size_t)R * K + i) = *reinterpret_cast<const uint4 *>(src + i);
+    if (threadIdx.x == 0) so[R] = w < 8 ? sg[n] : su[n];
+}
 
 }  // namespace
 }  // namespace gdn
@@ -286,16 +299,16 @@ struct kai_gdn_hybrid {
     float *final_norm = nullptr;
     gdn::Mat lm;
     // step buffers
-    float *h = nullptr, *mix = nullptr, *mlp = nullptr, *big0 = nullptr, *big1 = nullptr;
-    float *qkv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr, *qb = nullptr, *kb = nullptr,
-          *vb = nullptr, *gb = nullptr, *betab = nullptr, *ob = nullptr, *yb = nullptr;
+    float *h = nullptr, *mix = nullptr, *mlp = nullptr;
+    float *qkv = nullptr, *cv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr, *qb = nullptr,
+          *kb = nullptr, *vb = nullptr, *gb = nullptr, *betab = nullptr, *ob = nullptr, *yb = nullptr;
     float *qg = nullptr, *kx = nullptr, *vx = nullptr, *logits = nullptr;
     int32_t *next = nullptr;
     uint64_t *arg_part = nullptr;  // [max_batch][kArgBlocks]
     uint32_t *arg_cnt = nullptr;   // [max_batch], zero between launches
-    uint16_t *x16 = nullptr, *q16 = nullptr;
-    float *gemm_ws = nullptr, *attn_ws = nullptr;
-    size_t gemm_ws_bytes = 0, attn_ws_bytes = 0;
+    uint16_t *x16 = nullptr, *act16 = nullptr, *q16 = nullptr;
+    float *gemm_part = nullptr, *attn_ws = nullptr;
+    uint32_t *gemm_cnt = nullptr;  // zero between launches
     std::vector<void *> allocs;
     size_t bytes = 0, weight_bytes = 0;
     int batch = 0, pos = 0;
@@ -321,17 +334,68 @@ hipError_t fill(float *dst, size_t n, uint64_t seed, uint64_t stream, float amp,
     return hipGetLastError();
 }
 
-// A drawn int8 matrix [N][K] with per-output-channel scales.
-hipError_t make_mat(kai_gdn_hybrid *m, Mat &w, int N, int K, uint64_t seed, uint64_t stream, float *tmp) {
-    w.N = N;
+#define TRY(x)                              \
+    do {                                    \
+        hipError_t e_ = (x);                \
+        if (e_ != hipSuccess) return e_;    \
+    } while (0)
+
+int pad64(int n) { return (n + 63) / 64 * 64; }
+
+struct Part {
+    int rows;
+    uint64_t stream;
+};
+
+// Staging of the matrix builders: fp32 draws, row-major int8 (twice).
+struct Staging {
+    float *f = nullptr;
+    int8_t *q = nullptr, *q2 = nullptr;
+    float *s = nullptr;
+};
+
+// Drawn matrices concatenated by rows into one Mat; each part is drawn from
+// its own hash stream and quantised per output channel, then the whole
+// matrix is tiled for the GEMM.
+hipError_t make_fused(kai_gdn_hybrid *m, Mat &w, std::initializer_list<Part> parts, int K, uint64_t seed,
+                      const Staging &tmp) {
+    int used = 0;
+    for (const Part &p : parts) used += p.rows;
+    w.N = pad64(used);
     w.K = K;
-    hipError_t e;
-    if ((e = alloc_t(m, &w.q, (size_t)N * K)) != hipSuccess) return e;
-    if ((e = alloc_t(m, &w.s, (size_t)N)) != hipSuccess) return e;
-    if ((e = fill(tmp, (size_t)N * K, seed, stream, kWAmp, 0.f)) != hipSuccess) return e;
-    if ((e = launch_w8_quantize(tmp, w.q, w.s, N, K, nullptr)) != hipSuccess) return e;
-    m->weight_bytes += (size_t)N * K + (size_t)N * 4;
-    return hipSuccess;
+    TRY(alloc_t(m, &w.q, (size_t)w.N * K));
+    TRY(alloc_t(m, &w.s, (size_t)w.N));
+    if (w.N > used) {
+        TRY(hipMemset(tmp.q + (size_t)used * K, 0, (size_t)(w.N - used) * K));
+        TRY(fill(w.s + used, (size_t)(w.N - used), 0, 0, 0.f, 1.0f));
+    }
+    int off = 0;
+    for (const Part &p : parts) {
+        TRY(fill(tmp.f, (size_t)p.rows * K, seed, p.stream, kWAmp, 0.f));
+        TRY(launch_w8_quantize(tmp.f, tmp.q + (size_t)off * K, w.s + off, p.rows, K, nullptr));
+        off += p.rows;
+    }
+    TRY(launch_w8f_tile(tmp.q, w.q, w.N, K, nullptr));
+    m->weight_bytes += (size_t)w.N * K + (size_t)w.N * 4;
+    return hipDeviceSynchronize();
+}
+
+// gate_proj and up_proj [I][K], interleaved in groups of 8 rows, tiled.
+hipError_t make_gate_up(kai_gdn_hybrid *m, Mat &w, int I, int K, uint64_t seed, uint64_t sg, uint64_t su,
+                        const Staging &tmp) {
+    w.N = 2 * I;
+    w.K = K;
+    TRY(alloc_t(m, &w.q, (size_t)w.N * K));
+    TRY(alloc_t(m, &w.s, (size_t)w.N));
+    TRY(fill(tmp.f, (size_t)I * K, seed, sg, kWAmp, 0.f));
+    TRY(launch_w8_quantize(tmp.f, tmp.q, tmp.s, I, K, nullptr));
+    TRY(fill(tmp.f, (size_t)I * K, seed, su, kWAmp, 0.f));
+    TRY(launch_w8_quantize(tmp.f, tmp.q + (size_t)I * K, tmp.s + I, I, K, nullptr));
+    interleave_rows_kernel<<<w.N, 256>>>(tmp.q, tmp.q + (size_t)I * K, tmp.s, tmp.s + I, tmp.q2, w.s, K);
+    TRY(hipGetLastError());
+    TRY(launch_w8f_tile(tmp.q2, w.q, w.N, K, nullptr));
+    m->weight_bytes += (size_t)w.N * K + (size_t)w.N * 4;
+    return hipDeviceSynchronize();
 }
 
 hipError_t make_vec(kai_gdn_hybrid *m, float **v, size_t n, uint64_t seed, uint64_t stream, float amp,
@@ -340,15 +404,21 @@ hipError_t make_vec(kai_gdn_hybrid *m, float **v, size_t n, uint64_t seed, uint6
     return e != hipSuccess ? e : fill(*v, n, seed, stream, amp, center);
 }
 
-hipError_t gemm(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *y, hipStream_t st) {
-    return launch_w8_gemm(x, w.q, w.s, y, m->batch, w.N, w.K, m->gemm_ws, st);
+W8Out segments(std::initializer_list<W8Seg> segs) {
+    W8Out o{};
+    int q = 0;
+    for (const W8Seg &sg : segs) o.seg[q++] = sg;
+    o.nseg = q;
+    o.mode = kW8Segments;
+    return o;
 }
 
-#define TRY(x)                              \
-    do {                                    \
-        hipError_t e_ = (x);                \
-        if (e_ != hipSuccess) return e_;    \
-    } while (0)
+hipError_t gemm(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, const W8Out &o, hipStream_t st) {
+    return launch_w8f(x, w.q, w.s, m->batch, w.N, w.K, o, m->gemm_part, m->gemm_cnt, st);
+}
+hipError_t gemm_to(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *y, int ld, hipStream_t st) {
+    return gemm(m, x, w, segments({{y, ld, w.N}}), st);
+}
 
 hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
     const kai_gdn_hybrid_config &c = m->cfg;
@@ -356,14 +426,17 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
               Hkv = c.attn_kv_heads, Bm = c.max_batch;
     m->conv_dim = 2 * Hk * 128 + Hv * 128;
     m->value_dim = Hv * 128;
-    // the largest drawn matrix, fp32 staging for the quantiser
-    size_t tmp_n = (size_t)c.vocab * H;
-    tmp_n = std::max(tmp_n, (size_t)I * H);
-    tmp_n = std::max(tmp_n, (size_t)m->conv_dim * H);
-    tmp_n = std::max(tmp_n, (size_t)Hq * 512 * H);
-    float *tmp = nullptr;
-    TRY(hipMalloc(&tmp, tmp_n * 4));
+    // staging for the builders: the largest matrix (padded), fp32 and int8
+    const size_t tmp_n = std::max({(size_t)pad64(c.vocab) * H, (size_t)2 * I * H, (size_t)I * H,
+                                   (size_t)pad64(m->conv_dim + m->value_dim + 2 * Hv) * H,
+                                   (size_t)pad64(Hq * 512 + 2 * Hkv * 256) * H, (size_t)H * m->value_dim,
+                                   (size_t)H * Hq * 256});
+    Staging tmp;
     auto run = [&]() -> hipError_t {
+        TRY(hipMalloc(&tmp.f, tmp_n * 4));
+        TRY(hipMalloc(&tmp.q, tmp_n));
+        TRY(hipMalloc(&tmp.q2, (size_t)2 * I * H));
+        TRY(hipMalloc(&tmp.s, (size_t)2 * I * 4));
         m->layers.resize(c.layers);
         for (int l = 0; l < c.layers; ++l) {
             Layer &L = m->layers[l];
@@ -372,11 +445,9 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
             TRY(make_vec(m, &L.ln_in, H, seed, base + kLnIn, 0.1f, 0.f));
             TRY(make_vec(m, &L.ln_post, H, seed, base + kLnPost, 0.1f, 0.f));
             if (!L.attn) {
-                TRY(make_mat(m, L.qkv, m->conv_dim, H, seed, base + kQkv, tmp));
-                TRY(make_mat(m, L.z, m->value_dim, H, seed, base + kZ, tmp));
-                TRY(make_mat(m, L.bp, Hv, H, seed, base + kBp, tmp));
-                TRY(make_mat(m, L.ap, Hv, H, seed, base + kAp, tmp));
-                TRY(make_mat(m, L.out, H, m->value_dim, seed, base + kOut, tmp));
+                TRY(make_fused(m, L.in, {{m->conv_dim, base + kQkv}, {m->value_dim, base + kZ}, {Hv, base + kBp},
+                                         {Hv, base + kAp}}, H, seed, tmp));
+                TRY(make_fused(m, L.out, {{H, base + kOut}}, m->value_dim, seed, tmp));
                 TRY(make_vec(m, &L.conv_w, (size_t)m->conv_dim * 4, seed, base + kConvW, 0.5f, 0.f));
                 TRY(make_vec(m, &L.dt_bias, Hv, seed, base + kDtBias, 0.5f, 1.0f));
                 TRY(make_vec(m, &L.A_log, Hv, seed, base + kALog, 1.3862944f, 1.3862944f));  // U(0, ln 16)
@@ -384,33 +455,30 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
                 TRY(alloc_t(m, &L.S, (size_t)Bm * Hv * 128 * 128));
                 TRY(alloc_t(m, &L.conv_state, (size_t)Bm * m->conv_dim * 4));
             } else {
-                TRY(make_mat(m, L.qp, Hq * 512, H, seed, base + kQp, tmp));
-                TRY(make_mat(m, L.kp, Hkv * 256, H, seed, base + kKp, tmp));
-                TRY(make_mat(m, L.vp, Hkv * 256, H, seed, base + kVp, tmp));
-                TRY(make_mat(m, L.op, H, Hq * 256, seed, base + kOp, tmp));
+                TRY(make_fused(m, L.in, {{Hq * 512, base + kQp}, {Hkv * 256, base + kKp}, {Hkv * 256, base + kVp}},
+                               H, seed, tmp));
+                TRY(make_fused(m, L.out, {{H, base + kOp}}, Hq * 256, seed, tmp));
                 TRY(make_vec(m, &L.q_norm, 256, seed, base + kQn, 0.1f, 0.f));
                 TRY(make_vec(m, &L.k_norm, 256, seed, base + kKn, 0.1f, 0.f));
                 TRY(alloc_t(m, &L.Kc, (size_t)Bm * Hkv * c.max_context * 256));
                 TRY(alloc_t(m, &L.Vc, (size_t)Bm * Hkv * c.max_context * 256));
             }
-            TRY(make_mat(m, L.gate, I, H, seed, base + kGate, tmp));
-            TRY(make_mat(m, L.up, I, H, seed, base + kUp, tmp));
-            TRY(make_mat(m, L.down, H, I, seed, base + kDown, tmp));
+            TRY(make_gate_up(m, L.gate_up, I, H, seed, base + kGate, base + kUp, tmp));
+            TRY(make_fused(m, L.down, {{H, base + kDown}}, I, seed, tmp));
         }
         TRY(alloc_t(m, &m->embed, (size_t)c.vocab * H));
         fill_f16_kernel<<<fill_blocks((size_t)c.vocab * H), 256>>>(m->embed, (size_t)c.vocab * H, seed, kEmbed,
                                                                    1.0f, 0.f);
         TRY(hipGetLastError());
         TRY(make_vec(m, &m->final_norm, H, seed, kFinalNorm, 0.1f, 0.f));
-        TRY(make_mat(m, m->lm, c.vocab, H, seed, kLmHead, tmp));
+        TRY(make_fused(m, m->lm, {{c.vocab, kLmHead}}, H, seed, tmp));
         // step buffers
-        const size_t wide = std::max({(size_t)m->conv_dim, (size_t)I, (size_t)Hq * 512, (size_t)H,
-                                      (size_t)m->value_dim});
+        const size_t wide16 = std::max({(size_t)H, (size_t)m->value_dim, (size_t)Hq * 256});
         TRY(alloc_t(m, &m->h, (size_t)Bm * H));
         TRY(alloc_t(m, &m->mix, (size_t)Bm * H));
         TRY(alloc_t(m, &m->mlp, (size_t)Bm * H));
-        TRY(alloc_t(m, &m->big0, (size_t)Bm * wide));
-        TRY(alloc_t(m, &m->big1, (size_t)Bm * wide));
+        TRY(alloc_t(m, &m->qkv, (size_t)Bm * m->conv_dim));
+        TRY(alloc_t(m, &m->cv, (size_t)Bm * m->conv_dim));
         TRY(alloc_t(m, &m->zb, (size_t)Bm * m->value_dim));
         TRY(alloc_t(m, &m->ab, (size_t)Bm * Hv));
         TRY(alloc_t(m, &m->bb, (size_t)Bm * Hv));
@@ -421,6 +489,7 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         TRY(alloc_t(m, &m->betab, (size_t)Bm * Hv));
         TRY(alloc_t(m, &m->ob, (size_t)Bm * Hv * 128));
         TRY(alloc_t(m, &m->yb, (size_t)Bm * m->value_dim));
+        TRY(alloc_t(m, &m->qg, (size_t)Bm * Hq * 512));
         TRY(alloc_t(m, &m->kx, (size_t)Bm * Hkv * 256));
         TRY(alloc_t(m, &m->vx, (size_t)Bm * Hkv * 256));
         TRY(alloc_t(m, &m->logits, (size_t)Bm * c.vocab));
@@ -428,48 +497,55 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         TRY(alloc_t(m, &m->arg_part, (size_t)Bm * kArgBlocks));
         TRY(alloc_t(m, &m->arg_cnt, (size_t)Bm));
         TRY(hipMemset(m->arg_cnt, 0, (size_t)Bm * sizeof(uint32_t)));
-        TRY(alloc_t(m, &m->x16, (size_t)Bm * wide));
+        TRY(alloc_t(m, &m->x16, (size_t)Bm * wide16));
+        TRY(alloc_t(m, &m->act16, (size_t)Bm * I));
         TRY(alloc_t(m, &m->q16, (size_t)Bm * Hq * 256));
-        m->qkv = m->big0;
-        m->qg = m->big0;
-        // GEMM split-K workspace: the largest over the model's shapes
-        const int shapes[][2] = {{m->conv_dim, H}, {m->value_dim, H}, {Hv, H}, {H, m->value_dim},
-                                 {Hq * 512, H}, {Hkv * 256, H}, {H, Hq * 256}, {I, H}, {H, I},
-                                 {c.vocab, H}};
-        for (auto &s : shapes) m->gemm_ws_bytes = std::max(m->gemm_ws_bytes, w8_workspace_bytes(Bm, s[0], s[1]));
-        TRY(alloc(m, reinterpret_cast<void **>(&m->gemm_ws), m->gemm_ws_bytes));
-        m->attn_ws_bytes = attn_workspace_bytes(Bm, Hq, c.max_context);
-        TRY(alloc(m, reinterpret_cast<void **>(&m->attn_ws), m->attn_ws_bytes));
+        // GEMM split-K partials and counters: the largest over the model's matrices
+        size_t part = 0, groups = 0;
+        auto need = [&](const Mat &w) {
+            part = std::max(part, w8f_workspace_floats(Bm, w.N, w.K));
+            groups = std::max(groups, (size_t)w.N / 64);
+        };
+        for (const Layer &L : m->layers) {
+            need(L.in);
+            need(L.out);
+            need(L.gate_up);
+            need(L.down);
+        }
+        need(m->lm);
+        TRY(alloc_t(m, &m->gemm_part, part));
+        TRY(alloc_t(m, &m->gemm_cnt, groups));
+        TRY(hipMemset(m->gemm_cnt, 0, groups * sizeof(uint32_t)));
+        TRY(alloc(m, reinterpret_cast<void **>(&m->attn_ws), attn_workspace_bytes(Bm, Hq, c.max_context)));
         return hipDeviceSynchronize();
     };
     const hipError_t e = run();
-    (void)hipFree(tmp);
+    for (void *p : {(void *)tmp.f, (void *)tmp.q, (void *)tmp.q2, (void *)tmp.s})
+        if (p) (void)hipFree(p);
     return e;
 }
 
 hipError_t gdn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     const kai_gdn_hybrid_config &c = m->cfg;
-    const int B = m->batch, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads;
-    TRY(gemm(m, m->x16, L.qkv, m->qkv, st));
-    TRY(gemm(m, m->x16, L.z, m->zb, st));
-    TRY(gemm(m, m->x16, L.bp, m->bb, st));
-    TRY(gemm(m, m->x16, L.ap, m->ab, st));
-    TRY(launch_conv_update(m->qkv, L.conv_state, L.conv_w, m->big1, B, 1, m->conv_dim, true, st));
-    TRY(launch_gating_prologue(false, m->big1, m->ab, m->bb, L.A_log, L.dt_bias, m->qb, m->kb, m->vb, m->gb,
+    const int B = m->batch, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads, C = m->conv_dim, V = m->value_dim;
+    TRY(gemm(m, m->x16, L.in, segments({{m->qkv, C, C}, {m->zb, V, C + V}, {m->bb, Hv, C + V + Hv},
+                                        {m->ab, Hv, C + V + 2 * Hv}}), st));
+    TRY(launch_conv_update(m->qkv, L.conv_state, L.conv_w, m->cv, B, 1, C, true, st));
+    TRY(launch_gating_prologue(false, m->cv, m->ab, m->bb, L.A_log, L.dt_bias, m->qb, m->kb, m->vb, m->gb,
                                m->betab, B, Hk, Hv, st));
     TRY(launch_delta_decode(kF32, L.S, m->qb, m->kb, m->vb, m->gb, m->betab, m->ob, B, Hv, Hk, 128, 128,
                             1.0f / sqrtf(128.0f), st));
     TRY(launch_gated_rmsnorm(false, m->ob, m->zb, L.norm_w, m->yb, (size_t)B * Hv, c.rms_eps, st));
-    TRY(launch_convert(m->yb, kF32, m->x16, kF16, (size_t)B * m->value_dim, st));
-    return gemm(m, m->x16, L.out, m->mix, st);
+    TRY(launch_convert(m->yb, kF32, m->x16, kF16, (size_t)B * V, st));
+    return gemm_to(m, m->x16, L.out, m->mix, c.hidden, st);
 }
 
 hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     const kai_gdn_hybrid_config &c = m->cfg;
     const int B = m->batch, Hq = c.attn_q_heads, Hkv = c.attn_kv_heads;
-    TRY(gemm(m, m->x16, L.qp, m->qg, st));
-    TRY(gemm(m, m->x16, L.kp, m->kx, st));
-    TRY(gemm(m, m->x16, L.vp, m->vx, st));
+    const int nq = Hq * 512, nkv = Hkv * 256;
+    TRY(gemm(m, m->x16, L.in, segments({{m->qg, nq, nq}, {m->kx, nkv, nq + nkv}, {m->vx, nkv, nq + 2 * nkv}}),
+             st));
     attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, B), 256, 0, st>>>(m->qg, m->kx, m->vx, L.q_norm, L.k_norm, m->q16,
                                                                  L.Kc, L.Vc, Hq, Hkv, c.max_context, m->pos,
                                                                  c.rope_theta, c.rms_eps);
@@ -477,7 +553,7 @@ hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     // o * sigmoid(gate) -> fp16 in the span combine; gate = dims 256..511 of each qg head
     TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, nullptr, B, Hq, Hkv, c.max_context, m->pos + 1, 1.0f / 16.0f,
                            m->attn_ws, st, m->qg + 256, 512, m->x16));
-    return gemm(m, m->x16, L.op, m->mix, st);
+    return gemm_to(m, m->x16, L.out, m->mix, c.hidden, st);
 }
 
 hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits, hipStream_t st) {
@@ -486,24 +562,23 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
     embed_kernel<<<B, 256, 0, st>>>(tokens, m->embed, m->h, H, c.vocab);
     TRY(hipGetLastError());
     const float *pending = nullptr;
+    W8Out swiglu{};
+    swiglu.mode = kW8SwiGLU;
+    swiglu.x16 = m->act16;
     for (Layer &L : m->layers) {
         addnorm_kernel<<<B, 256, 0, st>>>(m->h, pending, L.ln_in, m->x16, H, c.rms_eps);
         TRY(hipGetLastError());
         TRY(L.attn ? attn_mixer(m, L, st) : gdn_mixer(m, L, st));
         addnorm_kernel<<<B, 256, 0, st>>>(m->h, m->mix, L.ln_post, m->x16, H, c.rms_eps);
         TRY(hipGetLastError());
-        TRY(gemm(m, m->x16, L.gate, m->big0, st));
-        TRY(gemm(m, m->x16, L.up, m->big1, st));
-        const size_t n = (size_t)B * c.inter;
-        swiglu_kernel<<<fill_blocks(n), 256, 0, st>>>(m->big0, m->big1, m->x16, n);
-        TRY(hipGetLastError());
-        TRY(gemm(m, m->x16, L.down, m->mlp, st));
+        TRY(gemm(m, m->x16, L.gate_up, swiglu, st));
+        TRY(gemm_to(m, m->act16, L.down, m->mlp, H, st));
         pending = m->mlp;
     }
     addnorm_kernel<<<B, 256, 0, st>>>(m->h, pending, m->final_norm, m->x16, H, c.rms_eps);
     TRY(hipGetLastError());
     float *lg = logits ? logits : m->logits;
-    TRY(gemm(m, m->x16, m->lm, lg, st));
+    TRY(gemm(m, m->x16, m->lm, segments({{lg, c.vocab, c.vocab}}), st));
     argmax_kernel<<<dim3(kArgBlocks, B), 256, 0, st>>>(lg, next ? next : m->next, c.vocab, m->arg_part,
                                                        m->arg_cnt);
     TRY(hipGetLastError());

@@ -109,6 +109,40 @@ int w8_splits(int N, int K);
 size_t w8_workspace_bytes(int M, int N, int K);
 hipError_t launch_w8_gemm(const uint16_t *x, const int8_t *W, const float *scale, float *y, int M,
                           int N, int K, float *workspace, hipStream_t st);
+// The model's fused int8 GEMM (rows of several matrices that share the input
+// concatenated), weights pre-tiled by launch_w8f_tile from row-major [N][K]:
+// N % 64 == 0, M <= 16, K a multiple of splits * waves * depth * 64.  Output
+// by `out`: kW8Segments writes channel ranges [seg[q-1].n_end, seg[q].n_end)
+// (16-multiples) to seg[q].dst with row stride seg[q].ld (channels past the
+// last segment are padding and not stored); kW8SwiGLU reads the rows as
+// gate/up interleaved in groups of 8 and writes x16 [M][N / 2] fp16.  With
+// splits > 1, `part` holds w8f_workspace_floats(M, N, K) floats and `cnt`
+// N / 64 counters that are zero before the first launch (each launch leaves
+// them zero); launches sharing them must not overlap.
+enum W8Mode : int { kW8Segments = 0, kW8SwiGLU = 1 };
+constexpr int kW8MaxSegs = 4;
+struct W8Seg {
+    float *dst;
+    int ld;
+    int n_end;
+};
+struct W8Out {
+    W8Seg seg[kW8MaxSegs];
+    int nseg;
+    int mode;
+    uint16_t *x16;
+};
+// Launch shape: waves per block (4 or 8), 64-k steps in flight per wave (1,
+// 2 or 4), k-splits across blocks (0: chosen by w8f_shape).
+struct W8fShape {
+    int waves, depth, splits;
+};
+W8fShape w8f_shape(int N, int K);
+size_t w8f_workspace_floats(int M, int N, int K);
+hipError_t launch_w8f_tile(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st);
+hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, int M, int N, int K,
+                      const W8Out &out, float *part, uint32_t *cnt, hipStream_t st,
+                      W8fShape shape = W8fShape{0, 0, 0});
 // Per-output-channel symmetric int8 quantisation of W[N][K] fp32.
 hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K, hipStream_t st);
 // Attention decode over an fp16 KV cache (head_dim 256, Hq / Hkv <= 4):

@@ -179,6 +179,227 @@ hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, i
 
 
 // ---------------------------------------------------------------------------
+// The model's int8 GEMM: the matmuls of one layer that read the same input
+// are one weight matrix (their rows concatenated), one launch.
+//
+// Weights are pre-tiled (w8f_tile_kernel) so that every wave load is one
+// contiguous 1 KB: for channel group c (64 channels, four 16-channel MFMA
+// tiles) and 64-k step s, the 4 KB at ((c * K / 64) + s) * 4096 hold tile
+// j's 1 KB at j * 1024, lane (g, r)'s 16 bytes at (16 g + r) * 16 = row
+// 64 c + 16 j + r, k = 64 s + 16 g .. +15.
+//
+// Block (group c = blockIdx.x, split s = blockIdx.y) takes k in [s kblk,
+// (s + 1) kblk); its WAVES waves split that range, each streaming its steps
+// with DEPTH steps of loads in flight; one activation load feeds the four
+// tiles.  The waves reduce through LDS, wave j finishing tile j.  With S > 1
+// splits, each block stores its partial (agent-scope, written through) and
+// the last of the group's S blocks to arrive (counter cnt[c], returned to
+// 0) sums the S partials in split order -- the result does not depend on
+// which block is last -- and runs the epilogue:
+//   kW8Segments: y = acc * scale into up to four output arrays, channel
+//                ranges of 16-multiples, each with its own row stride;
+//   kW8SwiGLU:   the rows are gate/up interleaved in groups of 8 (tile rows
+//                0..7 gate channels 8t..8t+7, rows 8..15 the up channels),
+//                out16[m][c] = fp16(silu(gate) * up) (Qwen3_5MLP,
+//                modeling_qwen3_5.py:704-717).
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kW8fGroup = 64;  // channels per block
+constexpr int kBufFlags = 0x00020000;  // buffer descriptor word 3 (raw dword access)
+constexpr int kSc1 = 16;               // cache policy: agent-coherent (sc1)
+
+// row-major Wq [N][K] -> the tiled layout above; one thread per 16 bytes
+__global__ __launch_bounds__(256) void w8f_tile_kernel(const int8_t *__restrict__ src, int8_t *__restrict__ dst,
+                                                       int K, size_t chunks) {
+    const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= chunks) return;
+    const int lane = (int)(q & 63), j = (int)((q >> 6) & 3);
+    const size_t cs = q >> 8;  // c * (K / 64) + s
+    const int steps = K / 64;
+    const size_t c = cs / steps, s = cs % steps;
+    const size_t n = 64 * c + 16 * j + (lane & 15);
+    const size_t k = 64 * s + 16 * (lane >> 4);
+    *reinterpret_cast<uint4 *>(dst + q * 16) = *reinterpret_cast<const uint4 *>(src + n * K + k);
+}
+
+template <int WAVES, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restrict__ x,
+                                                         const int8_t *__restrict__ W,
+                                                         const float *__restrict__ scale, int M, int N, int K,
+                                                         int kblk, int S, float *__restrict__ part,
+                                                         uint32_t *__restrict__ cnt, W8Out out) {
+    __shared__ f32x4_t red[WAVES][4][64];
+    __shared__ bool last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int c = blockIdx.x;
+    const int n0 = kW8fGroup * c;
+    const int kq = kblk / WAVES;      // this wave's k-range
+    const int nsteps = kq / kKStep;   // a multiple of DEPTH
+    const int kb = blockIdx.y * kblk + wave * kq;
+    const int8_t *wp = W + ((size_t)c * (K / kKStep) + kb / kKStep) * 4096 + lane * 16;
+    const bool row_ok = r < M;
+    // rows past M read row 0 (in bounds, one cache line per wave) and are zeroed
+    const uint16_t *xp = x + (size_t)(row_ok ? r : 0) * K + kb + 16 * g;
+    f32x4_t acc[4] = {zero4(), zero4(), zero4(), zero4()};
+    u32x4_t buf[DEPTH][4];
+    auto load_w = [&](u32x4_t (&w)[4], int st) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(wp + (size_t)st * 4096 + j * 1024));
+    };
+    auto mult = [&](const u32x4_t (&w)[4], int st) {
+        u32x4_t xa = *reinterpret_cast<const u32x4_t *>(xp + st * kKStep);
+        u32x4_t xb = *reinterpret_cast<const u32x4_t *>(xp + st * kKStep + 8);
+        if (!row_ok) xa = xb = u32x4_t{0u, 0u, 0u, 0u};
+        const f16x8_t fa = __builtin_bit_cast(f16x8_t, xa), fb = __builtin_bit_cast(f16x8_t, xb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f16x8_t w0, w1;
+            i8x16_to_f16(w[j], w0, w1);
+            acc[j] = mfma_f16(w0, fa, acc[j]);
+            acc[j] = mfma_f16(w1, fb, acc[j]);
+        }
+    };
+    // DEPTH steps in flight: step st + DEPTH is requested as step st is used
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) load_w(buf[i], i);
+    int base = 0;
+    for (; base + DEPTH < nsteps; base += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            mult(buf[i], base + i);
+            load_w(buf[i], base + DEPTH + i);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) mult(buf[i], base + i);
+    // reduce over the waves; wave j (< 4) ends with tile j of the block
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wave][j][lane] = acc[j];
+    __syncthreads();
+    if (wave >= 4) return;
+    const int j = wave;
+    f32x4_t t = red[0][j][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) t += red[w][j][lane];
+    const int n = n0 + 16 * j + 4 * g;  // C lane (g, r): channels n .. n+3 of batch row r
+    if (S > 1) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, 0, 0x7FFFFFFF, kBufFlags);
+        const int row_stride = N * 4;
+        if (row_ok)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, t), rs,
+                                                   ((blockIdx.y * M + r) * row_stride) + n * 4, 0, kSc1);
+        stores_done();
+        __syncthreads();
+        if (threadIdx.x == 0) last = arrive_last(&cnt[c], (uint32_t)S);
+        __syncthreads();
+        if (!last) return;
+        t = zero4();
+        if (row_ok) {
+            // every split's partial requested before any is summed
+            constexpr int kBatch = 8;
+            for (int s0 = 0; s0 < S; s0 += kBatch) {
+                u32x4_t v[kBatch];
+#pragma unroll
+                for (int q = 0; q < kBatch; ++q)
+                    if (s0 + q < S)
+                        v[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (((s0 + q) * M + r) * row_stride) + n * 4, 0,
+                                                                     kSc1);
+#pragma unroll
+                for (int q = 0; q < kBatch; ++q)
+                    if (s0 + q < S) t += __builtin_bit_cast(f32x4_t, v[q]);
+            }
+        }
+    }
+    // epilogue (wave j, tile j)
+    const f32x4_t y = t * *reinterpret_cast<const f32x4_t *>(scale + n);
+    if (out.mode == kW8SwiGLU) {
+        f32x4_t up;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) up[e] = __shfl_xor(y[e], 32);
+        if (g < 2 && row_ok) {
+            uint32_t h[2];
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const float a = y[e] / (1.0f + expf(-y[e])) * up[e];
+                const float b = y[e + 1] / (1.0f + expf(-y[e + 1])) * up[e + 1];
+                h[e / 2] = (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+            }
+            const int cc = (n0 + 16 * j) / 2 + 4 * g;
+            *reinterpret_cast<uint2 *>(out.x16 + (size_t)r * (N / 2) + cc) = make_uint2(h[0], h[1]);
+        }
+    } else if (row_ok && n < out.seg[out.nseg - 1].n_end) {  // channels past the last segment: padding
+        int sgi = 0, nb = 0;
+#pragma unroll
+        for (int q = 0; q < kW8MaxSegs - 1; ++q)
+            if (q < out.nseg - 1 && n >= out.seg[q].n_end) {
+                sgi = q + 1;
+                nb = out.seg[q].n_end;
+            }
+        float *dst = out.seg[0].dst;
+        int ld = out.seg[0].ld;
+#pragma unroll
+        for (int q = 1; q < kW8MaxSegs; ++q)
+            if (q == sgi) {
+                dst = out.seg[q].dst;
+                ld = out.seg[q].ld;
+            }
+        *reinterpret_cast<f32x4_t *>(dst + (size_t)r * ld + (n - nb)) = y;
+    }
+}
+
+}  // namespace
+
+// Launch shape from a sweep over the Qwen3.5-4B matrices at M = 1 and 16:
+// eight waves, one step in flight per wave, and k-splits only for narrow
+// matrices, the fewest that give 160 blocks (the cross-block hand-off costs
+// more than the extra parallelism beyond that).
+W8fShape w8f_shape(int N, int K) {
+    const int groups = N / kW8fGroup;
+    W8fShape sh{K % 512 == 0 ? 8 : 4, 1, 1};
+    for (int S = 2; S <= 32 && groups * sh.splits < 160; ++S)
+        if (K % (S * sh.waves * kKStep) == 0) sh.splits = S;
+    return sh;
+}
+
+size_t w8f_workspace_floats(int M, int N, int K) {
+    const W8fShape sh = w8f_shape(N, K);
+    return sh.splits > 1 ? (size_t)sh.splits * M * N : 0;
+}
+
+hipError_t launch_w8f_tile(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st) {
+    if (N % kW8fGroup != 0 || K % kKStep != 0) return hipErrorInvalidValue;
+    const size_t chunks = (size_t)N * K / 16;
+    w8f_tile_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, st>>>(src, dst, K, chunks);
+    return hipGetLastError();
+}
+
+hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, int M, int N, int K,
+                      const W8Out &out, float *part, uint32_t *cnt, hipStream_t st, W8fShape sh) {
+    if (M == 0 || N == 0) return hipSuccess;
+    if (sh.splits == 0) sh = w8f_shape(N, K);
+    const int S = sh.splits;
+    if (M > 16 || N % kW8fGroup != 0 || K % (S * sh.waves * sh.depth * kKStep) != 0) return hipErrorInvalidValue;
+    if (S > 1 && (!part || !cnt || (size_t)S * M * N * 4 > 0x7FFFFFFFull)) return hipErrorInvalidValue;
+    const dim3 grid(N / kW8fGroup, S);
+#define W8F_CASE(WV, DP)                                                                                  \
+    if (sh.waves == WV && sh.depth == DP) {                                                                \
+        w8f_kernel<WV, DP><<<grid, 64 * WV, 0, st>>>(x, W, scale, M, N, K, K / S, S, part, cnt, out);     \
+        return hipGetLastError();                                                                          \
+    }
+    W8F_CASE(4, 1)
+    W8F_CASE(4, 2)
+    W8F_CASE(4, 4)
+    W8F_CASE(8, 1)
+    W8F_CASE(8, 2)
+    W8F_CASE(8, 4)
+#undef W8F_CASE
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
 // Attention decode (HF Qwen3_5Attention with a KV cache, one new token per
 // sequence; eager_attention_forward, modeling_qwen3_5.py:606-627): for query
 // head h of sequence b, with kv = h / (Hq / Hkv) (repeat_kv),
