@@ -18,7 +18,9 @@ The JSON line also carries:
   secondary     prefill (config 3, T=16K), the fp16-state prefill at
                 T in {1K, 8K, 32K, 128K} (config 4: tokens/s and the per-layer
                 state footprint), conv+SiLU (config 1) and cumulative decay
-                ([4096][8192]) throughput and roofline
+                ([4096][8192]) throughput and roofline, the layer glue, and
+                the hybrid decode loop (config 5: B=1 and B=16, 256 greedy
+                steps after a 32K context)
 Synthetic inputs with the BASELINE distributions; random state.
 """
 from __future__ import annotations
@@ -301,6 +303,65 @@ def bench_layer_glue(L, ob, torch, timer, T=PF_T):
     return pro, rn
 
 
+HYB_CONTEXT, HYB_STEPS = 32768, 256
+
+
+def hybrid_step_bytes(cfg, weight_bytes, B, pos):
+    """HBM bytes one decode step of the hybrid model must move at position
+    pos: every int8 weight matrix with its scales once, the embedding rows,
+    the fp16 K and V caches up to pos + 1 (plus the appended row), and each
+    GDN layer's fp32 recurrent state (read + write) and conv state."""
+    attn = cfg.layers // cfg.attn_every
+    gdn = cfg.layers - attn
+    conv_dim = 2 * cfg.gdn_k_heads * 128 + cfg.gdn_v_heads * 128
+    kv = attn * B * cfg.attn_kv_heads * (pos + 1) * 256 * 2 * 2
+    state = gdn * B * (cfg.gdn_v_heads * 128 * 128 * 4 * 2 + conv_dim * 4 * 4 * 2)
+    return weight_bytes + B * cfg.hidden * 2 + kv + state
+
+
+def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_STEPS):
+    """the Qwen3.5-4B-shaped hybrid model (24 GDN + 8
+    attention layers, int8 per-output-channel weights, fp16 activations and
+    KV cache), greedy decoding of `steps` tokens per sequence after a
+    `context`-token context, batch 1 and 16.  The context is represented by
+    drawn states (KV caches, recurrent and conv states), not by running a
+    prefill; tokens never leave the device (each step's argmax feeds the
+    next).  Timed with HIP events around the whole loop."""
+    from orionsbelt_amd import hybrid as hb
+    rows = []
+    for B in batches:
+        cfg = hb.qwen35_4b(B, context + steps + 1)
+        m = hb.HybridModel(cfg, 12345)
+        m.reset(B, context, 7)
+        tok = torch.randint(0, cfg.vocab, (B,), dtype=torch.int32, device="cuda")
+        nxt = torch.empty_like(tok)
+        logits = torch.empty(B, cfg.vocab, dtype=torch.float32, device="cuda")
+        for _ in range(3):  # warm-up steps, then a fresh context
+            m.step(tok, nxt, logits)
+        m.reset(B, context, 7)
+        bufs = [tok, nxt]
+
+        def run():
+            for i in range(steps):
+                m.step(bufs[i & 1], bufs[(i + 1) & 1], logits)
+
+        ms = timer.time_ms(run, 1)
+        per = ms / steps
+        nbytes = sum(hybrid_step_bytes(cfg, m.weight_bytes, B, context + i) for i in range(steps)) / steps
+        gbs = nbytes / (per * 1e-3) / 1e9
+        rows.append({"batch": B, "context": context, "steps": steps, "ms_per_step": round(per, 4),
+                     "tokens_per_s": round(B / (per * 1e-3), 1), "bytes_per_step": int(nbytes),
+                     "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "device_bytes": m.device_bytes})
+        m.close()
+        del m, logits, tok, nxt, bufs
+        torch.cuda.empty_cache()
+    return {"workload": f"hybrid decode loop, Qwen3.5-4B shape (32 layers: 24 GDN + 8 attention, hidden 2560, "
+                        f"inter 9216, vocab 151936), int8 weights, fp16 activations and KV cache, greedy, "
+                        f"{steps} steps after a drawn {context}-token context (BASELINE configs[4])",
+            "runs": rows}
+
+
 def cpu_prefill_baseline(budget_s=10.0):
     from oracle import oracle as orc
     from tests.gdn_inputs import prefill_inputs
@@ -385,6 +446,8 @@ def run_profile(which, L, ob, torch, timer, steps, warmup):
     elif which == "layer":
         pro, rn = bench_layer_glue(L, ob, torch, timer)
         log(f"gating prologue: {pro}\ngated rmsnorm: {rn}")
+    elif which == "hybrid":
+        log(f"hybrid: {bench_hybrid(torch, timer, steps=steps)}")
     else:
         conv, decay = bench_stream(L, ob, torch, timer, reps=steps)
         log(f"{which}: {conv if which == 'conv' else decay}")
@@ -403,7 +466,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip prefill/conv/decay lines")
-    ap.add_argument("--profile", choices=["decode", "prefill", "prefill_f16", "layer", "conv", "cumdecay"],
+    ap.add_argument("--profile", choices=["decode", "prefill", "prefill_f16", "layer", "conv", "cumdecay",
+                                          "hybrid"],
                     help="run only this workload (and a 256 MiB device copy that calibrates "
                          "HBM byte counters) for rocprofv3; prints no JSON line")
     args = ap.parse_args()
@@ -444,6 +508,9 @@ def main():
         secondary["gating_prologue"], secondary["gated_rmsnorm"] = bench_layer_glue(L, ob, torch, timer)
         log(f"gating prologue: {secondary['gating_prologue']}\n"
             f"gated rmsnorm: {secondary['gated_rmsnorm']}")
+        log("hybrid decode loop, B=1 and B=16 after 32K ...")
+        secondary["hybrid_decode"] = bench_hybrid(torch, timer)
+        log(f"hybrid decode: {secondary['hybrid_decode']}")
 
     cpu = None
     if not args.no_cpu:
