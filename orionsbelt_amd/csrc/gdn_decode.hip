@@ -124,7 +124,145 @@ __global__ __launch_bounds__(256, MINW) void delta_decode_kernel(
     }
 }
 
+// One GDN layer's decode step after its in-projection, fused for the hybrid
+// loop: block (sequence b, value head h), 256 threads, fp32 state, d = 128.
+//   1. the conv update on HF's cache with SiLU (conv_update_kernel's
+//      arithmetic) for the block's 384 channels: q and k of key head
+//      kh = h / (Hv / Hk), v of head h.  The cache is read from conv_in and
+//      the shifted cache written to conv_out (a different array: the value
+//      heads that share a key head all read its q/k state); the first value
+//      head of a key head writes the q/k entries, every head its v entries;
+//   2. q, k L2-normalised (eps 1e-6), q scaled; g = -exp(A_log) *
+//      softplus(a + dt_bias), beta = sigmoid(b) (the gating prologue);
+//   3. the delta-rule step of delta_decode_kernel with one block owning all
+//      128 value columns;
+//   4. the gated RMSNorm of the output row with z (weight w [128]) and the
+//      fp16 rounding the out-projection reads: out16[b][h * 128 + c].
+// x holds the in-projection's qkv rows [B][(2 Hk + Hv) * 128].
+__global__ __launch_bounds__(256) void gdn_step_fused_kernel(
+    const float *__restrict__ x, const float *__restrict__ conv_in, float *__restrict__ conv_out,
+    const float *__restrict__ conv_w, const float *__restrict__ a_in, const float *__restrict__ b_in,
+    const float *__restrict__ A_log, const float *__restrict__ dt_bias, float *__restrict__ S,
+    const float *__restrict__ z, const float *__restrict__ norm_w, uint16_t *__restrict__ out16, int Hk, int Hv,
+    float q_scale, float eps) {
+#pragma clang fp contract(off)
+    constexpr int D = 128, TPR = 32, RG = 8, RPT = 16;
+    __shared__ float qs[D], ks[D], vs[D];
+    __shared__ float red_ss[4];
+    __shared__ float gate[2];
+    __shared__ float4 red[RG][TPR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int bh = blockIdx.x;
+    const int b = bh / Hv, h = bh % Hv;
+    const int rep = Hv / Hk, kh = h / rep;
+    const int64_t C = (int64_t)(2 * Hk + Hv) * D;
+    const int cgi = tid % TPR, rg = tid / TPR;
+    const int c = cgi * 4;
+    const int64_t sbase = (int64_t)bh * D * D;
+    // the state is independent of the prologue: request it first
+    float4 s[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) s[i] = load_f4<true>(S + sbase + (int64_t)(rg + RG * i) * D + c);
+
+    // 1. conv + SiLU: thread t < 128 takes q channel t and v channel t,
+    //    thread t >= 128 k channel t - 128
+    auto conv = [&](int64_t ch, bool write) {
+        const int64_t si = ((int64_t)b * C + ch) * 4;
+        const float4 st = *reinterpret_cast<const float4 *>(conv_in + si);
+        const float4 wv = *reinterpret_cast<const float4 *>(conv_w + ch * 4);
+        const float cur = x[(int64_t)b * C + ch];
+        float acc = st.y * wv.x + st.z * wv.y + st.w * wv.z + cur * wv.w;
+        acc = acc / (1.0f + expf(-acc));
+        if (write) *reinterpret_cast<float4 *>(conv_out + si) = make_float4(st.y, st.z, st.w, cur);
+        return acc;
+    };
+    const bool qk_writer = h % rep == 0;
+    float mine;
+    if (tid < D) {
+        mine = conv((int64_t)kh * D + tid, qk_writer);
+        vs[tid] = conv((int64_t)2 * Hk * D + (int64_t)h * D + tid, true);
+    } else {
+        mine = conv((int64_t)Hk * D + (int64_t)kh * D + (tid - D), qk_writer);
+    }
+    // 2. L2 norms (q: waves 0-1, k: waves 2-3) and the gates
+    float ss = mine * mine;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) red_ss[wave] = ss;
+    if (tid == 0) {
+        const float y = a_in[bh] + dt_bias[h];
+        const float sp = y > 20.f ? y : log1pf(expf(y));
+        gate[0] = -expf(A_log[h]) * sp;
+        gate[1] = 1.0f / (1.0f + expf(-b_in[bh]));
+    }
+    __syncthreads();
+    if (tid < D) qs[tid] = mine * (1.0f / sqrtf(red_ss[0] + red_ss[1] + 1e-6f)) * q_scale;
+    else ks[tid - D] = mine * (1.0f / sqrtf(red_ss[2] + red_ss[3] + 1e-6f));
+    __syncthreads();
+
+    // 3. the delta-rule step (delta_decode_kernel, one block per head)
+    float kj[RPT], qj[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        kj[i] = ks[rg + RG * i];
+        qj[i] = qs[rg + RG * i];
+    }
+    const float decay = expf(gate[0]);
+    const float bt = gate[1];
+    const float4 vv = *reinterpret_cast<const float4 *>(vs + c);
+    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        s[i] = make_float4(s[i].x * decay, s[i].y * decay, s[i].z * decay, s[i].w * decay);
+        kv = f4_fma(kj[i], s[i], kv);
+    }
+    red[rg][cgi] = kv;
+    __syncthreads();
+    kv = red[0][cgi];
+#pragma unroll
+    for (int r = 1; r < RG; ++r) kv = f4_add(kv, red[r][cgi]);
+    const float4 delta = make_float4((vv.x - kv.x) * bt, (vv.y - kv.y) * bt, (vv.z - kv.z) * bt, (vv.w - kv.w) * bt);
+    float4 op = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        s[i] = f4_fma(kj[i], delta, s[i]);
+        store_f4<true>(S + sbase + (int64_t)(rg + RG * i) * D + c, s[i]);
+        op = f4_fma(qj[i], s[i], op);
+    }
+    __syncthreads();
+    red[rg][cgi] = op;
+    __syncthreads();
+    if (rg != 0) return;
+    // 4. gated RMSNorm over the row (threads 0..31 of wave 0, 4 columns each)
+    float4 o4 = red[0][cgi];
+#pragma unroll
+    for (int r = 1; r < RG; ++r) o4 = f4_add(o4, red[r][cgi]);
+    float q2 = o4.x * o4.x + o4.y * o4.y + o4.z * o4.z + o4.w * o4.w;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) q2 += __shfl_xor(q2, o, 32);
+    const float inv = 1.0f / sqrtf(q2 / (float)D + eps);
+    const float4 zz = *reinterpret_cast<const float4 *>(z + (int64_t)bh * D + c);
+    const float4 ww = *reinterpret_cast<const float4 *>(norm_w + c);
+    auto gn = [&](float ov, float zv, float wv) { return (wv * (ov * inv)) * (zv / (1.0f + expf(-zv))); };
+    uint2 o;
+    o.x = (uint32_t)f32_to_f16_rne(gn(o4.x, zz.x, ww.x)) | ((uint32_t)f32_to_f16_rne(gn(o4.y, zz.y, ww.y)) << 16);
+    o.y = (uint32_t)f32_to_f16_rne(gn(o4.z, zz.z, ww.z)) | ((uint32_t)f32_to_f16_rne(gn(o4.w, zz.w, ww.w)) << 16);
+    *reinterpret_cast<uint2 *>(out16 + (int64_t)bh * D + c) = o;
+}
+
 }  // namespace
+
+hipError_t launch_gdn_step_fused(const float *x, const float *conv_in, float *conv_out, const float *conv_w,
+                                 const float *a, const float *b, const float *A_log, const float *dt_bias, float *S,
+                                 const float *z, const float *norm_w, uint16_t *out16, int B, int Hk, int Hv,
+                                 float q_scale, float eps, hipStream_t st) {
+    if (B <= 0) return hipSuccess;
+    if (Hk <= 0 || Hv % Hk != 0 || conv_in == conv_out) return hipErrorInvalidValue;
+    gdn_step_fused_kernel<<<dim3((unsigned)(B * Hv)), 256, 0, st>>>(x, conv_in, conv_out, conv_w, a, b, A_log,
+                                                                    dt_bias, S, z, norm_w, out16, Hk, Hv, q_scale,
+                                                                    eps);
+    return hipGetLastError();
+}
 
 // Production configuration of the decode kernel, measured on MI355X over 24
 // rotating 128 MiB states (B=64, 32 heads, 128x128): 2 column splits with

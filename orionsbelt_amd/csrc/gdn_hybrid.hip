@@ -267,7 +267,8 @@ struct Layer {
     float *conv_w = nullptr, *dt_bias = nullptr, *A_log = nullptr, *norm_w = nullptr;
     float *q_norm = nullptr, *k_norm = nullptr;
     Mat gate_up, down;
-    float *S = nullptr, *conv_state = nullptr;  // [B][Hv][128][128], [B][conv_dim][4]
+    float *S = nullptr;                          // [B][Hv][128][128]
+    float *conv_state[2] = {nullptr, nullptr};   // [B][conv_dim][4], the current one is conv_state[parity]
     uint16_t *Kc = nullptr, *Vc = nullptr;      // [B][Hkv][Tmax][256]
 };
 
@@ -300,8 +301,7 @@ struct kai_gdn_hybrid {
     gdn::Mat lm;
     // step buffers
     float *h = nullptr, *mix = nullptr, *mlp = nullptr;
-    float *qkv = nullptr, *cv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr, *qb = nullptr,
-          *kb = nullptr, *vb = nullptr, *gb = nullptr, *betab = nullptr, *ob = nullptr, *yb = nullptr;
+    float *qkv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr;
     float *qg = nullptr, *kx = nullptr, *vx = nullptr, *logits = nullptr;
     int32_t *next = nullptr;
     uint64_t *arg_part = nullptr;  // [max_batch][kArgBlocks]
@@ -312,6 +312,7 @@ struct kai_gdn_hybrid {
     std::vector<void *> allocs;
     size_t bytes = 0, weight_bytes = 0;
     int batch = 0, pos = 0;
+    int parity = 0;  // which conv cache of each GDN layer is current
 };
 
 namespace gdn {
@@ -453,7 +454,8 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
                 TRY(make_vec(m, &L.A_log, Hv, seed, base + kALog, 1.3862944f, 1.3862944f));  // U(0, ln 16)
                 TRY(make_vec(m, &L.norm_w, 128, seed, base + kNormW, 0.1f, 1.0f));
                 TRY(alloc_t(m, &L.S, (size_t)Bm * Hv * 128 * 128));
-                TRY(alloc_t(m, &L.conv_state, (size_t)Bm * m->conv_dim * 4));
+                TRY(alloc_t(m, &L.conv_state[0], (size_t)Bm * m->conv_dim * 4));
+                TRY(alloc_t(m, &L.conv_state[1], (size_t)Bm * m->conv_dim * 4));
             } else {
                 TRY(make_fused(m, L.in, {{Hq * 512, base + kQp}, {Hkv * 256, base + kKp}, {Hkv * 256, base + kVp}},
                                H, seed, tmp));
@@ -478,17 +480,9 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         TRY(alloc_t(m, &m->mix, (size_t)Bm * H));
         TRY(alloc_t(m, &m->mlp, (size_t)Bm * H));
         TRY(alloc_t(m, &m->qkv, (size_t)Bm * m->conv_dim));
-        TRY(alloc_t(m, &m->cv, (size_t)Bm * m->conv_dim));
         TRY(alloc_t(m, &m->zb, (size_t)Bm * m->value_dim));
         TRY(alloc_t(m, &m->ab, (size_t)Bm * Hv));
         TRY(alloc_t(m, &m->bb, (size_t)Bm * Hv));
-        TRY(alloc_t(m, &m->qb, (size_t)Bm * Hk * 128));
-        TRY(alloc_t(m, &m->kb, (size_t)Bm * Hk * 128));
-        TRY(alloc_t(m, &m->vb, (size_t)Bm * Hv * 128));
-        TRY(alloc_t(m, &m->gb, (size_t)Bm * Hv));
-        TRY(alloc_t(m, &m->betab, (size_t)Bm * Hv));
-        TRY(alloc_t(m, &m->ob, (size_t)Bm * Hv * 128));
-        TRY(alloc_t(m, &m->yb, (size_t)Bm * m->value_dim));
         TRY(alloc_t(m, &m->qg, (size_t)Bm * Hq * 512));
         TRY(alloc_t(m, &m->kx, (size_t)Bm * Hkv * 256));
         TRY(alloc_t(m, &m->vx, (size_t)Bm * Hkv * 256));
@@ -530,13 +524,10 @@ hipError_t gdn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     const int B = m->batch, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads, C = m->conv_dim, V = m->value_dim;
     TRY(gemm(m, m->x16, L.in, segments({{m->qkv, C, C}, {m->zb, V, C + V}, {m->bb, Hv, C + V + Hv},
                                         {m->ab, Hv, C + V + 2 * Hv}}), st));
-    TRY(launch_conv_update(m->qkv, L.conv_state, L.conv_w, m->cv, B, 1, C, true, st));
-    TRY(launch_gating_prologue(false, m->cv, m->ab, m->bb, L.A_log, L.dt_bias, m->qb, m->kb, m->vb, m->gb,
-                               m->betab, B, Hk, Hv, st));
-    TRY(launch_delta_decode(kF32, L.S, m->qb, m->kb, m->vb, m->gb, m->betab, m->ob, B, Hv, Hk, 128, 128,
-                            1.0f / sqrtf(128.0f), st));
-    TRY(launch_gated_rmsnorm(false, m->ob, m->zb, L.norm_w, m->yb, (size_t)B * Hv, c.rms_eps, st));
-    TRY(launch_convert(m->yb, kF32, m->x16, kF16, (size_t)B * V, st));
+    // conv update, gating prologue, delta rule, gated RMSNorm -> fp16: one kernel
+    TRY(launch_gdn_step_fused(m->qkv, L.conv_state[m->parity], L.conv_state[m->parity ^ 1], L.conv_w, m->ab,
+                              m->bb, L.A_log, L.dt_bias, L.S, m->zb, L.norm_w, m->x16, B, Hk, Hv,
+                              1.0f / sqrtf(128.0f), c.rms_eps, st));
     return gemm_to(m, m->x16, L.out, m->mix, c.hidden, st);
 }
 
@@ -583,6 +574,7 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
                                                        m->arg_cnt);
     TRY(hipGetLastError());
     ++m->pos;
+    m->parity ^= 1;
     return hipSuccess;
 }
 
@@ -590,6 +582,7 @@ hipError_t reset(kai_gdn_hybrid *m, int batch, int context, uint64_t seed) {
     const kai_gdn_hybrid_config &c = m->cfg;
     m->batch = batch;
     m->pos = context;
+    m->parity = 0;
     for (size_t l = 0; l < m->layers.size(); ++l) {
         Layer &L = m->layers[l];
         const uint64_t base = (1ull << 20) + 16ull * l;
@@ -597,10 +590,10 @@ hipError_t reset(kai_gdn_hybrid *m, int batch, int context, uint64_t seed) {
             const size_t ns = (size_t)batch * c.gdn_v_heads * 128 * 128, nc = (size_t)batch * m->conv_dim * 4;
             if (context > 0) {
                 TRY(fill(L.S, ns, seed, base + kStS, 0.034641016f, 0.f));
-                TRY(fill(L.conv_state, nc, seed, base + kStConv, 1.0f, 0.f));
+                TRY(fill(L.conv_state[0], nc, seed, base + kStConv, 1.0f, 0.f));
             } else {
                 TRY(hipMemset(L.S, 0, ns * 4));
-                TRY(hipMemset(L.conv_state, 0, nc * 4));
+                TRY(hipMemset(L.conv_state[0], 0, nc * 4));
             }
         } else {
             const size_t rows = (size_t)batch * c.attn_kv_heads;

@@ -61,6 +61,17 @@ hipError_t launch_delta_decode(int narrow_state, void *S, const float *q, const 
                                int B, int Hv, int Hk, int dk, int dv, float q_scale,
                                hipStream_t st);
 
+// One GDN layer's decode step after the in-projection, fused (d = 128, fp32
+// state): conv update + SiLU on HF's cache, q/k L2 norm, gates, the delta
+// rule, and the gated RMSNorm rounded to fp16 into out16 [B][Hv * 128].
+// x [B][(2 Hk + Hv) * 128] (the in-projection's qkv rows); the conv cache
+// [B][(2 Hk + Hv) * 128][4] is read from conv_in and written shifted to
+// conv_out (distinct arrays); a, b [B][Hv], S [B][Hv][128][128], z [B][Hv][128].
+hipError_t launch_gdn_step_fused(const float *x, const float *conv_in, float *conv_out, const float *conv_w,
+                                 const float *a, const float *b, const float *A_log, const float *dt_bias, float *S,
+                                 const float *z, const float *norm_w, uint16_t *out16, int B, int Hk, int Hv,
+                                 float q_scale, float eps, hipStream_t st);
+
 // ---- chunked prefill (gdn_prefill.hip) --------------------------------------
 
 constexpr int kChunk = 64;

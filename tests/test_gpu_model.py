@@ -106,8 +106,10 @@ def gpu_attn(L, q16, k16, v16, length, scaling):
 
 @pytest.mark.parametrize("B,Hq,Hkv,Tmax,length", [(1, 4, 1, 64, 1), (2, 16, 4, 300, 300),
                                                    (3, 8, 4, 1000, 777), (1, 16, 4, 4096, 4096),
-                                                   (16, 16, 4, 640, 513)])
+                                                   (16, 16, 4, 640, 513), (16, 16, 4, 4200, 4100)])
 def test_attn_decode_vs_oracle(L, B, Hq, Hkv, Tmax, length):
+    """Up to 16 sequences, GQA groups of 1 to 4 query heads, lengths that end
+    inside a 16-position group and inside a 256-position span."""
     rs = np.random.RandomState(length + B)
     D = 256
     q = (rs.randn(B, Hq, D) * 0.5).astype(np.float16)
