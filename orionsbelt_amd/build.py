@@ -6,6 +6,8 @@ Outputs:
     orionsbelt_amd/lib/libkai_gdn_hip.so    the C-ABI library
     orionsbelt_amd/bin/test_kai_gdn         kai test harness (C), links the library
     orionsbelt_amd/bin/bench_kai_gdn        kai bench harness (C), links the library
+    orionsbelt_amd/bin/gdn_e2e_decode       hybrid decode benchmark (C), the reference e2e
+                                            program's interface
 
 Every HIP translation unit is compiled with
 `-Xclang -target-feature -Xclang -packed-fp32-ops` (no packed fp32 ops are
@@ -79,7 +81,7 @@ def build_harness() -> None:
               "-D__HIP_PLATFORM_AMD__"]
     link = [f"-L{LIBDIR}", "-lkai_gdn_hip", "-Wl,-rpath,$ORIGIN/../lib",
             f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-lm"]
-    for name in ("test_kai_gdn", "bench_kai_gdn"):
+    for name in ("test_kai_gdn", "bench_kai_gdn", "gdn_e2e_decode"):
         _run([CC, *common, os.path.join(PKG, "harness", f"{name}.c"),
               "-o", os.path.join(BINDIR, name), *link])
 

@@ -66,8 +66,20 @@ def test_kai_prototypes_identical_to_reference(hdr, name):
 
 
 def test_c_harnesses_built():
-    for b in ("test_kai_gdn", "bench_kai_gdn"):
+    for b in ("test_kai_gdn", "bench_kai_gdn", "gdn_e2e_decode"):
         assert os.access(os.path.join(REPO, "orionsbelt_amd", "bin", b), os.X_OK), b
+
+
+def test_e2e_driver_cli():
+    """The hybrid decode driver keeps the reference program's flags: --help
+    runs without a GPU, bad token counts are rejected before any HIP call."""
+    exe = os.path.join(REPO, "orionsbelt_amd", "bin", "gdn_e2e_decode")
+    r = subprocess.run([exe, "--help"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0
+    for flag in ("--tokens", "--csv", "--ctx-sweep", "--batch", "--ctx"):
+        assert flag in r.stdout
+    r = subprocess.run([exe, "--tokens", "0"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "--tokens must be >= 1" in r.stderr
 
 
 def test_bench_refuses_multi_gpu():

@@ -178,3 +178,26 @@ def test_hybrid_qwen35_4b_shape(hb):
         assert np.array_equal(l1, l2) and np.array_equal(n1, n2)
     assert gm.position == 4003
     gm.close()
+
+
+def test_e2e_driver_runs(hb):
+    """The C driver (orionsbelt_amd/bin/gdn_e2e_decode, the reference e2e
+    program's interface) decodes at the 4B shape and prints the reference's
+    CSV rows: the decode report and a context sweep."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "orionsbelt_amd", "bin",
+                       "gdn_e2e_decode")
+    r = subprocess.run([exe, "--tokens", "4", "--csv", "--batch", "2", "--ctx", "300"], capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stderr
+    head, row = r.stdout.strip().splitlines()[-2:]
+    assert head.startswith("model,tokens,ttft_ms,tok_per_sec_mean,p50_us")
+    f = row.split(",")
+    assert f[0] == "Qwen3.5-4B" and f[1] == "4" and float(f[3]) > 0 and float(f[7]) > 0
+    r = subprocess.run([exe, "--csv", "--ctx-sweep", "1,300"], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr
+    lines = r.stdout.strip().splitlines()
+    assert lines[0].startswith("model,ctx_len,gdn_layer_us,full_attn_us,ffn_us,total_us")
+    assert [ln.split(",")[1] for ln in lines[1:]] == ["1", "300"]
+    assert all(float(ln.split(",")[5]) > 0 for ln in lines[1:])
