@@ -58,13 +58,21 @@ __global__ __launch_bounds__(256) void fill_f16_kernel(uint16_t *dst, size_t n, 
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
         dst[i] = f32_to_f16_rne(hash_value(seed, stream, i, amp, center));
 }
-// K/V cache rows [rows][Tmax][256], positions < len drawn, the rest zero.
-__global__ __launch_bounds__(256) void fill_cache_kernel(uint16_t *dst, size_t rows, int Tmax, int len,
+// K/V cache rows [rows][Tmax][256] (storage Tmax >= the logical length
+// Tlog), positions < len drawn, the rest zero.  The value of (row, t, d) is
+// the hash of its row-major index with Tlog positions per row (the CPU
+// model's layout); with TILED the element is stored at its tiled place
+// (kv_tiled_offset).
+template <bool TILED>
+__global__ __launch_bounds__(256) void fill_cache_kernel(uint16_t *dst, size_t rows, int Tmax, int Tlog, int len,
                                                          uint64_t seed, uint64_t stream, float amp) {
     const size_t n = rows * (size_t)Tmax * 256;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        const int t = (int)((i / 256) % Tmax);
-        dst[i] = t < len ? f32_to_f16_rne(hash_value(seed, stream, i, amp, 0.f)) : 0;
+        const size_t row = i / ((size_t)Tmax * 256);
+        const int t = (int)((i / 256) % Tmax), d = (int)(i % 256);
+        const size_t li = (row * Tlog + t) * 256 + d;
+        const uint16_t v = t < len ? f32_to_f16_rne(hash_value(seed, stream, li, amp, 0.f)) : 0;
+        dst[row * Tmax * 256 + (TILED ? kv_tiled_offset(t, d) : (size_t)t * 256 + d)] = v;
     }
 }
 unsigned fill_blocks(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
@@ -177,7 +185,7 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     }
     const uint16_t o = f32_to_f16_rne(y);
     if (is_q) q16[((size_t)b * Hq + slot) * 256 + d] = o;
-    else Kc[(((size_t)b * Hkv + (slot - Hq)) * Tmax + pos) * 256 + d] = o;
+    else Kc[((size_t)b * Hkv + (slot - Hq)) * Tmax * 256 + kv_tiled_offset(pos, d)] = o;  // K is tiled
 }
 
 // next[b] = the first index of the largest logit of row b.  Block (j, b)
@@ -269,7 +277,7 @@ struct Layer {
     Mat gate_up, down;
     float *S = nullptr;                          // [B][Hv][128][128]
     float *conv_state[2] = {nullptr, nullptr};   // [B][conv_dim][4], the current one is conv_state[parity]
-    uint16_t *Kc = nullptr, *Vc = nullptr;      // [B][Hkv][Tmax][256]
+    uint16_t *Kc = nullptr, *Vc = nullptr;      // [B][Hkv][tmax][256], K tiled by 16 positions
 };
 
 // Rows of the interleaved gate/up matrix: row R takes row 8 (R / 16) + R % 8
@@ -313,6 +321,7 @@ struct kai_gdn_hybrid {
     size_t bytes = 0, weight_bytes = 0;
     int batch = 0, pos = 0;
     int parity = 0;  // which conv cache of each GDN layer is current
+    int tmax = 0;    // KV cache positions: max_context rounded up to 16 (K is tiled by 16)
 };
 
 namespace gdn {
@@ -427,6 +436,7 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
               Hkv = c.attn_kv_heads, Bm = c.max_batch;
     m->conv_dim = 2 * Hk * 128 + Hv * 128;
     m->value_dim = Hv * 128;
+    m->tmax = (c.max_context + 15) / 16 * 16;
     // staging for the builders: the largest matrix (padded), fp32 and int8
     const size_t tmp_n = std::max({(size_t)pad64(c.vocab) * H, (size_t)2 * I * H, (size_t)I * H,
                                    (size_t)pad64(m->conv_dim + m->value_dim + 2 * Hv) * H,
@@ -462,8 +472,8 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
                 TRY(make_fused(m, L.out, {{H, base + kOp}}, Hq * 256, seed, tmp));
                 TRY(make_vec(m, &L.q_norm, 256, seed, base + kQn, 0.1f, 0.f));
                 TRY(make_vec(m, &L.k_norm, 256, seed, base + kKn, 0.1f, 0.f));
-                TRY(alloc_t(m, &L.Kc, (size_t)Bm * Hkv * c.max_context * 256));
-                TRY(alloc_t(m, &L.Vc, (size_t)Bm * Hkv * c.max_context * 256));
+                TRY(alloc_t(m, &L.Kc, (size_t)Bm * Hkv * m->tmax * 256));
+                TRY(alloc_t(m, &L.Vc, (size_t)Bm * Hkv * m->tmax * 256));
             }
             TRY(make_gate_up(m, L.gate_up, I, H, seed, base + kGate, base + kUp, tmp));
             TRY(make_fused(m, L.down, {{H, base + kDown}}, I, seed, tmp));
@@ -538,12 +548,12 @@ hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     TRY(gemm(m, m->x16, L.in, segments({{m->qg, nq, nq}, {m->kx, nkv, nq + nkv}, {m->vx, nkv, nq + 2 * nkv}}),
              st));
     attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, B), 256, 0, st>>>(m->qg, m->kx, m->vx, L.q_norm, L.k_norm, m->q16,
-                                                                 L.Kc, L.Vc, Hq, Hkv, c.max_context, m->pos,
+                                                                 L.Kc, L.Vc, Hq, Hkv, m->tmax, m->pos,
                                                                  c.rope_theta, c.rms_eps);
     TRY(hipGetLastError());
     // o * sigmoid(gate) -> fp16 in the span combine; gate = dims 256..511 of each qg head
-    TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, nullptr, B, Hq, Hkv, c.max_context, m->pos + 1, 1.0f / 16.0f,
-                           m->attn_ws, st, m->qg + 256, 512, m->x16));
+    TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, nullptr, B, Hq, Hkv, m->tmax, m->pos + 1, 1.0f / 16.0f,
+                           m->attn_ws, st, m->qg + 256, 512, m->x16, /*k_tiled=*/true));
     return gemm_to(m, m->x16, L.out, m->mix, c.hidden, st);
 }
 
@@ -597,9 +607,11 @@ hipError_t reset(kai_gdn_hybrid *m, int batch, int context, uint64_t seed) {
             }
         } else {
             const size_t rows = (size_t)batch * c.attn_kv_heads;
-            const size_t n = rows * c.max_context * 256;
-            fill_cache_kernel<<<fill_blocks(n), 256>>>(L.Kc, rows, c.max_context, context, seed, base + kStK, 1.0f);
-            fill_cache_kernel<<<fill_blocks(n), 256>>>(L.Vc, rows, c.max_context, context, seed, base + kStV, 1.0f);
+            const size_t n = rows * m->tmax * 256;
+            fill_cache_kernel<true><<<fill_blocks(n), 256>>>(L.Kc, rows, m->tmax, c.max_context, context, seed,
+                                                             base + kStK, 1.0f);
+            fill_cache_kernel<false><<<fill_blocks(n), 256>>>(L.Vc, rows, m->tmax, c.max_context, context, seed,
+                                                              base + kStV, 1.0f);
             TRY(hipGetLastError());
         }
     }

@@ -160,10 +160,19 @@ hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, i
 // out [B][Hq][256] fp32; `workspace` holds attn_workspace_bytes(B, Hq, L).
 // With `gate` (non-null), the output is instead out16 [B][Hq][256] fp16 =
 // fp16(o * sigmoid(gate[(b * Hq + h) * gate_stride + d])).
+// k_tiled: K is stored tiled by 16 positions (Tmax % 16 == 0), element
+// (t, d) of a (sequence, kv head) at kv_tiled_offset(t, d); V stays
+// row-major.
 size_t attn_workspace_bytes(int B, int Hq, int L);
 hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
                               int B, int Hq, int Hkv, int Tmax, int L, float scaling, float *workspace,
                               hipStream_t st, const float *gate = nullptr, int gate_stride = 0,
-                              uint16_t *out16 = nullptr);
+                              uint16_t *out16 = nullptr, bool k_tiled = false);
+// Offset (in halfs, from the row of position 0) of K[t][d] in the tiled
+// layout: group t / 16 holds 8 x 512 halfs; chunk j (dims 32 j .. 32 j + 31)
+// holds lane (g, r) = (d / 8 % 4, t % 16)'s 8 dims at lane * 8.
+__host__ __device__ inline size_t kv_tiled_offset(int t, int d) {
+    return (size_t)(t & ~15) * 256 + (size_t)(d >> 5) * 512 + (size_t)(((d >> 3) & 3) * 16 + (t & 15)) * 8 + (d & 7);
+}
 
 }  // namespace gdn

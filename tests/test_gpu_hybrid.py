@@ -102,9 +102,10 @@ def test_hybrid_greedy_loop_on_device(hb, fixture):
 
 def test_hybrid_drawn_context_two_spans(hb, fixture):
     """Three sequences after a drawn 300-token context (the attention decode
-    reads two 256-position spans and combines them)."""
+    reads two 256-position spans and combines them), in a cache of 310
+    positions (the device rounds its tiled K cache up to 320)."""
     d, fields = fixture
-    gm, om = models(hb, fields, 77, max_batch=3, max_context=320)
+    gm, om = models(hb, fields, 77, max_batch=3, max_context=310)
     gm.reset(3, 300, 9)
     om.reset(3, 300, 9)
     rs = np.random.RandomState(2)
