@@ -352,13 +352,17 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
 
 }  // namespace
 
-// Launch shape from a sweep over the Qwen3.5-4B matrices at M = 1 and 16:
-// eight waves, one step in flight per wave, and k-splits only for narrow
-// matrices, the fewest that give 160 blocks (the cross-block hand-off costs
-// more than the extra parallelism beyond that).
+// Launch shape from a sweep over the Qwen3.5-4B matrices at M = 1 and 16
+// (weights rotated through 1.5 GB so none comes from the Infinity Cache):
+// one step in flight per wave; eight waves per block when there are fewer
+// blocks than CUs (each block must pull more bytes), four when there are
+// more (a CU then holds several blocks at once: gate|up 10.7 us against
+// 12.3 us); k-splits only for narrow matrices, the fewest that give 160
+// blocks (the cross-block hand-off costs more than the extra parallelism
+// beyond that).
 W8fShape w8f_shape(int N, int K) {
     const int groups = N / kW8fGroup;
-    W8fShape sh{K % 512 == 0 ? 8 : 4, 1, 1};
+    W8fShape sh{K % 512 == 0 && groups <= 256 ? 8 : 4, 1, 1};
     for (int S = 2; S <= 32 && groups * sh.splits < 160; ++S)
         if (K % (S * sh.waves * kKStep) == 0) sh.splits = S;
     return sh;
