@@ -202,3 +202,23 @@ def test_e2e_driver_runs(hb):
     assert lines[0].startswith("model,ctx_len,gdn_layer_us,full_attn_us,ffn_us,total_us")
     assert [ln.split(",")[1] for ln in lines[1:]] == ["1", "300"]
     assert all(float(ln.split(",")[5]) > 0 for ln in lines[1:])
+
+
+def test_hybrid_real_head_counts_vs_oracle(hb, fixture):
+    """The 4B model's head counts (GDN 16 key / 32 value heads, attention 16
+    query / 4 kv heads, so the in-projection is the 4B's 12352 rows) with a
+    small hidden size and vocabulary, 8 layers (two attention), batch 4,
+    after a drawn 40-token context: logits against the CPU model."""
+    d, fields = fixture
+    over = dict(layers=8, hidden=512, inter=1024, vocab=2048, gdn_k_heads=16, gdn_v_heads=32, attn_q_heads=16,
+                attn_kv_heads=4, max_batch=4, max_context=64)
+    gm, om = models(hb, fields, 4242, **over)
+    gm.reset(4, 40, 11)
+    om.reset(4, 40, 11)
+    rs = np.random.RandomState(9)
+    for t in range(5):
+        tok = rs.randint(0, over["vocab"], 4)
+        nxt, lg = step(gm, tok, over["vocab"])
+        _, olg = om.step(tok)
+        assert_close(lg, olg, f"4B heads step {t}")
+        assert_greedy(nxt, lg, olg)
