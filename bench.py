@@ -146,27 +146,37 @@ def bench_decode(L, ob, torch, steps, warmup, timer):
     return ms_step, kern_ms, layers
 
 
-def cpu_decode_baseline(budget_s=12.0):
+def cpu_decode_baseline(budget_s=12.0, single_budget_s=6.0):
     """The oracle (OpenMP over (sequence, head)) on the same per-layer step;
     runs whole layers until the budget is spent, reports tokens/s of a
-    24-layer step."""
+    24-layer step.  Then the same on one thread (OpenMP set to 1)."""
     from oracle import oracle as orc
     from tests.gdn_inputs import decode_inputs
     S, q, k, v, g, beta = decode_inputs(1000, B_DEC, HV, HK, DK, DV)
-    orc.delta_rule_decode(S, q, k, v, g, beta, B_DEC, HV, HK, DK, DV, 1 / math.sqrt(DK))
-    n, t0 = 0, time.perf_counter()
-    while True:
-        S, _ = orc.delta_rule_decode(S, q, k, v, g, beta, B_DEC, HV, HK, DK, DV,
-                                     1 / math.sqrt(DK))
-        n += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or n >= 240:
-            break
-    per_layer = el / n
-    return {"value": round(B_DEC / (per_layer * LAYERS), 2), "unit": "tokens/s",
-            "cores": orc.num_threads(), "kind": "port",
+
+    def run(budget, cap):
+        nonlocal S
+        orc.delta_rule_decode(S, q, k, v, g, beta, B_DEC, HV, HK, DK, DV, 1 / math.sqrt(DK))
+        n, t0 = 0, time.perf_counter()
+        while True:
+            S, _ = orc.delta_rule_decode(S, q, k, v, g, beta, B_DEC, HV, HK, DK, DV, 1 / math.sqrt(DK))
+            n += 1
+            el = time.perf_counter() - t0
+            if el > budget or n >= cap:
+                return n, el
+
+    threads = orc.num_threads()
+    n, el = run(budget_s, 240)
+    orc.set_num_threads(1)
+    n1, el1 = run(single_budget_s, 24)
+    orc.set_num_threads(threads)
+    return {"value": round(B_DEC / (el / n * LAYERS), 2), "unit": "tokens/s",
+            "cores": threads, "kind": "port",
             "sample": f"{n} layer-steps of B=64 x 32 heads x 128x128 fp32 "
-                      f"({n / LAYERS:.1f} full 24-layer steps), {el:.1f} s"}
+                      f"({n / LAYERS:.1f} full 24-layer steps), {el:.1f} s",
+            "single_thread": {"value": round(B_DEC / (el1 / n1 * LAYERS), 2), "cores": 1,
+                              "sample": f"{n1} layer-steps, {el1:.1f} s"},
+            "cpu_model": cpu_model()}
 
 
 def bench_prefill(L, ob, torch, timer, reps=5):
@@ -432,6 +442,81 @@ def bench_stream(L, ob, torch, timer, reps=40, sets=4):
     )
 
 
+def measure_peaks(L, ob, torch, timer):
+    """What this GPU delivers, measured with the library's probes
+    (kai_gdn_hip_probe_*): a 2 GiB streaming copy (bytes read + written), a
+    4 GiB streaming read, and independent bf16 MFMA chains (32x32x16, and
+    16x16x32) on 16 blocks per CU.  Both buffers exceed the 256 MB Infinity
+    Cache."""
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sink = torch.empty(L.kai_gdn_hip_probe_sink_bytes() // 4 + 1, dtype=torch.float32, device="cuda")
+    nb = 2 << 30
+    src = torch.empty(nb // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+
+    def copy():
+        ob.check(L.kai_gdn_hip_probe_stream(src.data_ptr(), dst.data_ptr(), nb, 0, sink.data_ptr(), stream), "probe")
+
+    ms = timer.p50_ms(copy, warmup=3, reps=10)
+    copy_gbs = 2 * nb / (ms * 1e-3) / 1e9
+    del dst
+    big = torch.empty((4 << 30) // 4, dtype=torch.float32, device="cuda")
+    big.fill_(1.0)
+
+    def read():
+        ob.check(L.kai_gdn_hip_probe_stream(big.data_ptr(), None, big.numel() * 4, 1, sink.data_ptr(), stream),
+                 "probe")
+
+    ms = timer.p50_ms(read, warmup=3, reps=10)
+    read_gbs = big.numel() * 4 / (ms * 1e-3) / 1e9
+    del big, src
+    flops = ctypes.c_ulonglong(0)
+    tflops = []
+    for shape in (0, 1):
+        def mfma():
+            ob.check(L.kai_gdn_hip_probe_mfma_bf16(2000, shape, sink.data_ptr(), ctypes.byref(flops), stream),
+                     "probe")
+
+        ms = timer.p50_ms(mfma, warmup=3, reps=10)
+        tflops.append(flops.value / (ms * 1e-3) / 1e12)
+    torch.cuda.empty_cache()
+    return {"hbm_copy_gbs": round(copy_gbs, 1), "hbm_read_gbs": round(read_gbs, 1),
+            "mfma_bf16_tflops": round(tflops[0], 1), "mfma_bf16_16x16x32_tflops": round(tflops[1], 1),
+            "note": "measured on this GPU with kai_gdn_hip_probe_*: 2 GiB copy (bytes read + written), 4 GiB "
+                    "read, bf16 MFMA 32x32x16 chains (and 16x16x32, the prefill's instruction); the "
+                    "roofline fractions use the datasheet peaks, the *_measured fractions these"}
+
+
+def add_measured_fracs(d, peaks, read_bound=False):
+    """frac_measured next to every hbm_frac / mfma_frac of a result tree."""
+    if isinstance(d, list):
+        for x in d:
+            add_measured_fracs(x, peaks, read_bound)
+        return
+    if not isinstance(d, dict):
+        return
+    if "achieved_gbs" in d:
+        ref = peaks["hbm_read_gbs"] if read_bound else peaks["hbm_copy_gbs"]
+        d["hbm_frac_measured"] = round(d["achieved_gbs"] / ref, 4)
+    if "achieved_tflops" in d:
+        d["mfma_frac_measured"] = round(d["achieved_tflops"] / peaks["mfma_bf16_tflops"], 4)
+    for v in d.values():
+        if isinstance(v, (dict, list)):
+            add_measured_fracs(v, peaks, read_bound)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def run_profile(which, L, ob, torch, timer, steps, warmup):
     """Workload for rocprofv3: `which`, then a plain copy kernel
     (dst = src * 1 over 64M fp32: reads and writes exactly 268,435,456 bytes),
@@ -488,6 +573,9 @@ def main():
         run_profile(args.profile, L, ob, torch, timer, args.steps, args.warmup)
         return
 
+    log("measured ceilings (copy, read, MFMA probes) ...")
+    peaks = measure_peaks(L, ob, torch, timer)
+    log(f"peaks: {peaks}")
     log("decode: 24 layers x B=64 ...")
     ms_step, kern_ms, _ = bench_decode(L, ob, torch, args.steps, args.warmup, timer)
     achieved = DEC_BYTES / (kern_ms * 1e-3) / 1e9
@@ -543,8 +631,12 @@ def main():
                      "kernel": "delta_decode_kernel<128,128,f32>",
                      "bytes_per_launch": DEC_BYTES, "launch_us": round(kern_ms * 1e3, 2)},
         "cpu_baseline": cpu,
+        "measured_peaks": peaks,
         "secondary": secondary,
     }
+    line["roofline"]["frac_measured"] = round(achieved / peaks["hbm_copy_gbs"], 4)
+    for key, val in secondary.items():
+        add_measured_fracs(val, peaks, read_bound=(key == "hybrid_decode"))
     print(json.dumps(line), flush=True)
 
 

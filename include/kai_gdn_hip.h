@@ -273,6 +273,23 @@ const char *kai_gdn_hip_error_string(int code);
  * is invalid).  Synchronises the device, then clears the flag. */
 int kai_gdn_hip_check_device_error(void);
 
+/* ---- measurement probes --------------------------------------------------
+ * No reference counterpart: what the current device delivers for a
+ * streaming copy or read and for dense bf16 MFMA, so that roofline fractions
+ * can be stated against measured ceilings as well as datasheet peaks.  They
+ * compute nothing of the GDN path.  `sink` is device memory of
+ * kai_gdn_hip_probe_sink_bytes() bytes (written, contents meaningless). */
+size_t kai_gdn_hip_probe_sink_bytes(void);
+/* mode 0: dst = src over `bytes` (a multiple of 16, 16-byte aligned);
+ * mode 1: read src only (dst unused).  Time it with events on `stream`. */
+int kai_gdn_hip_probe_stream(const void *src, void *dst, size_t bytes, int mode, void *sink,
+                             void *stream);
+/* Independent bf16 MFMA chains of `iters` steps on every wave of 16 blocks
+ * per CU: shape 0 is 32x32x16 (four chains per wave), 1 is 16x16x32 (eight);
+ * *flops receives the launch's multiply-add count x 2. */
+int kai_gdn_hip_probe_mfma_bf16(int iters, int shape, void *sink, unsigned long long *flops,
+                                void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,14 @@ int orc_num_threads(void) {
 #endif
 }
 
+void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n > 0 ? n : 1);
+#else
+    (void)n;
+#endif
+}
+
 /* ======================================================================== */
 /* kai ukernels (portable scalar branches)                                   */
 /* ======================================================================== */

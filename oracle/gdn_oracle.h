@@ -228,8 +228,10 @@ int orc_hybrid_position(const orc_hybrid *m);
 long orc_hybrid_tensor(const orc_hybrid *m, int layer, int id, float *dst);
 void orc_hybrid_destroy(orc_hybrid *m);
 
-/* Number of OpenMP threads the oracle uses (1 when built without OpenMP). */
+/* Number of OpenMP threads the oracle uses (1 when built without OpenMP),
+ * and a way to set it (the CPU baseline's single-thread run). */
 int orc_num_threads(void);
+void orc_set_num_threads(int n);
 
 #ifdef __cplusplus
 }

@@ -302,6 +302,10 @@ def num_threads() -> int:
     return lib().orc_num_threads()
 
 
+def set_num_threads(n: int) -> None:
+    lib().orc_set_num_threads(int(n))
+
+
 # ---- hybrid decode loop ----------------------------------------------------
 
 class HybridConfig(ctypes.Structure):

@@ -61,6 +61,9 @@ HIP_SYMBOLS = (
     "kai_gdn_hip_init",
     "kai_gdn_hip_error_string",
     "kai_gdn_hip_check_device_error",
+    "kai_gdn_hip_probe_sink_bytes",
+    "kai_gdn_hip_probe_stream",
+    "kai_gdn_hip_probe_mfma_bf16",
 )
 ALL_SYMBOLS = KAI_SYMBOLS + HIP_SYMBOLS
 
@@ -133,6 +136,9 @@ _SIGS = {
     "kai_gdn_hip_init": (_i, []),
     "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
     "kai_gdn_hip_check_device_error": (_i, []),
+    "kai_gdn_hip_probe_sink_bytes": (_sz, []),
+    "kai_gdn_hip_probe_stream": (_i, [_vp, _vp, _sz, _i, _vp, _vp]),
+    "kai_gdn_hip_probe_mfma_bf16": (_i, [_i, _i, _vp, ctypes.POINTER(ctypes.c_ulonglong), _vp]),
 }
 
 _lib = None

@@ -175,4 +175,12 @@ __host__ __device__ inline size_t kv_tiled_offset(int t, int d) {
     return (size_t)(t & ~15) * 256 + (size_t)(d >> 5) * 512 + (size_t)(((d >> 3) & 3) * 16 + (t & 15)) * 8 + (d & 7);
 }
 
+// ---- measurement probes (gdn_probe.hip) -----------------------------------
+
+size_t probe_sink_words(int cu_count);
+hipError_t launch_probe_stream(const void *src, void *dst, size_t bytes, int mode, uint32_t *sink, int cu_count,
+                               hipStream_t st);
+hipError_t launch_probe_mfma(float *sink, int iters, int shape, int cu_count, unsigned long long *flops,
+                             hipStream_t st);
+
 }  // namespace gdn

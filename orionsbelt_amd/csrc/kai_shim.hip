@@ -273,6 +273,34 @@ extern "C" int kai_gdn_hip_check_device_error(void) {
     return (int)v;
 }
 
+extern "C" size_t kai_gdn_hip_probe_sink_bytes(void) {
+    DeviceCtx *c;
+    if (get_ctx(&c) != hipSuccess) return 0;
+    return gdn::probe_sink_words(c->scan.cu_count) * 4;
+}
+
+extern "C" int kai_gdn_hip_probe_stream(const void *src, void *dst, size_t bytes, int mode, void *sink,
+                                        void *stream) {
+    DeviceCtx *c;
+    hipError_t e = get_ctx(&c);
+    if (e != hipSuccess) return (int)e;
+    if (!src || !sink || (mode == 0 && !dst) || (mode != 0 && mode != 1) || bytes % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(src) % 16 != 0 || (mode == 0 && reinterpret_cast<uintptr_t>(dst) % 16 != 0))
+        return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_probe_stream(src, dst, bytes, mode, static_cast<uint32_t *>(sink), c->scan.cu_count,
+                                         (hipStream_t)stream);
+}
+
+extern "C" int kai_gdn_hip_probe_mfma_bf16(int iters, int shape, void *sink, unsigned long long *flops,
+                                           void *stream) {
+    DeviceCtx *c;
+    hipError_t e = get_ctx(&c);
+    if (e != hipSuccess) return (int)e;
+    if (iters < 1 || (shape != 0 && shape != 1) || !sink || !flops) return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_probe_mfma(static_cast<float *>(sink), iters, shape, c->scan.cu_count, flops,
+                                       (hipStream_t)stream);
+}
+
 // ===========================================================================
 // Device-pointer entry points
 // ===========================================================================
