@@ -18,7 +18,8 @@ The JSON line also carries:
   secondary     prefill (config 3, T=16K), the fp16-state prefill at
                 T in {1K, 8K, 32K, 128K} (config 4: tokens/s and the per-layer
                 state footprint), conv+SiLU (config 1) and cumulative decay
-                ([4096][8192]) throughput and roofline, the layer glue, and
+                ([4096][8192]) throughput and roofline, the gated scan and
+                the fp16/bf16 scan and decay variants, the layer glue, and
                 the hybrid decode loop (config 5: B=1 and B=16, 256 greedy
                 steps after a 32K context)
 Synthetic inputs with the BASELINE distributions; random state.
@@ -442,6 +443,62 @@ def bench_stream(L, ob, torch, timer, reps=40, sets=4):
     )
 
 
+def bench_scans(L, ob, torch, timer, reps=40, sets=4):
+    """The diagonal gated scan (row a3) and the narrow-state variants of the
+    scan and of the cumulative decay (row a6) at [4096][8192], rotating
+    `sets` buffer sets (over 1.5 GiB).  Bytes per launch: the scan reads g
+    and x and writes s ([T][C] fp32 each) and reads and writes its state
+    ([C], fp32 or 2-byte); the narrow decay reads a (fp32) and writes decay
+    (2-byte)."""
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    T, C = DEC_T, DEC_C
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    gs = [torch.rand(T * C, generator=gen, device="cuda") for _ in range(sets)]
+    xs = [torch.randn(T * C, generator=gen, device="cuda") for _ in range(sets)]
+    ss = [torch.empty(T * C, device="cuda") for _ in range(sets)]
+    st32 = torch.zeros(C, device="cuda")
+    st16 = torch.zeros(C, dtype=torch.int16, device="cuda")
+    d16 = [torch.empty(T * C, dtype=torch.int16, device="cuda") for _ in range(sets)]
+    it = [0]
+    out = {}
+
+    def run(name, fn, nbytes, narrow):
+        def call():
+            j = it[0] % sets
+            it[0] += 1
+            rc = fn(j)
+            if rc:
+                ob.check(rc, name)
+
+        for _ in range(sets):
+            call()
+        ms = timer.time_ms(call, reps)
+        if L.kai_gdn_hip_check_device_error() != 0:
+            raise RuntimeError(f"{name}: look-back watchdog fired")
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        what = "output" if name.startswith("cumdecay") else "state"
+        out[name] = {"workload": f"{name.replace('_', ' ')} [{T}][{C}]" + (f", {narrow} {what}" if narrow else ""),
+                     "us": round(ms * 1e3, 2), "bytes_per_launch": nbytes, "achieved_gbs": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    scan32 = 3 * T * C * 4 + 2 * C * 4
+    scan16 = 3 * T * C * 4 + 2 * C * 2
+    run("gated_scan_f32", lambda j: L.kai_run_gdn_gated_scan_f32_hip(
+        gs[j].data_ptr(), xs[j].data_ptr(), ss[j].data_ptr(), st32.data_ptr(), T, C, stream), scan32, None)
+    run("gated_scan_f16", lambda j: L.kai_run_gdn_gated_scan_f16_hip(
+        gs[j].data_ptr(), xs[j].data_ptr(), ss[j].data_ptr(), st16.data_ptr(), T, C, stream), scan16, "fp16")
+    run("gated_scan_bf16", lambda j: L.kai_run_gdn_gated_scan_bf16_hip(
+        gs[j].data_ptr(), xs[j].data_ptr(), ss[j].data_ptr(), st16.data_ptr(), T, C, stream), scan16, "bf16")
+    run("cumdecay_f16", lambda j: L.kai_run_gdn_cumdecay_f16_hip(
+        gs[j].data_ptr(), d16[j].data_ptr(), T, C, stream), T * C * 6, "fp16")
+    run("cumdecay_bf16", lambda j: L.kai_run_gdn_cumdecay_bf16_hip(
+        gs[j].data_ptr(), d16[j].data_ptr(), T, C, stream), T * C * 6, "bf16")
+    del gs, xs, ss, d16
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_peaks(L, ob, torch, timer):
     """What this GPU delivers, measured with the library's probes
     (kai_gdn_hip_probe_*): a 2 GiB streaming copy (bytes read + written), a
@@ -592,6 +649,9 @@ def main():
         log("conv / decay ...")
         secondary["conv"], secondary["cumdecay"] = bench_stream(L, ob, torch, timer)
         log(f"conv: {secondary['conv']}\ncumdecay: {secondary['cumdecay']}")
+        log("gated scan and narrow-state scan/decay ...")
+        secondary["scans"] = bench_scans(L, ob, torch, timer)
+        log(f"scans: {secondary['scans']}")
         log("layer glue (gating prologue, gated RMSNorm) ...")
         secondary["gating_prologue"], secondary["gated_rmsnorm"] = bench_layer_glue(L, ob, torch, timer)
         log(f"gating prologue: {secondary['gating_prologue']}\n"
