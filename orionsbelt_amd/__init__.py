@@ -47,6 +47,9 @@ HIP_SYMBOLS = (
     "kai_run_gdn_state_convert_hip",
     "kai_gdn_w8a16_gemm_workspace_bytes",
     "kai_run_gdn_w8a16_gemm_hip",
+    "kai_run_gdn_w8_tile_hip",
+    "kai_gdn_w8a16_gemm_tiled_workspace_bytes",
+    "kai_run_gdn_w8a16_gemm_tiled_hip",
     "kai_run_gdn_w8_quantize_hip",
     "kai_gdn_attn_decode_workspace_bytes",
     "kai_run_gdn_attn_decode_f16kv_hip",
@@ -120,6 +123,9 @@ _SIGS = {
     "kai_run_gdn_state_convert_hip": (_i, [_vp, _i, _vp, _i, _sz, _vp]),
     "kai_gdn_w8a16_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
     "kai_run_gdn_w8a16_gemm_hip": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "kai_run_gdn_w8_tile_hip": (_i, [_vp, _vp, _i, _i, _vp]),
+    "kai_gdn_w8a16_gemm_tiled_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kai_run_gdn_w8a16_gemm_tiled_hip": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "kai_run_gdn_w8_quantize_hip": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "kai_gdn_attn_decode_workspace_bytes": (_sz, [_i, _i, _i]),
     "kai_run_gdn_attn_decode_f16kv_hip":

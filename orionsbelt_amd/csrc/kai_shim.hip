@@ -605,6 +605,43 @@ extern "C" int kai_run_gdn_w8a16_gemm_hip(const uint16_t *x, const int8_t *Wq, c
                                     (hipStream_t)stream);
 }
 
+extern "C" int kai_run_gdn_w8_tile_hip(const int8_t *Wq, int8_t *Wt, int N, int K, void *stream) {
+    if (N < 0 || K <= 0 || N % 64 || K % 256) return (int)hipErrorInvalidValue;
+    if (N == 0) return 0;
+    if (!Wq || !Wt || Wq == Wt || !aligned(Wq, 16) || !aligned(Wt, 16)) return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_w8f_tile(Wq, Wt, N, K, (hipStream_t)stream);
+}
+
+// workspace: the split partials (floats), then N / 64 counters
+static size_t w8f_ws_bytes(int M, int N, int K) {
+    const size_t part = gdn::w8f_workspace_floats(M, N, K);
+    return part ? (part * sizeof(float) + (size_t)(N / 64) * sizeof(uint32_t) + 255) / 256 * 256 : 0;
+}
+
+extern "C" size_t kai_gdn_w8a16_gemm_tiled_workspace_bytes(int M, int N, int K) {
+    if (M <= 0 || M > 16 || N <= 0 || K <= 0 || N % 64 || K % 256) return 0;
+    return w8f_ws_bytes(M, N, K);
+}
+
+extern "C" int kai_run_gdn_w8a16_gemm_tiled_hip(const uint16_t *x, const int8_t *Wt, const float *scale, float *y,
+                                                int M, int N, int K, void *workspace, size_t workspace_bytes,
+                                                void *stream) {
+    if (M < 0 || M > 16 || N < 0 || K <= 0 || N % 64 || K % 256) return (int)hipErrorInvalidValue;
+    if (M == 0 || N == 0) return 0;
+    if (!x || !Wt || !scale || !y) return (int)hipErrorInvalidValue;
+    if (!aligned(x, 16) || !aligned(Wt, 16) || !aligned(scale, 16) || !aligned(y, 16))
+        return (int)hipErrorInvalidValue;
+    const size_t need = w8f_ws_bytes(M, N, K);
+    if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 256))) return (int)hipErrorInvalidValue;
+    float *part = static_cast<float *>(workspace);
+    uint32_t *cnt = need ? reinterpret_cast<uint32_t *>(part + gdn::w8f_workspace_floats(M, N, K)) : nullptr;
+    gdn::W8Out o{};
+    o.seg[0] = gdn::W8Seg{y, N, N};
+    o.nseg = 1;
+    o.mode = gdn::kW8Segments;
+    return (int)gdn::launch_w8f(x, Wt, scale, M, N, K, o, part, cnt, (hipStream_t)stream);
+}
+
 extern "C" int kai_run_gdn_w8_quantize_hip(const float *W, int8_t *Wq, float *scale, int N, int K,
                                            void *stream) {
     if (N < 0 || K < 0) return (int)hipErrorInvalidValue;

@@ -73,6 +73,61 @@ def test_w8a16_gemm_vs_oracle(L, M, N, K):
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))       # deterministic
 
 
+def gpu_gemm_tiled(L, x16, q, s, reps=1):
+    """Tile Wq on the device, run the tiled GEMM `reps` times on one zeroed
+    workspace; returns the outputs and the workspace's counters after."""
+    torch = torch_mod()
+    M, K = x16.shape
+    N = q.shape[0]
+    dx, dq, ds = dev(x16.view(np.int16)), dev(q), dev(s)
+    wt = torch.empty_like(dq)
+    assert L.kai_run_gdn_w8_tile_hip(P(dq), P(wt), N, K, stream()) == 0
+    nb = L.kai_gdn_w8a16_gemm_tiled_workspace_bytes(M, N, K)
+    ws = torch.zeros(max(nb, 256) // 4, dtype=torch.float32, device="cuda")
+    ys = []
+    for _ in range(reps):
+        y = empty((M, N), torch.float32)
+        assert L.kai_run_gdn_w8a16_gemm_tiled_hip(P(dx), P(wt), P(ds), P(y), M, N, K, P(ws), nb, stream()) == 0
+        ys.append(host(y))
+    cnt = host(ws.view(torch.int32))[-(N // 64):] if nb else np.zeros(1, np.int32)
+    return ys, cnt
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (5, 2560, 4096), (16, 12352, 2560), (3, 2560, 9216),
+                                   (16, 1024, 512), (1, 18432, 2560)])
+def test_w8a16_gemm_tiled_vs_oracle(L, M, N, K):
+    """The tiled-weight GEMM (the hybrid loop's): against the oracle at the
+    row-major GEMM's bar, deterministic over calls that share one workspace
+    (split shapes: down and out_proj), and the workspace's counters are back
+    at zero after every call."""
+    rs = np.random.RandomState(M * 11 + N)
+    x = rs.randn(M, K).astype(np.float16)
+    W = (rs.randn(N, K) * rs.uniform(0.01, 2.0, (N, 1))).astype(np.float32)
+    q, s = orc.w8_quantize(W)
+    (y, y2), cnt = gpu_gemm_tiled(L, x.view(np.uint16), q, s, reps=2)
+    ref = orc.w8_gemm(x.view(np.uint16), q, s)
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    assert not cnt.any()
+
+
+def test_w8a16_gemm_tiled_rejects_bad_args(L):
+    torch = torch_mod()
+    t = empty((16 * 4096,), torch.float32)
+    assert L.kai_run_gdn_w8_tile_hip(P(t), P(t), 64, 256, stream()) != 0          # in place
+    assert L.kai_run_gdn_w8_tile_hip(P(t), None, 64, 256, stream()) != 0
+    u = empty((16 * 4096,), torch.float32)
+    assert L.kai_run_gdn_w8_tile_hip(P(t), P(u), 48, 256, stream()) != 0          # N % 64
+    fn = L.kai_run_gdn_w8a16_gemm_tiled_hip
+    assert fn(P(t), P(u), P(t), P(t), 17, 64, 256, P(t), 1 << 20, stream()) != 0  # M > 16
+    assert fn(P(t), P(u), P(t), P(t), 1, 48, 256, P(t), 1 << 20, stream()) != 0   # N % 64
+    assert fn(P(t), P(u), P(t), P(t), 1, 64, 200, P(t), 1 << 20, stream()) != 0   # K % 256
+    nb = L.kai_gdn_w8a16_gemm_tiled_workspace_bytes(4, 2560, 4096)
+    assert nb > 0
+    assert fn(P(t), P(u), P(t), P(t), 4, 2560, 4096, None, nb, stream()) != 0      # split needs a workspace
+    assert fn(P(t), P(u), P(t), P(t), 4, 2560, 4096, P(t), nb - 4, stream()) != 0
+
+
 def test_w8a16_gemm_rejects_bad_args(L):
     torch = torch_mod()
     t = empty((16 * 2560,), torch.float32)
