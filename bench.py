@@ -330,14 +330,17 @@ def hybrid_step_bytes(cfg, weight_bytes, B, pos):
     return weight_bytes + B * cfg.hidden * 2 + kv + state
 
 
-def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_STEPS):
+def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_STEPS, real_context=False):
     """the Qwen3.5-4B-shaped hybrid model (24 GDN + 8
     attention layers, int8 per-output-channel weights, fp16 activations and
     KV cache), greedy decoding of `steps` tokens per sequence after a
     `context`-token context, batch 1 and 16.  The context is represented by
     drawn states (KV caches, recurrent and conv states), not by running a
     prefill; tokens never leave the device (each step's argmax feeds the
-    next).  Timed with HIP events around the whole loop."""
+    next).  Timed with HIP events around the whole loop.  With real_context
+    the context is built instead by stepping `context` uniform-random tokens
+    through the model (a prefill by decode steps, untimed), so that the
+    decode rate after a real context can be compared with the drawn one."""
     from orionsbelt_amd import hybrid as hb
     rows = []
     for B in batches:
@@ -349,7 +352,23 @@ def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_S
         logits = torch.empty(B, cfg.vocab, dtype=torch.float32, device="cuda")
         for _ in range(3):  # warm-up steps, then a fresh context
             m.step(tok, nxt, logits)
-        m.reset(B, context, 7)
+        if real_context:
+            m.reset(B, 0, 7)
+            gen = torch.Generator(device="cuda")
+            gen.manual_seed(2026)
+            prompt = torch.randint(0, cfg.vocab, (context, B), dtype=torch.int32, device="cuda", generator=gen)
+            t0 = time.perf_counter()
+            for t in range(context):
+                m.step(prompt[t], None, None)
+                if (t + 1) % 4096 == 0:
+                    torch.cuda.synchronize()
+                    log(f"  B={B}: {t + 1} context tokens stepped")
+            torch.cuda.synchronize()
+            log(f"  B={B}: stepped a {context}-token context in {time.perf_counter() - t0:.1f} s")
+            tok.copy_(prompt[-1])
+            del prompt
+        else:
+            m.reset(B, context, 7)
         bufs = [tok, nxt]
 
         def run():
@@ -360,16 +379,18 @@ def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_S
         per = ms / steps
         nbytes = sum(hybrid_step_bytes(cfg, m.weight_bytes, B, context + i) for i in range(steps)) / steps
         gbs = nbytes / (per * 1e-3) / 1e9
-        rows.append({"batch": B, "context": context, "steps": steps, "ms_per_step": round(per, 4),
+        rows.append({"batch": B, "context": context, "context_kind": "stepped" if real_context else "drawn",
+                     "steps": steps, "ms_per_step": round(per, 4),
                      "tokens_per_s": round(B / (per * 1e-3), 1), "bytes_per_step": int(nbytes),
                      "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                      "device_bytes": m.device_bytes})
         m.close()
         del m, logits, tok, nxt, bufs
         torch.cuda.empty_cache()
+    kind = "a stepped" if real_context else "a drawn"
     return {"workload": f"hybrid decode loop, Qwen3.5-4B shape (32 layers: 24 GDN + 8 attention, hidden 2560, "
                         f"inter 9216, vocab 151936), int8 weights, fp16 activations and KV cache, greedy, "
-                        f"{steps} steps after a drawn {context}-token context (BASELINE configs[4])",
+                        f"{steps} steps after {kind} {context}-token context (BASELINE configs[4])",
             "runs": rows}
 
 
@@ -590,6 +611,8 @@ def run_profile(which, L, ob, torch, timer, steps, warmup):
         log(f"gating prologue: {pro}\ngated rmsnorm: {rn}")
     elif which == "hybrid":
         log(f"hybrid: {bench_hybrid(torch, timer, steps=steps)}")
+    elif which == "hybrid_real":
+        log(f"hybrid (stepped context): {bench_hybrid(torch, timer, steps=steps, real_context=True)}")
     else:
         conv, decay = bench_stream(L, ob, torch, timer, reps=steps)
         log(f"{which}: {conv if which == 'conv' else decay}")
@@ -609,7 +632,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip prefill/conv/decay lines")
     ap.add_argument("--profile", choices=["decode", "prefill", "prefill_f16", "layer", "conv", "cumdecay",
-                                          "hybrid"],
+                                          "hybrid", "hybrid_real"],
                     help="run only this workload (and a 256 MiB device copy that calibrates "
                          "HBM byte counters) for rocprofv3; prints no JSON line")
     args = ap.parse_args()
