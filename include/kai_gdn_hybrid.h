@@ -46,7 +46,7 @@ typedef struct {
     int attn_q_heads;  /* 16; head dim 256 */
     int attn_kv_heads; /* 4 (q_heads / kv_heads <= 4) */
     int max_batch;   /* <= 16 */
-    int max_context; /* KV cache length */
+    int max_context; /* KV cache length (<= 2^24) */
     float rope_theta; /* 1e7 */
     float rms_eps;    /* 1e-6 */
 } kai_gdn_hybrid_config;

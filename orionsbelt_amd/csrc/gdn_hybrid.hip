@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cmath>
 #include <initializer_list>
+#include <new>
 #include <vector>
 
 #include "gdn_common.h"
@@ -653,13 +654,20 @@ extern "C" int kai_gdn_hybrid_create(const kai_gdn_hybrid_config *cfg, unsigned 
                     c.hidden <= 4 * 256 * gdn::kNormChunks && c.inter > 0 &&
                     c.inter % 256 == 0 && c.vocab > 0 && c.vocab % 16 == 0 && c.gdn_k_heads > 0 &&
                     c.gdn_v_heads % 16 == 0 && c.gdn_v_heads % c.gdn_k_heads == 0 && c.gdn_v_heads > 0 &&
-                    c.attn_kv_heads > 0 && c.attn_q_heads % c.attn_kv_heads == 0 &&
+                    c.attn_kv_heads > 0 && c.attn_q_heads > 0 && c.attn_q_heads % c.attn_kv_heads == 0 &&
                     c.attn_q_heads / c.attn_kv_heads <= 4 && c.max_batch >= 1 && c.max_batch <= 16 &&
-                    c.max_context >= 1 && c.rms_eps >= 0.f && c.rope_theta > 0.f;
+                    c.max_context >= 1 && c.max_context <= (1 << 24) && c.rms_eps >= 0.f && c.rope_theta > 0.f;
     if (!ok) return (int)hipErrorInvalidValue;
-    kai_gdn_hybrid *m = new kai_gdn_hybrid;
-    m->cfg = c;
-    const hipError_t e = gdn::build(m, seed);
+    // no C++ exception may cross the C ABI: allocation failures become codes
+    kai_gdn_hybrid *m = new (std::nothrow) kai_gdn_hybrid;
+    if (!m) return (int)hipErrorOutOfMemory;
+    hipError_t e;
+    try {
+        m->cfg = c;
+        e = gdn::build(m, seed);
+    } catch (...) {
+        e = hipErrorOutOfMemory;
+    }
     if (e != hipSuccess) {
         kai_gdn_hybrid_destroy(m);
         return (int)e;

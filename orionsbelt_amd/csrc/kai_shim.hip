@@ -25,6 +25,7 @@
 #include <cstring>
 #include <initializer_list>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include "gdn_internal.h"
@@ -86,8 +87,13 @@ hipError_t get_ctx(DeviceCtx **out) {
     DeviceCtx *c;
     {
         std::lock_guard<std::mutex> lk(g_ctx_mu);
-        if ((int)g_ctx.size() <= dev) g_ctx.resize(dev + 1, nullptr);
-        if (!g_ctx[dev]) g_ctx[dev] = new DeviceCtx();
+        try {  // no C++ exception may cross the C ABI
+            if ((int)g_ctx.size() <= dev) g_ctx.resize(dev + 1, nullptr);
+        } catch (...) {
+            return hipErrorOutOfMemory;
+        }
+        if (!g_ctx[dev]) g_ctx[dev] = new (std::nothrow) DeviceCtx();
+        if (!g_ctx[dev]) return hipErrorOutOfMemory;
         c = g_ctx[dev];
     }
     std::lock_guard<std::mutex> lk(c->mu);

@@ -149,6 +149,10 @@ def test_hybrid_rejects_bad_arguments(hb, fixture):
         hb.HybridModel(hb.config(**dict(fields, hidden=200)), 1)   # hidden % 256
     with pytest.raises(HipError):
         hb.HybridModel(hb.config(**dict(fields, attn_q_heads=8)), 1)   # 8 q heads per kv head
+    with pytest.raises(HipError):
+        hb.HybridModel(hb.config(**dict(fields, attn_q_heads=0)), 1)
+    with pytest.raises(HipError):
+        hb.HybridModel(hb.config(**dict(fields, max_context=(1 << 24) + 1)), 1)
 
 
 def test_hybrid_qwen35_4b_shape(hb):
