@@ -113,7 +113,10 @@ class Timer:
 
 
 
-def bench_decode(L, ob, torch, steps, warmup, timer):
+def bench_decode(L, ob, torch, steps, warmup, timer, f16_state=False):
+    """The configs[1] step: 24 launches of the decode kernel, one per layer,
+    each with its own state (fp32, or fp16 with f16_state: the narrow-state
+    variant of row a6, half the state bytes)."""
     from tests.gdn_inputs import decode_inputs
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     qs = 1.0 / math.sqrt(DK)
@@ -122,10 +125,12 @@ def bench_decode(L, ob, torch, steps, warmup, timer):
         S, q, k, v, g, beta = decode_inputs(1000 + l, B_DEC, HV, HK, DK, DV)
         t = {n: torch.from_numpy(a).cuda() for n, a in
              dict(S=S, q=q, k=k, v=v, g=g, beta=beta).items()}
+        if f16_state:
+            t["S"] = t["S"].half().view(torch.int16)
         t["o"] = torch.empty((B_DEC, HV, DV), dtype=torch.float32, device="cuda")
         layers.append(t)
     torch.cuda.synchronize()
-    fn = L.kai_run_gdn_delta_rule_decode_f32_hip
+    fn = L.kai_run_gdn_delta_rule_decode_f16state_hip if f16_state else L.kai_run_gdn_delta_rule_decode_f32_hip
 
     def launch(t):
         rc = fn(t["S"].data_ptr(), t["q"].data_ptr(), t["k"].data_ptr(), t["v"].data_ptr(),
@@ -672,6 +677,16 @@ def main():
         log("conv / decay ...")
         secondary["conv"], secondary["cumdecay"] = bench_stream(L, ob, torch, timer)
         log(f"conv: {secondary['conv']}\ncumdecay: {secondary['cumdecay']}")
+        log("decode with fp16 state ...")
+        ms16, kern16, _ = bench_decode(L, ob, torch, args.steps, args.warmup, timer, f16_state=True)
+        b16 = DEC_BYTES - B_DEC * HV * DK * DV * 4  # the state read + written at 2 bytes
+        gbs16 = b16 / (kern16 * 1e-3) / 1e9
+        secondary["decode_f16_state"] = {
+            "workload": "decode step, 24 layers, B=64, Hv=32 Hk=16, 128x128 fp16 state (fp32 arithmetic)",
+            "ms_per_step": round(ms16, 4), "tokens_per_s": round(B_DEC / (ms16 * 1e-3), 1),
+            "bytes_per_launch": b16, "launch_us": round(kern16 * 1e3, 2), "achieved_gbs": round(gbs16, 1),
+            "hbm_frac": round(gbs16 / HBM_PEAK_GBS, 4)}
+        log(f"decode fp16 state: {secondary['decode_f16_state']}")
         log("gated scan and narrow-state scan/decay ...")
         secondary["scans"] = bench_scans(L, ob, torch, timer)
         log(f"scans: {secondary['scans']}")
