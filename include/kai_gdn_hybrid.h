@@ -63,7 +63,9 @@ int kai_gdn_hybrid_create(const kai_gdn_hybrid_config *cfg, unsigned long long s
 int kai_gdn_hybrid_reset(kai_gdn_hybrid *m, int batch, int context, unsigned long long seed);
 /* One decode step on `stream`: tokens [batch] int32 (device) in, the next
  * tokens by greedy argmax (device, may be NULL) and the logits [batch][vocab]
- * fp32 (device, may be NULL) out.  The position advances by one. */
+ * fp32 (device, may be NULL) out.  The position advances by one.  A pointer
+ * that is not device (or managed) memory is refused (hipErrorInvalidValue)
+ * before anything is launched; so is a step when the KV cache is full. */
 int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits,
                         void *stream);
 /* Current position (context + steps taken) and device bytes held. */

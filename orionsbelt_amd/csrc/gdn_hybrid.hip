@@ -683,9 +683,23 @@ extern "C" int kai_gdn_hybrid_reset(kai_gdn_hybrid *m, int batch, int context, u
     return (int)gdn::reset(m, batch, context, seed);
 }
 
+namespace {
+// Device (or managed) memory: a host pointer handed to a step would fault
+// the GPU, so it is refused before anything is launched.
+bool device_ptr(const void *p) {
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+}  // namespace
+
 extern "C" int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits,
                                    void *stream) {
-    if (!m || !tokens) return (int)hipErrorInvalidValue;
+    if (!m || !tokens || !device_ptr(tokens) || (next && !device_ptr(next)) || (logits && !device_ptr(logits)))
+        return (int)hipErrorInvalidValue;
     if (m->pos >= m->cfg.max_context) return (int)hipErrorInvalidValue;  // the KV cache is full
     return (int)gdn::step(m, tokens, next, logits, (hipStream_t)stream);
 }

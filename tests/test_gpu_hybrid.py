@@ -145,6 +145,10 @@ def test_hybrid_rejects_bad_arguments(hb, fixture):
     step(gm, [5], fields["vocab"])
     with pytest.raises(HipError):
         step(gm, [5], fields["vocab"])  # the KV cache is full
+    import ctypes
+    import orionsbelt_amd as ob
+    host_tokens = (ctypes.c_int32 * 1)(5)
+    assert ob.lib().kai_gdn_hybrid_step(gm._h, ctypes.addressof(host_tokens), None, None, None) != 0  # host memory
     with pytest.raises(HipError):
         hb.HybridModel(hb.config(**dict(fields, hidden=200)), 1)   # hidden % 256
     with pytest.raises(HipError):
