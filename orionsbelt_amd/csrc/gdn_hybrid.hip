@@ -315,9 +315,10 @@ struct kai_gdn_hybrid {
     int32_t *next = nullptr;
     uint64_t *arg_part = nullptr;  // [max_batch][kArgBlocks]
     uint32_t *arg_cnt = nullptr;   // [max_batch], zero between launches
-    uint16_t *x16 = nullptr, *act16 = nullptr, *q16 = nullptr;
+    uint16_t *x16 = nullptr, *act16 = nullptr, *q16 = nullptr, *o16 = nullptr;
     float *gemm_part = nullptr, *attn_ws = nullptr;
     uint32_t *gemm_cnt = nullptr;  // zero between launches
+    uint32_t *norm_cnt = nullptr;  // the fused add + norm's grid counter, zero between launches
     std::vector<void *> allocs;
     size_t bytes = 0, weight_bytes = 0;
     int batch = 0, pos = 0;
@@ -431,6 +432,31 @@ hipError_t gemm_to(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *y,
     return gemm(m, x, w, segments({{y, ld, w.N}}), st);
 }
 
+// Up to this many sequences, a residual branch's matrix ends with the
+// residual add and the next RMSNorm in its last block (kW8AddNorm): at
+// batch 1 that saves a 3.5 us launch per norm.  Above, one block per row
+// in a kernel of its own is faster than one block for every row.
+constexpr int kFuseNormRows = 2;
+
+// d = x W^T (the branch); h += d; x16 = fp16(rmsnorm(h) * (1 + norm_w))
+hipError_t gemm_addnorm(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *d, const float *norm_w,
+                        hipStream_t st) {
+    const int B = m->batch, H = m->cfg.hidden;
+    if (B <= kFuseNormRows && H <= 4096) {
+        W8Out o = segments({{d, H, H}});
+        o.mode = kW8AddNorm;
+        o.h = m->h;
+        o.norm_w = norm_w;
+        o.eps = m->cfg.rms_eps;
+        o.x16 = m->x16;
+        o.norm_cnt = m->norm_cnt;
+        return gemm(m, x, w, o, st);
+    }
+    TRY(gemm_to(m, x, w, d, H, st));
+    addnorm_kernel<<<B, 256, 0, st>>>(m->h, d, norm_w, m->x16, H, m->cfg.rms_eps);
+    return hipGetLastError();
+}
+
 hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
     const kai_gdn_hybrid_config &c = m->cfg;
     const int H = c.hidden, I = c.inter, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads, Hq = c.attn_q_heads,
@@ -503,6 +529,9 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         TRY(alloc_t(m, &m->arg_cnt, (size_t)Bm));
         TRY(hipMemset(m->arg_cnt, 0, (size_t)Bm * sizeof(uint32_t)));
         TRY(alloc_t(m, &m->x16, (size_t)Bm * wide16));
+        TRY(alloc_t(m, &m->o16, (size_t)Bm * wide16));
+        TRY(alloc_t(m, &m->norm_cnt, 1));
+        TRY(hipMemset(m->norm_cnt, 0, sizeof(uint32_t)));
         TRY(alloc_t(m, &m->act16, (size_t)Bm * I));
         TRY(alloc_t(m, &m->q16, (size_t)Bm * Hq * 256));
         // GEMM split-K partials and counters: the largest over the model's matrices
@@ -521,7 +550,7 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         TRY(alloc_t(m, &m->gemm_part, part));
         TRY(alloc_t(m, &m->gemm_cnt, groups));
         TRY(hipMemset(m->gemm_cnt, 0, groups * sizeof(uint32_t)));
-        TRY(alloc(m, reinterpret_cast<void **>(&m->attn_ws), attn_workspace_bytes(Bm, Hq, c.max_context)));
+        TRY(alloc(m, reinterpret_cast<void **>(&m->attn_ws), attn_workspace_bytes_tiled(Bm, Hq, c.max_context)));
         return hipDeviceSynchronize();
     };
     const hipError_t e = run();
@@ -537,9 +566,9 @@ hipError_t gdn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
                                         {m->ab, Hv, C + V + 2 * Hv}}), st));
     // conv update, gating prologue, delta rule, gated RMSNorm -> fp16: one kernel
     TRY(launch_gdn_step_fused(m->qkv, L.conv_state[m->parity], L.conv_state[m->parity ^ 1], L.conv_w, m->ab,
-                              m->bb, L.A_log, L.dt_bias, L.S, m->zb, L.norm_w, m->x16, B, Hk, Hv,
+                              m->bb, L.A_log, L.dt_bias, L.S, m->zb, L.norm_w, m->o16, B, Hk, Hv,
                               1.0f / sqrtf(128.0f), c.rms_eps, st));
-    return gemm_to(m, m->x16, L.out, m->mix, c.hidden, st);
+    return gemm_addnorm(m, m->o16, L.out, m->mix, L.ln_post, st);
 }
 
 hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
@@ -554,8 +583,8 @@ hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     TRY(hipGetLastError());
     // o * sigmoid(gate) -> fp16 in the span combine; gate = dims 256..511 of each qg head
     TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, nullptr, B, Hq, Hkv, m->tmax, m->pos + 1, 1.0f / 16.0f,
-                           m->attn_ws, st, m->qg + 256, 512, m->x16, /*k_tiled=*/true));
-    return gemm_to(m, m->x16, L.out, m->mix, c.hidden, st);
+                           m->attn_ws, st, m->qg + 256, 512, m->o16, /*k_tiled=*/true));
+    return gemm_addnorm(m, m->o16, L.out, m->mix, L.ln_post, st);
 }
 
 hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits, hipStream_t st) {
@@ -563,22 +592,21 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
     const int B = m->batch, H = c.hidden;
     embed_kernel<<<B, 256, 0, st>>>(tokens, m->embed, m->h, H, c.vocab);
     TRY(hipGetLastError());
-    const float *pending = nullptr;
     W8Out swiglu{};
     swiglu.mode = kW8SwiGLU;
     swiglu.x16 = m->act16;
-    for (Layer &L : m->layers) {
-        addnorm_kernel<<<B, 256, 0, st>>>(m->h, pending, L.ln_in, m->x16, H, c.rms_eps);
-        TRY(hipGetLastError());
-        TRY(L.attn ? attn_mixer(m, L, st) : gdn_mixer(m, L, st));
-        addnorm_kernel<<<B, 256, 0, st>>>(m->h, m->mix, L.ln_post, m->x16, H, c.rms_eps);
-        TRY(hipGetLastError());
-        TRY(gemm(m, m->x16, L.gate_up, swiglu, st));
-        TRY(gemm_to(m, m->act16, L.down, m->mlp, H, st));
-        pending = m->mlp;
-    }
-    addnorm_kernel<<<B, 256, 0, st>>>(m->h, pending, m->final_norm, m->x16, H, c.rms_eps);
+    // each residual branch's matrix (out, down) adds the branch to h and
+    // normalises h for the next matrix: the next layer's input norm, or the
+    // final norm after the last layer
+    addnorm_kernel<<<B, 256, 0, st>>>(m->h, nullptr, m->layers[0].ln_in, m->x16, H, c.rms_eps);
     TRY(hipGetLastError());
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+        Layer &L = m->layers[l];
+        TRY(L.attn ? attn_mixer(m, L, st) : gdn_mixer(m, L, st));
+        TRY(gemm(m, m->x16, L.gate_up, swiglu, st));
+        const float *next_norm = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : m->final_norm;
+        TRY(gemm_addnorm(m, m->act16, L.down, m->mlp, next_norm, st));
+    }
     float *lg = logits ? logits : m->logits;
     TRY(gemm(m, m->x16, m->lm, segments({{lg, c.vocab, c.vocab}}), st));
     argmax_kernel<<<dim3(kArgBlocks, B), 256, 0, st>>>(lg, next ? next : m->next, c.vocab, m->arg_part,

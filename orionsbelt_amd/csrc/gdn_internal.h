@@ -130,7 +130,12 @@ hipError_t launch_w8_gemm(const uint16_t *x, const int8_t *W, const float *scale
 // splits > 1, `part` holds w8f_workspace_floats(M, N, K) floats and `cnt`
 // N / 64 counters that are zero before the first launch (each launch leaves
 // them zero); launches sharing them must not overlap.
-enum W8Mode : int { kW8Segments = 0, kW8SwiGLU = 1 };
+// kW8AddNorm: y -> seg[0].dst [M][N] (a residual branch d, row stride N);
+// then the grid's last block (norm_cnt, zero between launches) updates the
+// residual stream and normalises it for the next matrix, row by row:
+//   h += d;  x16 = fp16(h * rsqrt(mean(h^2) + eps) * (1 + norm_w))
+// (N <= 4096; the rows are done by one block, so meant for small M).
+enum W8Mode : int { kW8Segments = 0, kW8SwiGLU = 1, kW8AddNorm = 2 };
 constexpr int kW8MaxSegs = 4;
 struct W8Seg {
     float *dst;
@@ -142,6 +147,10 @@ struct W8Out {
     int nseg;
     int mode;
     uint16_t *x16;
+    float *h;              // kW8AddNorm: the residual stream [M][N]
+    const float *norm_w;   // kW8AddNorm: [N]
+    float eps;
+    uint32_t *norm_cnt;    // kW8AddNorm: one counter, zero between launches
 };
 // Launch shape: waves per block (4 or 8), 64-k steps in flight per wave (1,
 // 2 or 4), k-splits across blocks (0: chosen by w8f_shape).
@@ -157,13 +166,16 @@ hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, in
 // Per-output-channel symmetric int8 quantisation of W[N][K] fp32.
 hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K, hipStream_t st);
 // Attention decode over an fp16 KV cache (head_dim 256, Hq / Hkv <= 4):
-// out [B][Hq][256] fp32; `workspace` holds attn_workspace_bytes(B, Hq, L).
+// out [B][Hq][256] fp32; `workspace` holds attn_workspace_bytes(B, Hq, L),
+// or attn_workspace_bytes_tiled(B, Hq, L) for a k_tiled launch (whose
+// spans shrink to as few as 64 positions when the grid is small).
 // With `gate` (non-null), the output is instead out16 [B][Hq][256] fp16 =
 // fp16(o * sigmoid(gate[(b * Hq + h) * gate_stride + d])).
 // k_tiled: K is stored tiled by 16 positions (Tmax % 16 == 0), element
 // (t, d) of a (sequence, kv head) at kv_tiled_offset(t, d); V stays
 // row-major.
 size_t attn_workspace_bytes(int B, int Hq, int L);
+size_t attn_workspace_bytes_tiled(int B, int Hq, int L);  // the k_tiled launches' (shorter spans allowed)
 hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
                               int B, int Hq, int Hkv, int Tmax, int L, float scaling, float *workspace,
                               hipStream_t st, const float *gate = nullptr, int gate_stride = 0,

@@ -201,7 +201,11 @@ hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, i
 //   kW8SwiGLU:   the rows are gate/up interleaved in groups of 8 (tile rows
 //                0..7 gate channels 8t..8t+7, rows 8..15 the up channels),
 //                out16[m][c] = fp16(silu(gate) * up) (Qwen3_5MLP,
-//                modeling_qwen3_5.py:704-717).
+//                modeling_qwen3_5.py:704-717);
+//   kW8AddNorm:  y into a residual branch, then the grid's last block adds
+//                it to the residual stream and applies the next RMSNorm
+//                (Qwen3_5RMSNorm, weight 1 + w) into fp16 -- the decoder
+//                layer's "h = h + branch; x = norm(h)" without a launch.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -223,6 +227,56 @@ __global__ __launch_bounds__(256) void w8f_tile_kernel(const int8_t *__restrict_
     *reinterpret_cast<uint4 *>(dst + q * 16) = *reinterpret_cast<const uint4 *>(src + n * K + k);
 }
 
+// kW8AddNorm's last block, 256 threads: row b of d (written in this launch
+// by other blocks, so read through sc1), h and x16 as W8Out describes.
+__device__ void w8f_addnorm_rows(const W8Out &out, int M, int N, float *s_ss) {
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(out.seg[0].dst, 0, 0x7FFFFFFF, kBufFlags);
+    const int n4 = N / 4, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int b = 0; b < M; ++b) {
+        f32x4_t x[4], dv[4];
+        float4 *hr = reinterpret_cast<float4 *>(out.h + (size_t)b * N);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            if (i < n4) {
+                dv[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, (b * N + 4 * i) * 4,
+                                                                                          0, kSc1));
+                const float4 hv = hr[i];
+                x[j] = f32x4_t{hv.x, hv.y, hv.z, hv.w};
+            }
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            if (i < n4) {
+                x[j] += dv[j];
+                hr[i] = make_float4(x[j][0], x[j][1], x[j][2], x[j][3]);
+                ss += x[j][0] * x[j][0] + x[j][1] * x[j][1] + x[j][2] * x[j][2] + x[j][3] * x[j][3];
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) s_ss[wave] = ss;
+        __syncthreads();
+        const float inv = 1.0f / sqrtf((((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3]) / (float)N + out.eps);
+        __syncthreads();  // s_ss is rewritten by the next row
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            if (i < n4) {
+                const float4 wv = reinterpret_cast<const float4 *>(out.norm_w)[i];
+                uint2 o;
+                o.x = (uint32_t)f32_to_f16_rne(x[j][0] * inv * (1.0f + wv.x)) |
+                      ((uint32_t)f32_to_f16_rne(x[j][1] * inv * (1.0f + wv.y)) << 16);
+                o.y = (uint32_t)f32_to_f16_rne(x[j][2] * inv * (1.0f + wv.z)) |
+                      ((uint32_t)f32_to_f16_rne(x[j][3] * inv * (1.0f + wv.w)) << 16);
+                reinterpret_cast<uint2 *>(out.x16 + (size_t)b * N)[i] = o;
+            }
+        }
+    }
+}
+
 template <int WAVES, int DEPTH>
 __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restrict__ x,
                                                          const int8_t *__restrict__ W,
@@ -230,6 +284,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
                                                          int kblk, int S, float *__restrict__ part,
                                                          uint32_t *__restrict__ cnt, W8Out out) {
     __shared__ f32x4_t red[WAVES][4][64];
+    __shared__ float s_ss[4];
     __shared__ bool last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, r = lane & 15;
@@ -330,6 +385,14 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
             const int cc = (n0 + 16 * j) / 2 + 4 * g;
             *reinterpret_cast<uint2 *>(out.x16 + (size_t)r * (N / 2) + cc) = make_uint2(h[0], h[1]);
         }
+    } else if (out.mode == kW8AddNorm) {
+        const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(out.seg[0].dst, 0, 0x7FFFFFFF, kBufFlags);
+        if (row_ok) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), rd, (r * N + n) * 4, 0, kSc1);
+        stores_done();
+        __syncthreads();
+        if (threadIdx.x == 0) last = arrive_last(out.norm_cnt, gridDim.x);
+        __syncthreads();
+        if (last) w8f_addnorm_rows(out, M, N, s_ss);
     } else if (row_ok && n < out.seg[out.nseg - 1].n_end) {  // channels past the last segment: padding
         int sgi = 0, nb = 0;
 #pragma unroll
@@ -387,6 +450,10 @@ hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, in
     const int S = sh.splits;
     if (M > 16 || N % kW8fGroup != 0 || K % (S * sh.waves * sh.depth * kKStep) != 0) return hipErrorInvalidValue;
     if (S > 1 && (!part || !cnt || (size_t)S * M * N * 4 > 0x7FFFFFFFull)) return hipErrorInvalidValue;
+    if (out.mode == kW8AddNorm &&
+        (N > 4096 || out.nseg != 1 || out.seg[0].ld != N || !out.seg[0].dst || !out.h || !out.norm_w ||
+         !out.x16 || !out.norm_cnt))
+        return hipErrorInvalidValue;
     const dim3 grid(N / kW8fGroup, S);
 #define W8F_CASE(WV, DP)                                                                                  \
     if (sh.waves == WV && sh.depth == DP) {                                                                \
@@ -433,7 +500,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__rest
                                                           const uint16_t *__restrict__ Kc,
                                                           const uint16_t *__restrict__ Vc,
                                                           float *__restrict__ part, int Hq, int Hkv,
-                                                          int Tmax, int L, int nspan, float sc_log2) {
+                                                          int Tmax, int L, int nspan, int G, float sc_log2) {
     __shared__ float s_m[4][kAttRepMax], s_l[4][kAttRepMax];
     __shared__ float s_o[4][kAttRepMax][kAttD];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -458,10 +525,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__rest
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[h][i] = 0.f;
     }
-    // Groups of 16 positions, double-buffered: the K rows and V rows of
-    // group n + 1 are in flight while group n is scored and accumulated.
-    // Rows past L are clamped to L - 1 (in bounds; masked by p = 0).
-    const int t_begin = span * kAttSpan + wave * 64;
+    // Each wave takes G groups of 16 positions (the span is 64 G),
+    // double-buffered: the K rows and V rows of the next group are in
+    // flight while a group is scored and accumulated.  Rows past L are
+    // clamped to L - 1 (in bounds; masked by p = 0).
+    const int t_begin = span * (64 * G) + wave * (16 * G);
+    const int t_end = min(t_begin + 16 * G, L);
     u32x4_t kbuf[2][8];
     u32x2_t vbuf[2][16];
     auto load_group = [&](int t0, u32x4_t (&kb)[8], u32x2_t (&vb)[16]) {
@@ -482,14 +551,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__rest
             vb[i] = __builtin_nontemporal_load(
                 reinterpret_cast<const u32x2_t *>(Vc + (kvrow + min(t0 + i, L - 1)) * kAttD + 4 * lane));
     };
-    if (t_begin < L) load_group(t_begin, kbuf[0], vbuf[0]);
-#pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-        const int t0 = t_begin + 16 * grp;
-        if (t0 >= L) break;  // uniform over the wave
-        if (grp < 3 && t0 + 16 < L) load_group(t0 + 16, kbuf[(grp + 1) & 1], vbuf[(grp + 1) & 1]);
-        const u32x4_t(&kb)[8] = kbuf[grp & 1];
-        const u32x2_t(&vb)[16] = vbuf[grp & 1];
+    auto process = [&](const u32x4_t (&kb)[8], const u32x2_t (&vb)[16], int t0) {
         f32x4_t acc = zero4();
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -545,6 +607,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t *__rest
                     for (int i = 0; i < 4; ++i) o[h][i] += ph * v[i];
                 }
             }
+    };
+    if (t_begin < t_end) load_group(t_begin, kbuf[0], vbuf[0]);
+    for (int t0 = t_begin; t0 < t_end; t0 += 32) {  // uniform over the wave
+        const int t1 = t0 + 16;
+        if (t1 < t_end) load_group(t1, kbuf[1], vbuf[1]);
+        process(kbuf[0], vbuf[0], t0);
+        if (t1 >= t_end) break;
+        if (t1 + 16 < t_end) load_group(t1 + 16, kbuf[0], vbuf[0]);
+        process(kbuf[1], vbuf[1], t1);
     }
     // merge the four waves (each may have seen no position: m = -inf, l = 0)
     if (lane == 0)
@@ -641,19 +712,37 @@ size_t attn_workspace_bytes(int B, int Hq, int L) {
     return (size_t)B * Hq * nspan * kAttPart * sizeof(float);
 }
 
+// Groups of 16 positions per wave.  256-position spans (G = 4), unless that
+// grid is small (under 2048 blocks) for a tiled-K cache: then the span is
+// sized so that the blocks fill 512 slots (2 per CU on 256 CUs) in one round
+// -- at B = 1 and 32K, 129 x 4 = 516 blocks of 256 positions would leave 4
+// blocks for a second round that doubles the kernel's time.
+int attn_groups(int B, int Hkv, int L, bool k_tiled) {
+    const long blocks256 = (long)B * Hkv * ((L + kAttSpan - 1) / kAttSpan);
+    if (!k_tiled || blocks256 >= 2048) return 4;
+    const int per_kv = max(1, 512 / (B * Hkv));
+    return max(1, (L + 64 * per_kv - 1) / (64 * per_kv));
+}
+
+size_t attn_workspace_bytes_tiled(int B, int Hq, int L) {
+    const int nspan = (L + 63) / 64;  // enough for any span of a whole number of 64 positions
+    return (size_t)B * Hq * nspan * kAttPart * sizeof(float);
+}
+
 hipError_t launch_attn_decode(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
                               int B, int Hq, int Hkv, int Tmax, int L, float scaling, float *workspace,
                               hipStream_t st, const float *gate, int gate_stride, uint16_t *out16, bool k_tiled) {
     if (B == 0) return hipSuccess;
     if (k_tiled && Tmax % 16 != 0) return hipErrorInvalidValue;
-    const int nspan = (L + kAttSpan - 1) / kAttSpan;
+    const int G = attn_groups(B, Hkv, L, k_tiled);
+    const int nspan = (L + 64 * G - 1) / (64 * G);
     const float sc_log2 = scaling * 1.4426950408889634f;
     if (k_tiled)
         attn_decode_kernel<true><<<dim3(nspan, Hkv, B), 256, 0, st>>>(q, Kc, Vc, workspace, Hq, Hkv, Tmax, L, nspan,
-                                                                      sc_log2);
+                                                                      G, sc_log2);
     else
         attn_decode_kernel<false><<<dim3(nspan, Hkv, B), 256, 0, st>>>(q, Kc, Vc, workspace, Hq, Hkv, Tmax, L,
-                                                                       nspan, sc_log2);
+                                                                       nspan, G, sc_log2);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     attn_combine_kernel<<<dim3(B * Hq), kAttD, 0, st>>>(workspace, out, gate, gate_stride, out16, nspan);

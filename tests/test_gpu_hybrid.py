@@ -230,3 +230,25 @@ def test_hybrid_real_head_counts_vs_oracle(hb, fixture):
         _, olg = om.step(tok)
         assert_close(lg, olg, f"4B heads step {t}")
         assert_greedy(nxt, lg, olg)
+
+
+def test_hybrid_long_context_span_sizes_vs_oracle(hb, fixture):
+    """Small attention grids size their spans to fill the GPU in one round
+    (16 G positions per wave): batch 4 with 4 kv heads after drawn contexts
+    of 3000 (G = 2) and 5000 positions (G = 3, an odd count of groups), and
+    batch 1 at 5000 (G = 1 on 128-way span splits) -- logits against the
+    CPU model."""
+    d, fields = fixture
+    over = dict(layers=4, hidden=512, inter=1024, vocab=2048, gdn_k_heads=16, gdn_v_heads=32, attn_q_heads=16,
+                attn_kv_heads=4, max_batch=4, max_context=5010)
+    gm, om = models(hb, fields, 515, **over)
+    rs = np.random.RandomState(5)
+    for batch, ctx in ((4, 3000), (4, 5000), (1, 5000)):
+        gm.reset(batch, ctx, 3)
+        om.reset(batch, ctx, 3)
+        for t in range(2):
+            tok = rs.randint(0, over["vocab"], batch)
+            nxt, lg = step(gm, tok, over["vocab"])
+            _, olg = om.step(tok)
+            assert_close(lg, olg, f"batch {batch} context {ctx} step {t}")
+            assert_greedy(nxt, lg, olg)
