@@ -259,7 +259,9 @@ __device__ void w8f_addnorm_rows(const W8Out &out, int M, int N, float *s_ss) {
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
         if (lane == 0) s_ss[wave] = ss;
         __syncthreads();
-        const float inv = 1.0f / sqrtf((((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3]) / (float)N + out.eps);
+        // the wave sums in the pairing of the hybrid model's addnorm kernel,
+        // so both paths give bit-identical rows
+        const float inv = 1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)N + out.eps);
         __syncthreads();  // s_ss is rewritten by the next row
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

@@ -252,3 +252,21 @@ def test_hybrid_long_context_span_sizes_vs_oracle(hb, fixture):
             _, olg = om.step(tok)
             assert_close(lg, olg, f"batch {batch} context {ctx} step {t}")
             assert_greedy(nxt, lg, olg)
+
+
+def test_hybrid_fused_and_separate_norms_agree(hb, fixture):
+    """Up to batch 2 the residual add and RMSNorm run in the last block of
+    the out and down matrices; from batch 3 in a kernel of their own, with
+    the same arithmetic in the same order.  The same two sequences stepped
+    at batch 2 and (with a third) at batch 3 give bit-identical logits and
+    greedy tokens."""
+    d, fields = fixture
+    gm, _ = models(hb, fields, int(d["seed"]), max_batch=3)
+    tokens = d["tokens"]
+    gm.reset(2, 0, 0)
+    two = [step(gm, tokens[:, t], fields["vocab"]) for t in range(6)]
+    gm.reset(3, 0, 0)
+    three = [step(gm, np.concatenate([tokens[:, t], tokens[:1, t]]), fields["vocab"]) for t in range(6)]
+    for t, ((n2, l2), (n3, l3)) in enumerate(zip(two, three)):
+        assert np.array_equal(l3[:2], l2), f"step {t}"
+        assert np.array_equal(n3[:2], n2), f"step {t}"
