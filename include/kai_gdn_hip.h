@@ -30,6 +30,22 @@ extern "C" {
 int kai_run_gdn_cumdecay_f32_hip(const float *a, float *decay, size_t seq,
                                  size_t channels, void *stream);
 
+/* No counterpart in the reference.  kai_run_gdn_cumdecay_f32_hip without any
+ * allocation, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops): the look-back scan's scratch is a
+ * fixed array in the library's device code (about 6 MiB per GPU, held until
+ * the process ends) instead of memory allocated on first use.  It covers
+ * ceil(seq / 128) * channels <= KAI_GDN_NOALLOC_SCAN_MAX_WORDS (for example
+ * seq = 4096, channels = 8192); larger shapes return hipErrorInvalidValue
+ * without writing anything.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU race, so order them (one stream, or
+ * synchronise between streams).  A timed-out look-back wait is reported by
+ * kai_gdn_hip_check_device_error().  The first call on a device (or
+ * kai_gdn_hip_init on it) sets the scratch up and synchronises the device. */
+#define KAI_GDN_NOALLOC_SCAN_MAX_WORDS 262144
+int kai_run_gdn_cumdecay_f32_noalloc_hip(const float *a, float *decay, size_t seq,
+                                         size_t channels, void *stream);
+
 /* Replaces kai_run_gdn_gated_scan_f32_sve (kai_gdn_gated_scan_f32_sve.h:35-36). */
 int kai_run_gdn_gated_scan_f32_hip(const float *g, const float *x, float *s,
                                    float *state, size_t seq, size_t channels,

@@ -24,6 +24,7 @@ KAI_SYMBOLS = (
 )
 HIP_SYMBOLS = (
     "kai_run_gdn_cumdecay_f32_hip",
+    "kai_run_gdn_cumdecay_f32_noalloc_hip",
     "kai_run_gdn_gated_scan_f32_hip",
     "kai_run_gdn_causal_dwconv1d_f32_k4_hip",
     "kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip",
@@ -94,6 +95,7 @@ _SIGS = {
     "kai_run_gdn_causal_dwconv1d_f32_k4_sve": (None, [_vp, _vp, _vp, _vp, _sz, _sz]),
     "kai_run_gdn_gemv_f32_f32_f32_1x4_neon": (None, [_vp, _vp, _vp, _sz, _sz]),
     "kai_run_gdn_cumdecay_f32_hip": (_i, [_vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_cumdecay_f32_noalloc_hip": (_i, [_vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_cumdecay_f16_hip": (_i, [_vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_cumdecay_bf16_hip": (_i, [_vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_gated_scan_f32_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),

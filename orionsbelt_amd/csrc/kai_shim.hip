@@ -182,6 +182,74 @@ hipError_t run_scan(int mode, int narrow, const float *g, const float *x, void *
     return hipSuccess;
 }
 
+// ---- cumulative decay without allocation -----------------------------------
+// The look-back scan's scratch for kai_run_gdn_cumdecay_f32_noalloc_hip lives
+// in a file-scope device array of fixed size instead of hipMalloc'd memory:
+// words [0, kNaHeader) hold the tile counter (word 0) and the error word
+// (word 8), then three status arrays of kNaStatusWords words each.  Each GPU
+// holds its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, never device memory: every host use goes through the
+// per-device address from hipGetSymbolAddress (NaDev::ptr).
+constexpr size_t kNaStatusWords = KAI_GDN_NOALLOC_SCAN_MAX_WORDS;
+constexpr size_t kNaHeader = 64;
+constexpr size_t kNaWords = kNaHeader + 3 * kNaStatusWords;
+static __device__ __align__(256) unsigned long long scratch[kNaWords];
+
+// Zero `n` 64-bit words (a kernel, not hipMemsetAsync: callers of the
+// no-allocation entry point may capture it into a graph).
+__global__ void na_zero_kernel(unsigned long long *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0ull;
+}
+
+struct NaDev {
+    std::mutex mu;
+    bool ready = false;
+    unsigned long long *ptr = nullptr;   // device address of this GPU's `scratch`
+    int cu_count = 0;
+    uint32_t epoch = 0;                  // tag of the last launch's status words
+    unsigned long long counter = 0;      // value of the tile counter after the last launch
+};
+constexpr int kNaMaxDevices = 64;
+NaDev g_na[kNaMaxDevices];
+
+// Per-device set-up, once, with the device current: the array's address and
+// its contents cleared.  No allocation (hipGetSymbolAddress, a kernel launch
+// and a device synchronisation).
+hipError_t na_dev(NaDev **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kNaMaxDevices) return hipErrorInvalidDevice;
+    NaDev *d = &g_na[dev];
+    std::lock_guard<std::mutex> lk(d->mu);
+    if (!d->ready) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        e = hipDeviceGetAttribute(&d->cu_count, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        na_zero_kernel<<<256, 256, 0, nullptr>>>(static_cast<unsigned long long *>(p), kNaWords);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) return e;
+        d->ptr = static_cast<unsigned long long *>(p);
+        d->epoch = 0;
+        d->counter = 0;
+        d->ready = true;
+    }
+    *out = d;
+    return hipSuccess;
+}
+
+// The device's no-allocation error word, or nullptr before its set-up.
+uint32_t *na_err_word(int dev) {
+    if (dev < 0 || dev >= kNaMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_na[dev].mu);
+    return g_na[dev].ready ? reinterpret_cast<uint32_t *>(g_na[dev].ptr + 8) : nullptr;
+}
+
 // ---- synchronous (kai) path helpers ----------------------------------------
 
 bool is_device_ptr(const void *p) {
@@ -262,7 +330,10 @@ bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 extern "C" int kai_gdn_hip_init(void) {
     DeviceCtx *c;
-    return (int)get_ctx(&c);
+    hipError_t e = get_ctx(&c);
+    if (e != hipSuccess) return (int)e;
+    NaDev *d;
+    return (int)na_dev(&d);
 }
 
 extern "C" const char *kai_gdn_hip_error_string(int code) {
@@ -276,6 +347,14 @@ extern "C" int kai_gdn_hip_check_device_error(void) {
     uint32_t v = 0;
     if (hipMemcpy(&v, c->scan.err, sizeof v, hipMemcpyDeviceToHost) != hipSuccess) return -1;
     if (v) (void)hipMemset(c->scan.err, 0, sizeof v);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    if (uint32_t *na = na_err_word(dev)) {  // the no-allocation scan's error word
+        uint32_t w = 0;
+        if (hipMemcpy(&w, na, sizeof w, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+        if (w) (void)hipMemset(na, 0, sizeof w);
+        v |= w;
+    }
     return (int)v;
 }
 
@@ -327,6 +406,43 @@ extern "C" int kai_run_gdn_cumdecay_bf16_hip(const float *a, uint16_t *decay, si
                                              size_t channels, void *stream) {
     return (int)run_scan(0, gdn::kBF16, a, nullptr, decay, nullptr, seq, channels,
                          (hipStream_t)stream);
+}
+
+extern "C" int kai_run_gdn_cumdecay_f32_noalloc_hip(const float *a, float *decay, size_t seq,
+                                                    size_t channels, void *stream) {
+    if (seq == 0 || channels == 0) return 0;
+    if (!a || !decay) return (int)hipErrorInvalidValue;
+    // beyond the fixed scratch: one status word per (row tile, channel)
+    const size_t nr = gdn::scan_row_tiles(seq, 0);
+    if (channels > kNaStatusWords || nr > kNaStatusWords / channels) return (int)hipErrorInvalidValue;
+    NaDev *d;
+    hipError_t e = na_dev(&d);
+    if (e != hipSuccess) return (int)e;
+    const hipStream_t st = (hipStream_t)stream;
+    std::lock_guard<std::mutex> lk(d->mu);
+    unsigned long long *hdr = d->ptr;
+    unsigned long long *incl = hdr + kNaHeader;
+    if (d->epoch == 0xFFFFFFFFu) {  // tag space exhausted: clear the status words, restart tags
+        na_zero_kernel<<<1024, 256, 0, st>>>(incl, 3 * kNaStatusWords);
+        if ((e = hipGetLastError()) != hipSuccess) return (int)e;
+        d->epoch = 0;
+    }
+    gdn::ScanScratch s{};
+    s.counter = hdr;
+    s.err = reinterpret_cast<uint32_t *>(hdr + 8);
+    s.incl = incl;
+    s.aggG = incl + kNaStatusWords;
+    s.aggX = incl + 2 * kNaStatusWords;
+    s.words = kNaStatusWords;
+    s.cu_count = d->cu_count;
+    const uint32_t epoch = d->epoch + 1;
+    unsigned long long used = 0;
+    e = gdn::launch_lookback_scan(0, gdn::kF32, a, nullptr, decay, nullptr, seq, channels, s, d->counter,
+                                  epoch, &used, st);
+    if (e != hipSuccess) return (int)e;
+    d->epoch = epoch;
+    d->counter += used;
+    return 0;
 }
 
 extern "C" int kai_run_gdn_gated_scan_f32_hip(const float *g, const float *x, float *s,
