@@ -26,7 +26,12 @@ extern "C" {
 /* ---- kai ukernels, device pointers -------------------------------------- */
 
 /* Replaces kai_run_gdn_cumdecay_f32_sve
- * (kleidiai_submission/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.h:33-34). */
+ * (kleidiai_submission/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.h:33-34).
+ * The cumulative decay and gated scan entry points below run a single-pass
+ * look-back scan whose waits are bounded: a wait that gives up marks that
+ * launch's output invalid and sets a device error word, which the caller
+ * reads with kai_gdn_hip_check_device_error() (the synchronous kai symbols
+ * check it themselves and exit(1)). */
 int kai_run_gdn_cumdecay_f32_hip(const float *a, float *decay, size_t seq,
                                  size_t channels, void *stream);
 

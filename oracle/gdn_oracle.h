@@ -60,7 +60,7 @@ extern "C" {
 /* ---- kai ukernels, portable scalar branch ------------------------------ */
 
 /* decay[t][c] = prod_{i<=t} a[i][c]; running product starts at 1.0f.
- * kleidiai_submission/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.c:122-129 */
+ * kleidiai_submission/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.c:82-90 */
 void orc_cumdecay_f32(const float *a, float *decay, size_t seq, size_t channels);
 
 /* acc = x + acc*g per channel, state in/out.

@@ -619,6 +619,9 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
 
 hipError_t reset(kai_gdn_hybrid *m, int batch, int context, uint64_t seed) {
     const kai_gdn_hybrid_config &c = m->cfg;
+    // a step may still run on any stream the caller used: the fills below
+    // (null stream) overwrite the states and caches it reads
+    TRY(hipDeviceSynchronize());
     m->batch = batch;
     m->pos = context;
     m->parity = 0;

@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void conv_k4_kernel(const float *__restrict__ 
 // ---------------------------------------------------------------------------
 // Recurrence per channel: s_t = g_t * s_{t-1} + x_t (mode 1, the kai gated
 // scan, kai_gdn_gated_scan_f32_sve.c:86-95) or s_t = s_{t-1} * a_t from
-// s_{-1} = 1 (mode 0, kai cumdecay, kai_gdn_cumdecay_f32_sve.c:122-129).
+// s_{-1} = 1 (mode 0, kai cumdecay, kai_gdn_cumdecay_f32_sve.c:82-90).
 //
 // A tile is RH * TS rows x 256 channels, held in registers by a workgroup of
 // RH row groups x 256 threads: thread (row group q, lane l) owns channel l

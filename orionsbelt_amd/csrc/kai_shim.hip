@@ -304,10 +304,19 @@ void finish(DeviceCtx *c, Arg *args, int n) {
 }
 
 // After a synchronous call has drained the internal stream: a scan launched
-// there has ended.
+// there has ended.  A look-back wait that gave up leaves the error word set
+// and the output invalid; the synchronous symbols have no error channel, so
+// that is fatal here (the reference's convention, test_kai_gdn.c:38-42).
 void scan_settled(DeviceCtx *c) {
     std::lock_guard<std::mutex> lk(c->mu);
     if (c->scan_stream == c->stream) c->scan_pending = false;
+    uint32_t err = 0;
+    check(hipMemcpy(&err, c->scan.err, sizeof err, hipMemcpyDeviceToHost), "hipMemcpy (scan error word)");
+    if (err) {
+        (void)hipMemset(c->scan.err, 0, sizeof err);
+        std::fprintf(stderr, "libkai_gdn_hip: a scan's look-back wait timed out (error word %u)\n", err);
+        std::exit(1);
+    }
 }
 
 DeviceCtx *sync_ctx() {
