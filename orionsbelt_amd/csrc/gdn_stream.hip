@@ -6,6 +6,8 @@
 // All layouts are the reference kai layouts: [seq][channels] row-major with
 // channels contiguous, so a wavefront reading one row of 64 channels issues
 // one contiguous 256 B (or 1 KiB with float4) request.
+#include <type_traits>
+
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -234,8 +236,14 @@ __global__ __launch_bounds__(kScanThreads *RH) void lookback_scan_kernel(
     unsigned long long counter_base, uint32_t epoch, uint32_t *err) {
 #pragma clang fp contract(off)
     constexpr int TT = TS * RH;
+    // The multiplicative maps of the cumulative decay (a tile's product, the
+    // carry composed during the look-back and the inclusive value published
+    // for the next tile) are carried in fp64 and rounded once each; the
+    // values inside a tile keep the reference's fp32 order.
+    using Map = std::conditional_t<MODE == 0, double, float>;
     __shared__ long long s_tile[2];
-    __shared__ float s_ag[RH][kScanThreads];
+    __shared__ Map s_ag[RH][kScanThreads];
+    __shared__ Map s_incl[MODE == 0 ? kScanThreads : 1];
     __shared__ float s_ax[RH][kScanThreads];
     __shared__ float s_carry[RH][kScanThreads];
     const long long n_tiles = (long long)n_row_tiles * n_col_tiles;
@@ -274,12 +282,13 @@ __global__ __launch_bounds__(kScanThreads *RH) void lookback_scan_kernel(
 
         // 1. this row group's map, identity start, reference order
         {
-            float AG = 1.0f, AX = 0.0f;
+            Map AG = 1.0f;
+            float AX = 0.0f;
 #pragma unroll
             for (int i = 0; i < TS; ++i) {
                 if (i < nrows) {
                     if constexpr (MODE == 1) AX = xv[i] + AX * gv[i];
-                    AG = AG * gv[i];
+                    AG = AG * (Map)gv[i];
                 }
             }
             s_ag[sub][lc] = AG;
@@ -297,22 +306,26 @@ __global__ __launch_bounds__(kScanThreads *RH) void lookback_scan_kernel(
 
         if (sub == 0) {
             float carry = 0.f;
+            Map carry_m = 0.f;
+            // the tile's map: row-group maps composed in row order
+            Map AG = s_ag[0][lc];
+            float AX = (MODE == 1) ? s_ax[0][lc] : 0.f;
+#pragma unroll
+            for (int q = 1; q < RH; ++q) {
+                if constexpr (MODE == 1) AX = s_ax[q][lc] + AX * s_ag[q][lc];
+                AG = AG * s_ag[q][lc];
+            }
             if (r == 0) {
                 if (live) carry = (MODE == 0) ? 1.0f : narrow_load<NARROW>(state, c);
+                carry_m = 1.0f;
             } else if (live) {
-                // the tile's map: row-group maps composed in row order
-                float AG = s_ag[0][lc], AX = (MODE == 1) ? s_ax[0][lc] : 0.f;
-#pragma unroll
-                for (int q = 1; q < RH; ++q) {
-                    if constexpr (MODE == 1) AX = s_ax[q][lc] + AX * s_ag[q][lc];
-                    AG = AG * s_ag[q][lc];
-                }
                 // 2. publish it
                 const int64_t me = (int64_t)r * ch + c;
-                store_status(aggG + me, pack_status(epoch, AG));
+                store_status(aggG + me, pack_status(epoch, (float)AG));
                 if constexpr (MODE == 1) store_status(aggX + me, pack_status(epoch, AX));
                 // 3. look back
-                float GA = 1.0f, XA = 0.0f;
+                Map GA = 1.0f;
+                float XA = 0.0f;
                 int p = r - 1;
                 uint32_t spins = 0;
                 for (;;) {
@@ -320,14 +333,19 @@ __global__ __launch_bounds__(kScanThreads *RH) void lookback_scan_kernel(
                     const unsigned long long wi = load_status(incl + at);
                     if (status_tag(wi) == epoch) {
                         const float sp = status_val(wi);
-                        carry = (MODE == 0) ? GA * sp : GA * sp + XA;
+                        if constexpr (MODE == 0) {
+                            carry_m = GA * (Map)sp;
+                            carry = (float)carry_m;
+                        } else {
+                            carry = GA * sp + XA;
+                        }
                         break;
                     }
                     const unsigned long long wg = load_status(aggG + at);
                     const unsigned long long wx = (MODE == 1) ? load_status(aggX + at) : wg;
                     if (p > 0 && status_tag(wg) == epoch && status_tag(wx) == epoch) {
                         if constexpr (MODE == 1) XA = GA * status_val(wx) + XA;
-                        GA = GA * status_val(wg);
+                        GA = GA * (Map)status_val(wg);
                         --p;
                         spins = 0;
                         continue;
@@ -341,6 +359,7 @@ __global__ __launch_bounds__(kScanThreads *RH) void lookback_scan_kernel(
                 }
             }
             s_carry[0][lc] = carry;
+            if constexpr (MODE == 0) s_incl[lc] = carry_m * AG;  // this tile's inclusive value
         }
 
         // 4. the reference recurrence from the carry, row group by row group
@@ -366,8 +385,11 @@ __global__ __launch_bounds__(kScanThreads *RH) void lookback_scan_kernel(
             }
         }
         if (live && sub == RH - 1) {
-            if (r + 1 < n_row_tiles)
-                store_status(incl + (int64_t)r * ch + c, pack_status(epoch, run));
+            if (r + 1 < n_row_tiles) {
+                float iv = run;
+                if constexpr (MODE == 0) iv = (float)s_incl[lc];
+                store_status(incl + (int64_t)r * ch + c, pack_status(epoch, iv));
+            }
             if constexpr (MODE == 1)
                 if (r == n_row_tiles - 1) narrow_store<NARROW>(state, c, run);
         }

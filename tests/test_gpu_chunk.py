@@ -1,16 +1,26 @@
 """GPU parity of the chunkwise (WY) prefill against the oracle's restatement
 of HF torch_chunk_gated_delta_rule (fp32), through the C-ABI.
 
-The kernel feeds bf16 operands to MFMA (q/k/v are bf16 inputs; T, W, the
-bf16 copy of S, v_new and the gated q/k are rounded to bf16 once each) and
-accumulates in fp32; the state stays fp32.  Stated bound, relative to the
-largest reference magnitude of the compared tensor:
-    max |got - ref| / max |ref|      <= 2e-2
-    ||got - ref||_2 / ||ref||_2      <= 1e-2
-for outputs and final state, scaled by 1.5^log2(T/4096) above T = 4096
-(docs/CORRECTNESS_TOLERANCES.md:34-49).  Long sequences are cut into
-segments that run in parallel (their results depend on the cut, within the
-bound); calls split inside one segment are checked bit for bit.
+The kernel feeds bf16 operands to MFMA (q/k/v are bf16 inputs; T - I, the
+bf16 copy of S, v_new and A are rounded to bf16 once each; R enters as a
+bf16 hi + lo pair) and accumulates in fp32; the state stays fp32 and the
+output is stored in bf16.  Bounds, relative to the largest reference
+magnitude (max) and as a relative 2-norm (l2):
+    output  max <= 1.0e-2   l2 <= 5.0e-3
+    state   max <= 5.0e-3   l2 <= 3.0e-3
+Measured on MI355X for every case below, T = 1 .. 16384 (all 32 value
+heads at T = 16384, fp32 and fp16 state alike): output max 3.9e-3 .. 7.9e-3,
+l2 2.9e-3 .. 3.1e-3; state max 1.4e-3 .. 3.3e-3, l2 1.5e-3 .. 1.9e-3.  The
+fp32 oracle is itself within 1.5e-6 of the fp64 restatement, so these are the
+kernel's bf16 roundings.  The bounds are at most 2x the worst measured value
+and at the reference's bf16 bound after two chunks, 1e-2
+(test_gdn_mixed.c:150-153,176-194); the error does not grow with T (the
+gates bound it), so no drift factor is applied (the reference's rule,
+docs/CORRECTNESS_TOLERANCES.md:34-49, would allow 1.5x at 8K and 2.25x at
+16K).  The rank-1 repeated-key chunks have their own, stated bound.  Long
+sequences are cut into segments that run in parallel (their results depend
+on the cut, within the bound); calls split inside one segment are checked
+bit for bit.  Every check prints the measured errors (pytest -s).
 """
 import math
 
@@ -23,11 +33,7 @@ from tests.gpu_util import P, dev, empty, host, host_u16, stream, torch_mod
 
 pytestmark = pytest.mark.gpu
 
-MAX_REL, L2_REL = 2e-2, 1e-2
-
-
-def drift(T):
-    return max(1.0, 1.5 ** math.log2(T / 4096)) if T > 4096 else 1.0
+BOUNDS = {"output": (1.0e-2, 5.0e-3), "state": (5.0e-3, 3.0e-3)}
 
 
 @pytest.fixture(scope="module")
@@ -74,9 +80,13 @@ def gpu_prefill(L, q, k, v, g, beta, S, f16=False, calls=None):
 
 
 def check(got, ref, T, label):
+    """`label` starts with "output" or "state" (or names them after a
+    prefix): that tensor's bound applies."""
+    kind = "state" if "state" in label else "output"
     mx, l2 = rel_errors(got, ref)
-    f = drift(T)
-    assert mx <= MAX_REL * f and l2 <= L2_REL * f, f"{label}: max_rel {mx:.3e} l2_rel {l2:.3e}"
+    bmx, bl2 = BOUNDS[kind]
+    print(f"{label} (T={T}): max_rel {mx:.3e} l2_rel {l2:.3e}", flush=True)
+    assert mx <= bmx and l2 <= bl2, f"{label}: max_rel {mx:.3e} l2_rel {l2:.3e} (bound {bmx:.1e} / {bl2:.1e})"
     return mx, l2
 
 
@@ -163,8 +173,9 @@ def test_prefill_repeated_keys(L):
     hi + lo pair), and the diagonal blocks of T must be exact enough to
     cancel (fp32 substitution).  Rank-1 keys also amplify the bf16 rounding
     of T's off-diagonal blocks and of v_new, so the bound here is looser than
-    the generic one: max_rel <= 4e-2 and l2_rel <= 3e-2 (measured about
-    2e-2)."""
+    the generic one: max_rel <= 4e-2 and l2_rel <= 3.5e-2 (measured: output
+    1.9e-2 / 1.6e-2, state 2.7e-2 / 2.5e-2 at beta = 1; 1.7e-2 / 1.8e-2 at
+    beta = 0.9)."""
     for beta_v, g_v in [(1.0, 0.0), (0.9, -0.01)]:
         q, k, v, g, beta, S = prefill_inputs(41, 1, 256, 2, 1)
         k[:, :] = k[:, :1]
@@ -174,7 +185,8 @@ def test_prefill_repeated_keys(L):
         o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, 256, 2, 1, 128, 128, 64)
         for got, ref, what in [(o, o_ref, "output"), (Sg, S_ref, "state")]:
             mx, l2 = rel_errors(got, ref)
-            assert mx <= 4e-2 and l2 <= 3e-2, f"beta={beta_v} {what}: max_rel {mx:.3e} l2_rel {l2:.3e}"
+            print(f"repeated keys beta={beta_v} {what}: max_rel {mx:.3e} l2_rel {l2:.3e}", flush=True)
+            assert mx <= 4e-2 and l2 <= 3.5e-2, f"beta={beta_v} {what}: max_rel {mx:.3e} l2_rel {l2:.3e}"
 
 
 def test_prefill_split_calls_bit_identical(L):
@@ -216,27 +228,103 @@ def test_prefill_f16_state(L):
     check(Sg, S_ref, 300, "state (fp16)")
 
 
-def test_prefill_long_sequence_properties(L):
-    """T = 16K at the config-3 head shape: finite, one call agrees with two
-    calls split at a chunk boundary (each call cuts its own sequence into
-    segments, so the agreement is to the stated bound, not bit for bit), and
-    the value heads of the last key head agree with the oracle over the whole
-    sequence."""
+def test_prefill_config3_all_heads(L):
+    """Config 3 (B=1, T=16384, Hv=32, Hk=16, chunk 64, bf16 q/k/v, fp32
+    state): every value head against the oracle over the whole sequence,
+    then the properties: finite, and one call agrees with two calls split at
+    a chunk boundary (each call cuts its own sequence into segments, so the
+    agreement is to the stated bound, not bit for bit)."""
     B, T, Hv, Hk = 1, 16384, 32, 16
     q, k, v, g, beta, S = prefill_inputs(3, B, T, Hv, Hk)
     o1, S1 = gpu_prefill(L, q, k, v, g, beta, S)
     assert np.isfinite(o1).all() and np.isfinite(S1).all()
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, B, T, Hv, Hk, 128, 128, 64)
+    check(o1, o_ref, T, "output, all 32 heads")
+    check(S1, S_ref, T, "state, all 32 heads")
     o2, S2 = gpu_prefill(L, q, k, v, g, beta, S, calls=[8192, 8192])
     check(o2, o1, T, "two calls vs one, output")
     check(S2, S1, T, "two calls vs one, state")
-    hv = slice(Hv - 2, Hv)  # value heads 30, 31 read key head 15
-    sub = [np.ascontiguousarray(x) for x in (q[:, :, Hk - 1:], k[:, :, Hk - 1:], v[:, :, hv],
-                                             g[:, :, hv], beta[:, :, hv], S[:, hv])]
-    o_ref, S_ref = orc.chunk_gdr(*sub, B, T, 2, 1, 128, 128, 64)
-    check(o1[:, :, hv], o_ref, T, "output, heads 30-31")
-    check(S1[:, hv], S_ref, T, "state, heads 30-31")
 
 
 def test_prefill_rejects_bad_args(L):
     assert L.kai_run_gdn_chunk_delta_rule_bf16_f32_hip(None, None, None, None, None, None, None,
                                                        1, 64, 3, 2, 1.0, None) != 0
+
+
+@pytest.mark.parametrize("T", [1024, 8192])
+def test_prefill_config4_f16_state_all_heads(L, T):
+    """Config 4 (fp16 recurrent state, fp32 accumulation) at the 4B head
+    shape (Hv=32, Hk=16): every value head against the oracle, which starts
+    from the same fp16-rounded state; the kernel's final state is narrowed to
+    fp16 once, on exit."""
+    B, Hv, Hk = 1, 32, 16
+    q, k, v, g, beta, S = prefill_inputs(60 + T, B, T, Hv, Hk)
+    S16 = S.astype(np.float16).astype(np.float32)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S16, f16=True)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S16, B, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, f"output T={T}")
+    check(Sg, S_ref, T, f"state (fp16) T={T}")
+
+
+def device_inputs(seed, T, Hv, Hk, d=128):
+    """Config-2/3 distributions drawn on the device (long sequences): bf16
+    q, k (L2-normalised), v; fp32 g = -softplus(N) * e^U(-2,0), beta =
+    sigmoid(N); an fp16 initial state ~ N(0, 0.02)."""
+    torch = torch_mod()
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    def randn(*shape):
+        return torch.randn(*shape, device="cuda", generator=gen)
+    q = torch.nn.functional.normalize(randn(1, T, Hk, d), dim=-1).to(torch.bfloat16)
+    k = torch.nn.functional.normalize(randn(1, T, Hk, d), dim=-1).to(torch.bfloat16)
+    v = randn(1, T, Hv, d).to(torch.bfloat16)
+    u = torch.rand(1, T, Hv, device="cuda", generator=gen) * -2.0
+    g = (-torch.nn.functional.softplus(randn(1, T, Hv)) * torch.exp(u)).contiguous()
+    beta = torch.sigmoid(randn(1, T, Hv)).contiguous()
+    S = (0.02 * randn(1, Hv, d, d)).to(torch.float16)
+    return q, k, v, g, beta, S
+
+
+def gpu_prefill_dev(L, q, k, v, g, beta, S16, calls):
+    """fp16-state prefill of device tensors over consecutive calls; returns
+    (o bf16 [1][T][Hv][128], final fp16 state) on the device."""
+    import orionsbelt_amd as ob
+    torch = torch_mod()
+    _, T, Hk, d = q.shape
+    Hv = v.shape[2]
+    S = S16.clone()
+    o = torch.empty((1, T, Hv, d), dtype=torch.bfloat16, device="cuda")
+    t0 = 0
+    for tlen in calls:
+        sl = slice(t0, t0 + tlen)
+        xs = [x[:, sl].contiguous() for x in (q, k, v, g, beta)]
+        oc = torch.empty((1, tlen, Hv, d), dtype=torch.bfloat16, device="cuda")
+        ob.check(L.kai_run_gdn_chunk_delta_rule_bf16_f16state_hip(
+            *(P(x) for x in xs), P(oc), P(S), 1, tlen, Hv, Hk, 1.0 / math.sqrt(d), stream()), "prefill f16")
+        o[:, sl] = oc
+        t0 += tlen
+    torch.cuda.synchronize()
+    return o, S
+
+
+@pytest.mark.parametrize("T", [32768, 131072])
+def test_prefill_config4_long_sequences(L, T):
+    """Config 4 at T = 32K and 128K: finite; one call agrees with two calls
+    split at the middle (a chunk boundary) to the stated bound; the two value
+    heads of the last key head agree with the oracle over the whole
+    sequence."""
+    torch = torch_mod()
+    Hv, Hk = 32, 16
+    print(f"config 4 fp16 state T={T}", flush=True)
+    q, k, v, g, beta, S = device_inputs(T, T, Hv, Hk)
+    o1, S1 = gpu_prefill_dev(L, q, k, v, g, beta, S, [T])
+    assert torch.isfinite(o1).all().item() and torch.isfinite(S1).all().item()
+    o2, S2 = gpu_prefill_dev(L, q, k, v, g, beta, S, [T // 2, T // 2])
+    f32 = lambda x: x.float().cpu().numpy()  # noqa: E731
+    check(f32(o2), f32(o1), T, "two calls vs one, output")
+    check(f32(S2), f32(S1), T, "two calls vs one, state")
+    hv = slice(Hv - 2, Hv)  # value heads 30, 31 read key head 15
+    sub = [np.ascontiguousarray(f32(x)) for x in (q[:, :, Hk - 1:], k[:, :, Hk - 1:], v[:, :, hv], g[:, :, hv],
+                                                   beta[:, :, hv], S[:, hv])]
+    o_ref, S_ref = orc.chunk_gdr(*sub, 1, T, 2, 1, 128, 128, 64)
+    check(f32(o1[:, :, hv]), o_ref, T, f"output T={T}, heads 30-31")
+    check(f32(S1[:, hv]), S_ref, T, f"state (fp16) T={T}, heads 30-31")

@@ -163,11 +163,25 @@ def test_cumdecay_multi_tile(L, seq, ch):
     got = run_cumdecay(L, a, seq, ch)
     ref = orc.cumdecay_f32(a, seq, ch)
     assert_kai_close(got, ref, 1e-6, 1e-5, "cumdecay")   # test_kai_gdn.c:434, BASELINE 1e-5
-    # slow gates keep products O(1) over the whole sequence: relative bound
+    # Slow gates keep products O(1) over the whole sequence, so the relative
+    # rounding of the fp32 products themselves shows.  Both are held against
+    # the exact (float64) product: the reference's sequential fp32 product to
+    # BASELINE's 1e-5 (it is 8.2e-6 from exact at [4096][8192]), the kernel
+    # to 4e-6 (measured 1.9e-6 there: the carry into each 128-row tile and
+    # the inclusive values it passes on are composed in fp64 and rounded once,
+    # the rows inside a tile follow the reference's fp32 order).  Kernel and
+    # reference may differ from each other by the sum of their errors.
     a2 = rs.uniform(0.9995, 1.0005, seq * ch).astype(np.float32)
     got2 = run_cumdecay(L, a2, seq, ch)
     ref2 = orc.cumdecay_f32(a2, seq, ch)
-    assert_kai_close(got2, ref2, 0.0, 1e-5 if seq <= 1000 else 3e-5, "cumdecay slow gates")
+    exact = np.cumprod(a2.reshape(seq, ch).astype(np.float64), axis=0).ravel()
+    err_gpu = float(np.max(np.abs(got2 - exact) / np.abs(exact)))
+    err_ref = float(np.max(np.abs(ref2 - exact) / np.abs(exact)))
+    print(f"cumdecay slow gates [{seq}][{ch}]: kernel vs exact {err_gpu:.3e}, reference vs exact {err_ref:.3e}")
+    assert err_gpu <= 4e-6, err_gpu
+    assert err_ref <= 1e-5, err_ref
+    if seq <= 128:
+        assert np.array_equal(bits(got2), bits(ref2))
 
 
 def test_gated_scan_reference_sweep(L):
