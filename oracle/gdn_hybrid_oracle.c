@@ -38,7 +38,10 @@ static float hash_value(uint64_t seed, uint64_t stream, uint64_t i, float amp, f
     const float u = (float)(h >> 40) * (1.0f / 16777216.0f);
     return (u * 2.0f - 1.0f) * amp + center;
 }
+/* Element i is a function of (seed, stream, i) alone, so the loops below may
+ * run in any order or in parallel and draw the same values. */
 static void draw(float *dst, size_t n, uint64_t seed, uint64_t stream, float amp, float center) {
+#pragma omp parallel for schedule(static)
     for (size_t i = 0; i < n; ++i) dst[i] = hash_value(seed, stream, i, amp, center);
 }
 
@@ -138,6 +141,7 @@ orc_hybrid *orc_hybrid_create(const orc_hybrid_config *cfg, uint64_t seed) {
     }
     const size_t ne = (size_t)c->vocab * H;
     m->embed = malloc(2 * ne);
+#pragma omp parallel for schedule(static)
     for (size_t i = 0; i < ne; ++i) m->embed[i] = orc_f32_to_f16(hash_value(seed, G_EMBED, i, 1.0f, 0.f));
     m->final_norm = make_vec(H, seed, G_FINAL_NORM, 0.1f, 0.f);
     make_mat(&m->lm, c->vocab, H, seed, G_LM_HEAD);
@@ -186,6 +190,7 @@ void orc_hybrid_reset(orc_hybrid *m, int batch, int context, uint64_t seed) {
             }
         } else {
             const size_t n = (size_t)batch * c->attn_kv_heads * c->max_context * 256;
+#pragma omp parallel for schedule(static)
             for (size_t i = 0; i < n; ++i) {
                 const int t = (int)((i / 256) % c->max_context);
                 L->Kc[i] = t < context ? orc_f32_to_f16(hash_value(seed, base + S_K, i, 1.0f, 0.f)) : 0;

@@ -589,14 +589,18 @@ static float f16_bits_to_float(uint16_t h) { return orc_f16_to_f32(h); }
 
 void orc_w8_gemm(const uint16_t *x, const int8_t *Wq, const float *scale, float *y, int M,
                  int N, int K) {
+    /* the activations widened once (the same values the sum would widen) */
+    float *xf = malloc(sizeof(float) * (size_t)M * K);
+    for (size_t i = 0; i < (size_t)M * K; ++i) xf[i] = f16_bits_to_float(x[i]);
 #pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
         for (int m = 0; m < M; ++m) {
             double acc = 0.0;
             for (int k = 0; k < K; ++k)
-                acc += (double)f16_bits_to_float(x[(size_t)m * K + k]) * Wq[(size_t)n * K + k];
+                acc += (double)xf[(size_t)m * K + k] * Wq[(size_t)n * K + k];
             y[(size_t)m * N + n] = (float)acc * scale[n];
         }
+    free(xf);
 }
 
 /* ---- attention decode (see header) ---------------------------------------- */

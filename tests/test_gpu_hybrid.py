@@ -2,11 +2,17 @@
 C-ABI, against the oracle's CPU model (oracle/gdn_hybrid_oracle.c) drawn from
 the same seed, and against the HF Qwen3_5ForCausalLM logits fixture.
 
-Tolerance: 1e-3 of the step's largest |logit| (the device sums the int8
-matmuls in fp32 where the oracle sums in double and uses hardware exp and
-rsqrt; an fp16 rounding of an activation that lands the other side of a
-rounding boundary moves a logit by about 1e-4 of the largest), and the
-greedy token wherever the oracle's top-2 margin exceeds 2e-3 of it.
+Tolerance: 1e-3 of the step's largest |logit| for models of up to 8
+layers (the device sums the int8 matmuls in fp32 where the oracle sums in
+double and uses hardware exp and rsqrt; an fp16 rounding of an activation
+that lands the other side of a rounding boundary moves a logit by about 1e-4
+of the largest), and the greedy token wherever the oracle's top-2 margin
+exceeds twice the tolerance.  Those flips accumulate through the residual
+stream: at the 4B widths the measured error is 7e-4 (4 layers), 1.1e-3 (8),
+1.6-1.8e-3 (16) and 2.2-2.6e-3 (32 layers), growing as sqrt(layers) and the
+same after an empty or an 8192-token context, with the 2-norm error tracking
+the maximum.  Deeper models are therefore held to 7e-4 * sqrt(layers) (4e-3
+at 32 layers).
 """
 import numpy as np
 import pytest
@@ -49,18 +55,22 @@ def step(gm, tokens, vocab):
     return host(nxt), host(logits)
 
 
-def assert_close(lg, ref, what):
+def tol(layers=8):
+    return max(TOL, 7e-4 * np.sqrt(layers))
+
+
+def assert_close(lg, ref, what, layers=8):
     scale = np.abs(ref).max()
     err = np.abs(lg - ref).max()
     print(f"{what}: max |dlogit| {err:.3e} = {err / scale:.2e} of the largest")
-    assert err <= TOL * scale, what
+    assert err <= tol(layers) * scale, what
 
 
-def assert_greedy(nxt, lg, ref):
+def assert_greedy(nxt, lg, ref, layers=8):
     # the device's token is its own logits' first maximum, exactly
     assert np.array_equal(nxt, lg.argmax(1))
     top2 = np.sort(ref, 1)[:, -2:]
-    clear = top2[:, 1] - top2[:, 0] > 2e-3 * np.abs(ref).max()
+    clear = top2[:, 1] - top2[:, 0] > 2 * tol(layers) * np.abs(ref).max()
     assert np.array_equal(nxt[clear], ref.argmax(1)[clear])
 
 
@@ -186,6 +196,93 @@ def test_hybrid_qwen35_4b_shape(hb):
         assert np.array_equal(n1, l1.argmax(1))
         assert np.array_equal(l1, l2) and np.array_equal(n1, n2)
     assert gm.position == 4003
+    gm.close()
+
+
+def oracle_config(cfg):
+    return orc.HybridConfig(*[getattr(cfg, n) for n, _ in orc.HybridConfig._fields_])
+
+
+def test_hybrid_qwen35_4b_vs_oracle(hb):
+    """The full Qwen3.5-4B shape (hidden 2560, the 9216-wide MLP with its
+    split-k down matrix and fused residual norm at batch <= 2, the separate
+    norm kernel at batch 3, the 151936-wide LM head) against the CPU model,
+    at batch 2 and batch 3 after a drawn 8192-token context, two steps each."""
+    cfg = hb.qwen35_4b(3, 8200)
+    gm = hb.HybridModel(cfg, 2468)
+    om = orc.HybridModel(oracle_config(cfg), 2468)
+    rs = np.random.RandomState(5)
+    for B in (2, 3):
+        gm.reset(B, 8192, 31)
+        om.reset(B, 8192, 31)
+        for t in range(2):
+            tok = rs.randint(0, cfg.vocab, B)
+            nxt, lg = step(gm, tok, cfg.vocab)
+            _, olg = om.step(tok)
+            assert_close(lg, olg, f"4B shape B={B} ctx 8192 step {t}", cfg.layers)
+            assert_greedy(nxt, lg, olg, cfg.layers)
+    gm.close()
+
+
+def test_hybrid_reduced_hidden_32k_context_vs_oracle(hb):
+    """Attention over a 32K-position drawn context (the spans and their
+    combine at the config-5 length) with the 4B head counts and a small
+    hidden size, against the CPU model: batch 2, two steps."""
+    over = dict(layers=8, attn_every=4, hidden=512, inter=1024, vocab=2048, gdn_k_heads=16, gdn_v_heads=32,
+                attn_q_heads=16, attn_kv_heads=4, max_batch=2, max_context=32768 + 8, rope_theta=1e7,
+                rms_eps=1e-6)
+    gm = hb.HybridModel(hb.config(**over), 97)
+    om = orc.HybridModel(orc.HybridConfig(*[over[n] for n, _ in orc.HybridConfig._fields_]), 97)
+    gm.reset(2, 32768, 3)
+    om.reset(2, 32768, 3)
+    rs = np.random.RandomState(6)
+    for t in range(2):
+        tok = rs.randint(0, over["vocab"], 2)
+        nxt, lg = step(gm, tok, over["vocab"])
+        _, olg = om.step(tok)
+        assert_close(lg, olg, f"ctx 32768 step {t}")
+        assert_greedy(nxt, lg, olg)
+    assert gm.position == 32770
+    gm.close()
+
+
+def test_hybrid_config5_batch16_ctx32k(hb):
+    """Config 5's batch-16 decode at the 4B shape after a drawn 32K context
+    (the state the bench times): finite logits, each device token its own
+    logits' argmax, a replay from the same reset bit-identical, and row 0
+    unchanged when every other row is fed different tokens (rows never mix)."""
+    torch = torch_mod()
+    B = 16
+    cfg = hb.qwen35_4b(B, 32768 + 64)
+    gm = hb.HybridModel(cfg, 12345)
+    rs = np.random.RandomState(8)
+    first = rs.randint(0, cfg.vocab, B).astype(np.int32)
+
+    def run(tok0):
+        gm.reset(B, 32768, 7)
+        nxt = empty((B,), torch.int32)
+        logits = empty((B, cfg.vocab), torch.float32)
+        tok = dev(tok0)
+        out = []
+        for _t in range(3):
+            gm.step(tok, nxt, logits)
+            out.append((host(nxt).copy(), host(logits).copy()))
+            tok = nxt.clone()
+        return out
+
+    a = run(first)
+    b = run(first)
+    other = first.copy()
+    other[1:] = (other[1:] + 1000) % cfg.vocab
+    c = run(other)
+    for (n1, l1), (n2, l2), (n3, l3) in zip(a, b, c):
+        assert np.isfinite(l1).all()
+        assert ((n1 >= 0) & (n1 < cfg.vocab)).all()
+        assert np.array_equal(n1, l1.argmax(1))
+        assert np.array_equal(l1, l2) and np.array_equal(n1, n2)
+        assert np.array_equal(l3[0], l1[0]) and n3[0] == n1[0]
+        assert not np.array_equal(l3[1:], l1[1:])
+    assert gm.position == 32768 + 3
     gm.close()
 
 
