@@ -14,7 +14,11 @@ The JSON line also carries:
   roofline      the decode kernel: algorithmic bytes per launch / its mean
                 launch time from HIP events on the launch stream, vs 8 TB/s
   cpu_baseline  the CPU oracle (oracle/, OpenMP over (sequence, head)) on a
-                bounded sample of the same step, on this host's cores
+                bounded sample of the same step, on this host's cores,
+                pinned; then on one pinned thread.  The conv, decay and scan
+                lines carry their own cpu_baseline: the reference's scalar C
+                (compiled from its sources into oracle/_ref) on one pinned
+                thread, and the OpenMP port on all cores
   secondary     prefill (config 3, T=16K), the fp16-state prefill at
                 T in {1K, 8K, 32K, 128K} (config 4: tokens/s and the per-layer
                 state footprint), conv+SiLU (config 1) and cumulative decay
@@ -111,6 +115,20 @@ class Timer:
         ts = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
         return ts[(reps - 1) // 2]
 
+    def per_call_ms(self, fns):
+        """Each callable of `fns` run once, in order, with an event recorded
+        between consecutive calls on the launch stream; returns the list of
+        per-call durations (each kernel's own launch time)."""
+        t = self.torch
+        ev = [t.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)]
+        t.cuda.synchronize()
+        ev[0].record()
+        for i, fn in enumerate(fns):
+            fn()
+            ev[i + 1].record()
+        ev[-1].synchronize()
+        return [ev[i].elapsed_time(ev[i + 1]) for i in range(len(fns))]
+
 
 
 def bench_decode(L, ob, torch, steps, warmup, timer, f16_state=False):
@@ -146,16 +164,136 @@ def bench_decode(L, ob, torch, steps, warmup, timer, f16_state=False):
     for _ in range(warmup):
         step()
     ms_step = timer.time_ms(step, steps)
-    # the timed region holds only decode launches, back to back on one
-    # stream: the mean launch duration is the region time / launch count
+    # The timed region holds only decode launches, back to back on the
+    # stream the events are recorded on: its time / launch count is the mean
+    # launch duration (the rocprofv3 average agrees within 1%).  Events
+    # recorded between every pair of launches, the alternative, add each
+    # event's own cost (about 3 us) to every launch; that figure is kept as
+    # a cross-check.
     kern_ms = ms_step / LAYERS
-    return ms_step, kern_ms, layers
+    durs = timer.per_call_ms([(lambda t=t: launch(t)) for _ in range(min(steps, 20)) for t in layers])
+    return ms_step, kern_ms, sum(durs) / len(durs)
 
 
-def cpu_decode_baseline(budget_s=12.0, single_budget_s=6.0):
-    """The oracle (OpenMP over (sequence, head)) on the same per-layer step;
-    runs whole layers until the budget is spent, reports tokens/s of a
-    24-layer step.  Then the same on one thread (OpenMP set to 1)."""
+def cpu_sets():
+    """The CPUs the CPU legs are pinned to: the first omp_get_max_threads()
+    CPUs this process may run on (all cores), and the first of them alone
+    (one thread)."""
+    from oracle import oracle as orc
+    allowed = sorted(os.sched_getaffinity(0))
+    return allowed[:max(1, min(orc.num_threads(), len(allowed)))], allowed
+
+
+def pin(cpus):
+    """What `taskset -a -p` does: pin every thread of this process (OpenMP
+    workers included; threads started later inherit the mask) to `cpus`."""
+    for tid in os.listdir("/proc/self/task"):
+        try:
+            os.sched_setaffinity(int(tid), set(cpus))
+        except OSError:
+            pass
+
+
+def cpu_p50_ms(fn, budget_s, min_reps=3, max_reps=30):
+    """One untimed call, then calls timed one by one until `budget_s` is
+    spent (at least `min_reps`, at most `max_reps`); median by nearest rank,
+    the GPU protocol's statistic.  Returns (p50 ms, calls timed, seconds)."""
+    fn()
+    ts, t_start = [], time.perf_counter()
+    while len(ts) < max_reps and (len(ts) < min_reps or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[(len(ts) - 1) // 2], len(ts), time.perf_counter() - t_start
+
+
+def cpu_stream_baseline(budget_s=1.0):
+    """CPU legs of the [4096][8192] stream lines (conv, decay, scans):
+    - "reference": the reference's own portable C, compiled from its sources
+      by oracle/Makefile into oracle/_ref (kai ukernels' scalar branches for
+      the fp32 conv, decay and scan; gdn_sve.c for the fp16/bf16 scan and
+      decay), one thread pinned to one core;
+    - "port": this repo's C restatement (oracle/, OpenMP over channels) on
+      all cores, pinned.
+    The kai conv has no SiLU, so the conv line's reference leg is the conv
+    alone; the port runs conv+SiLU, the GPU line's workload.  Inputs have
+    the GPU lines' distributions: the conv inputs of config 1; decay factors
+    exp(-softplus(N(0,1)) exp(U(-2,0))) for the fp32 decay; gates U(0,1)
+    and x N(0,1) for the scans and the narrow decays."""
+    from oracle import oracle as orc
+    from tests.gdn_inputs import conv_inputs
+    P = orc.P
+    T, C = DEC_T, DEC_C
+    cx, w, hist = (np.ascontiguousarray(v, dtype=np.float32) for v in conv_inputs(1, CONV_T, CONV_C))
+    rs = np.random.RandomState(2)
+    gl = -np.log1p(np.exp(rs.randn(T * C))) * np.exp(rs.uniform(-2, 0, T * C))
+    a = np.exp(gl).astype(np.float32)
+    del gl
+    x = rs.randn(T * C).astype(np.float32)
+    g = rs.uniform(0.0, 1.0, T * C).astype(np.float32)
+    out = np.empty(T * C, np.float32)
+    out16 = np.empty(T * C, np.uint16)
+    st32 = np.zeros(C, np.float32)
+    st16 = np.zeros(C, np.uint16)
+    z = (ctypes.c_size_t(T), ctypes.c_size_t(C))
+    kai, sve, port = orc.ref_kai(), orc.ref_sve(), orc.lib()
+    scan32 = 3 * T * C * 4 + 2 * C * 4
+    scan16 = 3 * T * C * 4 + 2 * C * 2
+    # line name: (bytes, reference (lib, symbol, args) or None, port (symbol, args))
+    jobs = {
+        "conv": (CONV_BYTES, (kai, "kai_run_gdn_causal_dwconv1d_f32_k4_sve", (P(cx), P(w), P(out), P(hist))),
+                 ("orc_causal_dwconv1d_silu_f32_k4", (P(cx), P(w), P(out), P(hist)))),
+        "cumdecay": (DECAY_BYTES, (kai, "kai_run_gdn_cumdecay_f32_sve", (P(a), P(out))),
+                     ("orc_cumdecay_f32", (P(a), P(out)))),
+        "gated_scan_f32": (scan32, (kai, "kai_run_gdn_gated_scan_f32_sve", (P(g), P(x), P(out), P(st32))),
+                           ("orc_gated_scan_f32", (P(g), P(x), P(out), P(st32)))),
+        "gated_scan_f16": (scan16, (sve, "gdn_gated_scan_f16", (P(g), P(x), P(out), P(st16))),
+                           ("orc_gated_scan_f16", (P(g), P(x), P(out), P(st16)))),
+        "gated_scan_bf16": (scan16, (sve, "gdn_gated_scan_bf16", (P(g), P(x), P(out), P(st16))),
+                            ("orc_gated_scan_bf16", (P(g), P(x), P(out), P(st16)))),
+        "cumdecay_f16": (T * C * 6, (sve, "gdn_cumdecay_f16", (P(g), P(out16))),
+                         ("orc_cumdecay_f16", (P(g), P(out16)))),
+        "cumdecay_bf16": (T * C * 6, (sve, "gdn_cumdecay_bf16", (P(g), P(out16))),
+                          ("orc_cumdecay_bf16", (P(g), P(out16)))),
+    }
+    all_cpus, allowed = cpu_sets()
+    threads = orc.num_threads()
+    res = {}
+    for name, (nbytes, ref, (psym, pargs)) in jobs.items():
+        entry = {"unit": "GB/s", "cpu_model": cpu_model()}
+        pin(all_cpus)
+        pfn = getattr(port, psym)
+        ms, n, el = cpu_p50_ms(lambda: pfn(*pargs, *z), budget_s)
+        port_leg = {"value": round(nbytes / (ms * 1e-3) / 1e9, 2), "us": round(ms * 1e3, 1),
+                    "cores": len(all_cpus), "kind": "port",
+                    "sample": f"{psym}, [{T}][{C}], p50 of {n} calls ({el:.1f} s), "
+                              f"{threads} OpenMP threads pinned to CPUs {all_cpus[0]}-{all_cpus[-1]}"}
+        lib, rsym, rargs = ref
+        if lib is not None:
+            pin(all_cpus[:1])
+            orc.set_num_threads(1)
+            rfn = getattr(lib, rsym)
+            ms, n, el = cpu_p50_ms(lambda: rfn(*rargs, *z), budget_s)
+            orc.set_num_threads(threads)
+            entry.update({"value": round(nbytes / (ms * 1e-3) / 1e9, 3), "us": round(ms * 1e3, 1),
+                          "cores": 1, "kind": "reference",
+                          "sample": f"{rsym} (reference source, oracle/_ref build, -O3), [{T}][{C}], "
+                                    f"p50 of {n} calls ({el:.1f} s), one thread pinned to CPU {all_cpus[0]}"})
+            entry["port_all_cores"] = port_leg
+        else:
+            entry.update(port_leg)
+            entry["note"] = "oracle/_ref not built: the port is the baseline"
+        res[name] = entry
+    pin(allowed)
+    return res
+
+
+def cpu_decode_baseline(budget_s=12.0, single_budget_s=10.0):
+    """The oracle (OpenMP over (sequence, head)) on the same per-layer step,
+    pinned to the cores it uses; runs whole layers until the budget is spent,
+    reports tokens/s of a 24-layer step.  Then the same on one thread
+    (OpenMP set to 1, pinned to one core)."""
     from oracle import oracle as orc
     from tests.gdn_inputs import decode_inputs
     S, q, k, v, g, beta = decode_inputs(1000, B_DEC, HV, HK, DK, DV)
@@ -172,16 +310,21 @@ def cpu_decode_baseline(budget_s=12.0, single_budget_s=6.0):
                 return n, el
 
     threads = orc.num_threads()
-    n, el = run(budget_s, 240)
+    all_cpus, allowed = cpu_sets()
+    pin(all_cpus)
+    n, el = run(budget_s, 2400)
+    pin(all_cpus[:1])
     orc.set_num_threads(1)
-    n1, el1 = run(single_budget_s, 24)
+    n1, el1 = run(single_budget_s, 240)
     orc.set_num_threads(threads)
+    pin(allowed)
     return {"value": round(B_DEC / (el / n * LAYERS), 2), "unit": "tokens/s",
-            "cores": threads, "kind": "port",
+            "cores": len(all_cpus), "kind": "port",
             "sample": f"{n} layer-steps of B=64 x 32 heads x 128x128 fp32 "
-                      f"({n / LAYERS:.1f} full 24-layer steps), {el:.1f} s",
+                      f"({n / LAYERS:.1f} full 24-layer steps), {el:.1f} s, {threads} OpenMP threads "
+                      f"pinned to CPUs {all_cpus[0]}-{all_cpus[-1]}",
             "single_thread": {"value": round(B_DEC / (el1 / n1 * LAYERS), 2), "cores": 1,
-                              "sample": f"{n1} layer-steps, {el1:.1f} s"},
+                              "sample": f"{n1} layer-steps, {el1:.1f} s, pinned to CPU {all_cpus[0]}"},
             "cpu_model": cpu_model()}
 
 
@@ -251,13 +394,22 @@ def bench_prefill_f16_state(L, ob, torch, timer, lengths=(1024, 8192, 32768, 131
 
         ms = timer.p50_ms(run, warmup=20, reps=30)
         flop = PF_FLOP_PER_CHUNK_HEAD * ((T + 63) // 64) * HV
+        state_b = S16.numel() * S16.element_size()
+        carry_b = int(L.kai_gdn_hip_prefill_workspace_bytes(1, T, HV))
         rows.append({"T": T, "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
                      "achieved_tflops": round(flop / (ms * 1e-3) / 1e12, 2),
-                     "state_bytes_per_layer": HV * 128 * 128 * 2})
+                     "state_bytes_per_layer": state_b, "carry_bytes": carry_b,
+                     "footprint_bytes_one_layer": state_b + carry_b,
+                     "library_device_bytes_held": int(L.kai_gdn_hip_device_bytes_held())})
         del q, k, v, g, beta, S, S16, o
     return {"workload": "chunked WY prefill with fp16 state (fp32 accumulate), B=1 Hv=32 Hk=16 "
                         "d=128, bf16 q/k/v (BASELINE configs[3])",
-            "state_bytes_per_layer": HV * 128 * 128 * 2,
+            "footprint_note": "state_bytes_per_layer: the fp16 state tensor a layer keeps between calls "
+                              "(measured from the allocation); carry_bytes: the library's segment carry "
+                              "buffer for this T (one per device, shared by all layers, whose calls run "
+                              "one after another); library_device_bytes_held: all device memory the "
+                              "library holds after the call (the carry buffer grown with 25% headroom, "
+                              "scan status arrays, staging)",
             "state_bytes_per_layer_fp32_state": HV * 128 * 128 * 4,
             "lengths": rows}
 
@@ -404,6 +556,8 @@ def cpu_prefill_baseline(budget_s=10.0):
     from tests.gdn_inputs import prefill_inputs
     T = 256
     q, k, v, g, beta, S = prefill_inputs(7, 1, T, HV, HK)
+    all_cpus, allowed = cpu_sets()
+    pin(all_cpus)
     n, t0 = 0, time.perf_counter()
     while True:
         orc.chunk_gdr(q, k, v, g, beta, S, 1, T, HV, HK, 128, 128, 64)
@@ -411,8 +565,11 @@ def cpu_prefill_baseline(budget_s=10.0):
         el = time.perf_counter() - t0
         if el > budget_s:
             break
-    return {"value": round(n * T / el, 1), "unit": "tokens/s", "cores": orc.num_threads(),
-            "kind": "port", "sample": f"{n} x T={T} (32 heads), {el:.1f} s"}
+    pin(allowed)
+    return {"value": round(n * T / el, 1), "unit": "tokens/s", "cores": len(all_cpus),
+            "kind": "port", "sample": f"{n} x T={T} (32 heads, OpenMP over heads), {el:.1f} s, "
+                                      f"pinned to CPUs {all_cpus[0]}-{all_cpus[-1]}",
+            "cpu_model": cpu_model()}
 
 
 def bench_stream(L, ob, torch, timer, reps=40, sets=4):
@@ -605,8 +762,8 @@ def run_profile(which, L, ob, torch, timer, steps, warmup):
     (dst = src * 1 over 64M fp32: reads and writes exactly 268,435,456 bytes),
     the reference for scaling FETCH_SIZE / WRITE_SIZE to bytes."""
     if which == "decode":
-        ms, kern, _ = bench_decode(L, ob, torch, steps, warmup, timer)
-        log(f"decode: {ms:.4f} ms/step, {kern * 1e3:.2f} us/launch")
+        ms, kern, pairs = bench_decode(L, ob, torch, steps, warmup, timer)
+        log(f"decode: {ms:.4f} ms/step, {kern * 1e3:.2f} us/launch ({pairs * 1e3:.2f} with events between launches)")
     elif which == "prefill":
         log(f"prefill: {bench_prefill(L, ob, torch, timer, reps=steps)}")
     elif which == "prefill_f16":
@@ -662,7 +819,7 @@ def main():
     peaks = measure_peaks(L, ob, torch, timer)
     log(f"peaks: {peaks}")
     log("decode: 24 layers x B=64 ...")
-    ms_step, kern_ms, _ = bench_decode(L, ob, torch, args.steps, args.warmup, timer)
+    ms_step, kern_ms, kern_pairs = bench_decode(L, ob, torch, args.steps, args.warmup, timer)
     achieved = DEC_BYTES / (kern_ms * 1e-3) / 1e9
     log(f"decode: {ms_step:.3f} ms/step, kernel {kern_ms * 1e3:.1f} us ({achieved:.0f} GB/s)")
 
@@ -678,13 +835,14 @@ def main():
         secondary["conv"], secondary["cumdecay"] = bench_stream(L, ob, torch, timer)
         log(f"conv: {secondary['conv']}\ncumdecay: {secondary['cumdecay']}")
         log("decode with fp16 state ...")
-        ms16, kern16, _ = bench_decode(L, ob, torch, args.steps, args.warmup, timer, f16_state=True)
+        ms16, kern16, pairs16 = bench_decode(L, ob, torch, args.steps, args.warmup, timer, f16_state=True)
         b16 = DEC_BYTES - B_DEC * HV * DK * DV * 4  # the state read + written at 2 bytes
         gbs16 = b16 / (kern16 * 1e-3) / 1e9
         secondary["decode_f16_state"] = {
             "workload": "decode step, 24 layers, B=64, Hv=32 Hk=16, 128x128 fp16 state (fp32 arithmetic)",
             "ms_per_step": round(ms16, 4), "tokens_per_s": round(B_DEC / (ms16 * 1e-3), 1),
-            "bytes_per_launch": b16, "launch_us": round(kern16 * 1e3, 2), "achieved_gbs": round(gbs16, 1),
+            "bytes_per_launch": b16, "launch_us": round(kern16 * 1e3, 2),
+            "launch_us_event_pairs": round(pairs16 * 1e3, 2), "achieved_gbs": round(gbs16, 1),
             "hbm_frac": round(gbs16 / HBM_PEAK_GBS, 4)}
         log(f"decode fp16 state: {secondary['decode_f16_state']}")
         log("gated scan and narrow-state scan/decay ...")
@@ -705,6 +863,12 @@ def main():
         log(f"cpu: {cpu}")
         if not args.no_secondary:
             secondary["prefill"]["cpu_baseline"] = cpu_prefill_baseline()
+            log("cpu baselines of the stream lines (reference scalar build, port) ...")
+            stream_cpu = cpu_stream_baseline()
+            for name, entry in stream_cpu.items():
+                line_ = secondary["scans"].get(name) or secondary.get(name)
+                line_["cpu_baseline"] = entry
+            log(f"cpu stream: {stream_cpu}")
 
     line = {
         "metric": "GDN decode tok/s (B=64, 24 layers, 1 GPU) + % of HBM roofline",
@@ -727,7 +891,11 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profile_traffic("delta_decode_kernel"),
                      "kernel": "delta_decode_kernel<128,128,f32>",
-                     "bytes_per_launch": DEC_BYTES, "launch_us": round(kern_ms * 1e3, 2)},
+                     "bytes_per_launch": DEC_BYTES, "launch_us": round(kern_ms * 1e3, 2),
+                     "launch_us_event_pairs": round(kern_pairs * 1e3, 2),
+                     "launch_note": "launch_us: the timed region (decode launches only, back to back) / "
+                                    "launch count; launch_us_event_pairs: events recorded between every "
+                                    "two launches, which adds each event's own cost"},
         "cpu_baseline": cpu,
         "measured_peaks": peaks,
         "secondary": secondary,

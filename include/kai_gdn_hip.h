@@ -308,6 +308,18 @@ const char *kai_gdn_hip_error_string(int code);
  * is invalid).  Synchronises the device, then clears the flag. */
 int kai_gdn_hip_check_device_error(void);
 
+/* ---- device memory queries -----------------------------------------------
+ * No reference counterpart (the reference's kernels allocate nothing on a
+ * device).  Bytes of library-owned device workspace that one chunked-prefill
+ * call of this shape uses (the segment carry buffer; 0 when the call runs as
+ * one segment).  Calls on one device share that buffer, so a model's layers
+ * need it once, not once per layer.  Needs no device. */
+size_t kai_gdn_hip_prefill_workspace_bytes(int batch, int seq_len, int num_v_heads);
+/* Device bytes the library holds on the current device right now (prefill
+ * carry buffer, scan status arrays, host-pointer staging buffers); they grow
+ * with the largest call seen and are kept until the process ends. */
+size_t kai_gdn_hip_device_bytes_held(void);
+
 /* ---- measurement probes --------------------------------------------------
  * No reference counterpart: what the current device delivers for a
  * streaming copy or read and for dense bf16 MFMA, so that roofline fractions

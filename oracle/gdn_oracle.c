@@ -5,7 +5,7 @@
  * measured or shipped.  See gdn_oracle.h for the function list, the reference
  * file:line each one follows and what pins it.
  *
- * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp).
+ * Build: oracle/Makefile (gcc -O3 -ffp-contract=off -fopenmp).
  */
 #include "gdn_oracle.h"
 
@@ -37,18 +37,31 @@ void orc_set_num_threads(int n) {
 /* kai ukernels (portable scalar branches)                                   */
 /* ======================================================================== */
 
+/* The channel loops below walk ORC_CB adjacent channels through the
+ * sequence together (t outer, the channel group inner: one cache line of
+ * each row per step) instead of one channel at a time.  Every channel's
+ * operations and their order are unchanged, so the results are those of
+ * the reference's channel-by-channel loops, whatever the thread count. */
+#define ORC_CB 16
+#define ORC_GROUPS(channels) ((long)(((channels) + ORC_CB - 1) / ORC_CB))
+#define ORC_GROUP_WIDTH(gg, channels) \
+    ((channels) - (size_t)(gg) * ORC_CB < ORC_CB ? (channels) - (size_t)(gg) * ORC_CB : ORC_CB)
+
 void orc_cumdecay_f32(const float *a, float *decay, size_t seq, size_t channels) {
-    /* Channels are independent; the parallel loop does not change any
-     * per-channel operation order, so results are thread-count invariant. */
 #ifdef _OPENMP
 #pragma omp parallel for schedule(static) if (seq * channels > 65536)
 #endif
-    for (long cc = 0; cc < (long)channels; ++cc) {
-        size_t c = (size_t)cc;
-        float run = 1.0f;
+    for (long gg = 0; gg < ORC_GROUPS(channels); ++gg) {
+        const size_t c0 = (size_t)gg * ORC_CB, n = ORC_GROUP_WIDTH(gg, channels);
+        float run[ORC_CB];
+        for (size_t j = 0; j < n; ++j) run[j] = 1.0f;
         for (size_t t = 0; t < seq; ++t) {
-            run = run * a[t * channels + c];
-            decay[t * channels + c] = run;
+            const float *ar = a + t * channels + c0;
+            float *dr = decay + t * channels + c0;
+            for (size_t j = 0; j < n; ++j) {
+                run[j] = run[j] * ar[j];
+                dr[j] = run[j];
+            }
         }
     }
 }
@@ -58,14 +71,18 @@ void orc_gated_scan_f32(const float *g, const float *x, float *s, float *state,
 #ifdef _OPENMP
 #pragma omp parallel for schedule(static) if (seq * channels > 65536)
 #endif
-    for (long cc = 0; cc < (long)channels; ++cc) {
-        size_t c = (size_t)cc;
-        float acc = state[c];
+    for (long gg = 0; gg < ORC_GROUPS(channels); ++gg) {
+        const size_t c0 = (size_t)gg * ORC_CB, n = ORC_GROUP_WIDTH(gg, channels);
+        float acc[ORC_CB];
+        for (size_t j = 0; j < n; ++j) acc[j] = state[c0 + j];
         for (size_t t = 0; t < seq; ++t) {
-            acc = x[t * channels + c] + acc * g[t * channels + c];
-            s[t * channels + c] = acc;
+            const size_t r = t * channels + c0;
+            for (size_t j = 0; j < n; ++j) {
+                acc[j] = x[r + j] + acc[j] * g[r + j];
+                s[r + j] = acc[j];
+            }
         }
-        state[c] = acc;
+        for (size_t j = 0; j < n; ++j) state[c0 + j] = acc[j];
     }
 }
 
@@ -74,26 +91,38 @@ static void conv_k4(const float *in, const float *w, float *out, float *hist,
 #ifdef _OPENMP
 #pragma omp parallel for schedule(static) if (seq * channels > 65536)
 #endif
-    for (long cc = 0; cc < (long)channels; ++cc) {
-        size_t c = (size_t)cc;
-        float h0 = hist[0 * channels + c];
-        float h1 = hist[1 * channels + c];
-        float h2 = hist[2 * channels + c];
-        const float w0 = w[0 * channels + c], w1 = w[1 * channels + c];
-        const float w2 = w[2 * channels + c], w3 = w[3 * channels + c];
-        for (size_t t = 0; t < seq; ++t) {
-            float cur = in[t * channels + c];
-            /* left-to-right: ((h0*w0 + h1*w1) + h2*w2) + cur*w3 */
-            float acc = h0 * w0 + h1 * w1 + h2 * w2 + cur * w3;
-            if (silu) acc = acc / (1.0f + expf(-acc));
-            out[t * channels + c] = acc;
-            h0 = h1;
-            h1 = h2;
-            h2 = cur;
+    for (long gg = 0; gg < ORC_GROUPS(channels); ++gg) {
+        const size_t c0 = (size_t)gg * ORC_CB, n = ORC_GROUP_WIDTH(gg, channels);
+        float h0[ORC_CB], h1[ORC_CB], h2[ORC_CB], w0[ORC_CB], w1[ORC_CB], w2[ORC_CB], w3[ORC_CB];
+        for (size_t j = 0; j < n; ++j) {
+            const size_t c = c0 + j;
+            h0[j] = hist[0 * channels + c];
+            h1[j] = hist[1 * channels + c];
+            h2[j] = hist[2 * channels + c];
+            w0[j] = w[0 * channels + c];
+            w1[j] = w[1 * channels + c];
+            w2[j] = w[2 * channels + c];
+            w3[j] = w[3 * channels + c];
         }
-        hist[0 * channels + c] = h0;
-        hist[1 * channels + c] = h1;
-        hist[2 * channels + c] = h2;
+        for (size_t t = 0; t < seq; ++t) {
+            const size_t r = t * channels + c0;
+            for (size_t j = 0; j < n; ++j) {
+                const float cur = in[r + j];
+                /* left-to-right: ((h0*w0 + h1*w1) + h2*w2) + cur*w3 */
+                float acc = h0[j] * w0[j] + h1[j] * w1[j] + h2[j] * w2[j] + cur * w3[j];
+                if (silu) acc = acc / (1.0f + expf(-acc));
+                out[r + j] = acc;
+                h0[j] = h1[j];
+                h1[j] = h2[j];
+                h2[j] = cur;
+            }
+        }
+        for (size_t j = 0; j < n; ++j) {
+            const size_t c = c0 + j;
+            hist[0 * channels + c] = h0[j];
+            hist[1 * channels + c] = h1[j];
+            hist[2 * channels + c] = h2[j];
+        }
     }
 }
 
@@ -187,49 +216,48 @@ uint16_t orc_f32_to_bf16(float f) {
 
 float orc_bf16_to_f32(uint16_t b) { return bits_f32((uint32_t)b << 16); }
 
-void orc_cumdecay_f16(const float *a, uint16_t *decay, size_t seq, size_t channels) {
-    for (size_t c = 0; c < channels; ++c) {
-        float run = 1.0f;
-        for (size_t t = 0; t < seq; ++t) {
-            run = run * a[t * channels + c];
-            decay[t * channels + c] = orc_f32_to_f16(run);
-        }
+#define ORC_NARROW_DECAY(name, cvt)                                                      \
+    void name(const float *a, uint16_t *decay, size_t seq, size_t channels) {            \
+        _Pragma("omp parallel for schedule(static) if (seq * channels > 65536)")          \
+        for (long gg = 0; gg < ORC_GROUPS(channels); ++gg) {                              \
+            const size_t c0 = (size_t)gg * ORC_CB, n = ORC_GROUP_WIDTH(gg, channels);     \
+            float run[ORC_CB];                                                            \
+            for (size_t j = 0; j < n; ++j) run[j] = 1.0f;                                 \
+            for (size_t t = 0; t < seq; ++t) {                                            \
+                const size_t r = t * channels + c0;                                       \
+                for (size_t j = 0; j < n; ++j) {                                          \
+                    run[j] = run[j] * a[r + j];                                           \
+                    decay[r + j] = cvt(run[j]);                                           \
+                }                                                                         \
+            }                                                                             \
+        }                                                                                 \
     }
-}
 
-void orc_gated_scan_f16(const float *g, const float *x, float *s, uint16_t *state,
-                        size_t seq, size_t channels) {
-    for (size_t c = 0; c < channels; ++c) {
-        float acc = orc_f16_to_f32(state[c]);
-        for (size_t t = 0; t < seq; ++t) {
-            acc = x[t * channels + c] + acc * g[t * channels + c];
-            s[t * channels + c] = acc;
-        }
-        state[c] = orc_f32_to_f16(acc);
+#define ORC_NARROW_SCAN(name, to_f32, from_f32)                                          \
+    void name(const float *g, const float *x, float *s, uint16_t *state, size_t seq,     \
+              size_t channels) {                                                          \
+        _Pragma("omp parallel for schedule(static) if (seq * channels > 65536)")          \
+        for (long gg = 0; gg < ORC_GROUPS(channels); ++gg) {                              \
+            const size_t c0 = (size_t)gg * ORC_CB, n = ORC_GROUP_WIDTH(gg, channels);     \
+            float acc[ORC_CB];                                                            \
+            for (size_t j = 0; j < n; ++j) acc[j] = to_f32(state[c0 + j]);                \
+            for (size_t t = 0; t < seq; ++t) {                                            \
+                const size_t r = t * channels + c0;                                       \
+                for (size_t j = 0; j < n; ++j) {                                          \
+                    acc[j] = x[r + j] + acc[j] * g[r + j];                                \
+                    s[r + j] = acc[j];                                                    \
+                }                                                                         \
+            }                                                                             \
+            for (size_t j = 0; j < n; ++j) state[c0 + j] = from_f32(acc[j]);              \
+        }                                                                                 \
     }
-}
 
-void orc_cumdecay_bf16(const float *a, uint16_t *decay, size_t seq, size_t channels) {
-    for (size_t c = 0; c < channels; ++c) {
-        float run = 1.0f;
-        for (size_t t = 0; t < seq; ++t) {
-            run = run * a[t * channels + c];
-            decay[t * channels + c] = orc_f32_to_bf16(run);
-        }
-    }
-}
-
-void orc_gated_scan_bf16(const float *g, const float *x, float *s, uint16_t *state,
-                         size_t seq, size_t channels) {
-    for (size_t c = 0; c < channels; ++c) {
-        float acc = orc_bf16_to_f32(state[c]);
-        for (size_t t = 0; t < seq; ++t) {
-            acc = x[t * channels + c] + acc * g[t * channels + c];
-            s[t * channels + c] = acc;
-        }
-        state[c] = orc_f32_to_bf16(acc);
-    }
-}
+/* fp32 running product / state, narrowed on store (gdn_sve.c's mixed-
+ * precision branches); the same channel grouping as the fp32 loops. */
+ORC_NARROW_DECAY(orc_cumdecay_f16, orc_f32_to_f16)
+ORC_NARROW_SCAN(orc_gated_scan_f16, orc_f16_to_f32, orc_f32_to_f16)
+ORC_NARROW_DECAY(orc_cumdecay_bf16, orc_f32_to_bf16)
+ORC_NARROW_SCAN(orc_gated_scan_bf16, orc_bf16_to_f32, orc_f32_to_bf16)
 
 /* ======================================================================== */
 /* Matrix-state delta rule                                                   */

@@ -65,6 +65,8 @@ HIP_SYMBOLS = (
     "kai_gdn_hip_init",
     "kai_gdn_hip_error_string",
     "kai_gdn_hip_check_device_error",
+    "kai_gdn_hip_prefill_workspace_bytes",
+    "kai_gdn_hip_device_bytes_held",
     "kai_gdn_hip_probe_sink_bytes",
     "kai_gdn_hip_probe_stream",
     "kai_gdn_hip_probe_mfma_bf16",
@@ -144,6 +146,8 @@ _SIGS = {
     "kai_gdn_hip_init": (_i, []),
     "kai_gdn_hip_error_string": (ctypes.c_char_p, [_i]),
     "kai_gdn_hip_check_device_error": (_i, []),
+    "kai_gdn_hip_prefill_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kai_gdn_hip_device_bytes_held": (_sz, []),
     "kai_gdn_hip_probe_sink_bytes": (_sz, []),
     "kai_gdn_hip_probe_stream": (_i, [_vp, _vp, _sz, _i, _vp, _vp]),
     "kai_gdn_hip_probe_mfma_bf16": (_i, [_i, _i, _vp, ctypes.POINTER(ctypes.c_ulonglong), _vp]),

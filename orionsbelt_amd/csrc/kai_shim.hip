@@ -367,6 +367,20 @@ extern "C" int kai_gdn_hip_check_device_error(void) {
     return (int)v;
 }
 
+extern "C" size_t kai_gdn_hip_prefill_workspace_bytes(int batch, int seq_len, int num_v_heads) {
+    if (batch <= 0 || seq_len <= 0 || num_v_heads <= 0) return 0;
+    return gdn::prefill_carry_bytes(batch, seq_len, num_v_heads);
+}
+
+extern "C" size_t kai_gdn_hip_device_bytes_held(void) {
+    DeviceCtx *c;
+    if (get_ctx(&c) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lk(c->mu);
+    size_t n = 256 + c->chunk_ws.cap;  // 256: the scan counter and error word
+    for (const DevBuf &s : c->stage) n += s.cap;
+    return n + 3 * c->scan_words * sizeof(unsigned long long);
+}
+
 extern "C" size_t kai_gdn_hip_probe_sink_bytes(void) {
     DeviceCtx *c;
     if (get_ctx(&c) != hipSuccess) return 0;

@@ -103,6 +103,29 @@ def test_ref_sweep_bit_identical(refkai):
             assert bits_equal(orc.gemv_f32(a, b, k, n), orc.gemv_f32(a, b, k, n, L=refkai))
 
 
+def test_ref_sve_narrow_sweep_bit_identical():
+    """fp16/bf16 decay and scan against the live gdn_sve.c build over the
+    same ragged sizes (channel counts off the oracle's 16-channel groups,
+    and sizes above its OpenMP threshold)."""
+    L = orc.ref_sve()
+    if L is None:
+        pytest.skip("oracle/_ref not built (needs the reference tree)")
+    rs = np.random.RandomState(8)
+    for seq in REF_SEQS:
+        for ch in REF_CHANS + [129, 255, 2051]:
+            n = seq * ch
+            a = rs.uniform(0.1, 1.5, n).astype(np.float32)
+            g = rs.uniform(-0.99, 0.99, n).astype(np.float32)
+            x = rs.uniform(-2, 2, n).astype(np.float32)
+            for fmt in ("f16", "bf16"):
+                st = rs.randint(0, 0x3C00, ch).astype(np.uint16)
+                assert np.array_equal(orc.cumdecay_narrow(a, seq, ch, fmt),
+                                      orc.cumdecay_narrow(a, seq, ch, fmt, L=L, prefix="gdn_")), (seq, ch, fmt)
+                r1 = orc.gated_scan_narrow(g, x, st, seq, ch, fmt)
+                r2 = orc.gated_scan_narrow(g, x, st, seq, ch, fmt, L=L, prefix="gdn_")
+                assert bits_equal(r1[0], r2[0]) and np.array_equal(r1[1], r2[1]), (seq, ch, fmt)
+
+
 def test_degenerate_writes_nothing():
     """seq=0 / channels=0 leave outputs and state untouched
     (test_kai_gdn.c:520-637)."""
