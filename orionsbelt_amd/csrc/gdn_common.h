@@ -93,6 +93,16 @@ template <bool NT> GDN_DEV void store_u2(void *p, u32x2_t v) {
     if constexpr (NT) __builtin_nontemporal_store(v, q);
     else *q = v;
 }
+template <bool NT> GDN_DEV u32x4_t load_u4(const void *p) {
+    const u32x4_t *q = reinterpret_cast<const u32x4_t *>(p);
+    if constexpr (NT) return __builtin_nontemporal_load(q);
+    else return *q;
+}
+template <bool NT> GDN_DEV void store_u4(void *p, u32x4_t v) {
+    u32x4_t *q = reinterpret_cast<u32x4_t *>(p);
+    if constexpr (NT) __builtin_nontemporal_store(v, q);
+    else *q = v;
+}
 
 // ---- device-wide hand-off between the blocks of one launch -----------------
 // The "last block finishes the reduction" pattern.  An agent-scope fence

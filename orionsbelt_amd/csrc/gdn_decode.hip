@@ -14,34 +14,59 @@
 // The two column reductions (k^T S and q^T S over the key dimension) are
 // per-thread partial sums over its rows followed by a reduction across the
 // RG row groups in LDS.
+#include <type_traits>
+
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
 namespace gdn {
 namespace {
 
-// State I/O.  NT selects non-temporal loads and stores: the state is touched
-// once per step, so it need not be kept in L2 or the Infinity Cache.
-template <int NARROW, bool NT> struct StateIO;
-template <bool NT> struct StateIO<kF32, NT> {
-    static GDN_DEV float4 load(const void *S, int64_t i) {
+// State I/O of V consecutive value columns.  NT selects non-temporal loads
+// and stores: the state is touched once per step, so it need not be kept in
+// L2 or the Infinity Cache.  fp32 moves 4 columns (16 bytes) per lane; fp16
+// 4 (8 bytes) or 8 (16 bytes).
+template <int NARROW, bool NT, int V> struct StateIO;
+template <bool NT> struct StateIO<kF32, NT, 4> {
+    typedef float4 Raw;
+    static GDN_DEV Raw load_raw(const void *S, int64_t i) {
         return load_f4<NT>(static_cast<const float *>(S) + i);
     }
-    static GDN_DEV void store(void *S, int64_t i, float4 v) {
-        store_f4<NT>(static_cast<float *>(S) + i, v);
+    static GDN_DEV void unpack(Raw v, float (&x)[4]) {
+        x[0] = v.x;
+        x[1] = v.y;
+        x[2] = v.z;
+        x[3] = v.w;
+    }
+    static GDN_DEV void load(const void *S, int64_t i, float (&x)[4]) { unpack(load_raw(S, i), x); }
+    static GDN_DEV void store(void *S, int64_t i, const float (&x)[4]) {
+        store_f4<NT>(static_cast<float *>(S) + i, make_float4(x[0], x[1], x[2], x[3]));
     }
 };
-template <bool NT> struct StateIO<kF16, NT> {
-    static GDN_DEV float4 load(const void *S, int64_t i) {
-        const u32x2_t u = load_u2<NT>(static_cast<const uint16_t *>(S) + i);
-        return make_float4(f16_to_f32((uint16_t)(u[0] & 0xFFFF)), f16_to_f32((uint16_t)(u[0] >> 16)),
-                           f16_to_f32((uint16_t)(u[1] & 0xFFFF)), f16_to_f32((uint16_t)(u[1] >> 16)));
+template <bool NT, int V> struct StateIO<kF16, NT, V> {
+    static_assert(V == 4 || V == 8, "fp16 state: 4 or 8 columns per lane");
+    static constexpr int W = V / 2;  // 32-bit words
+    typedef std::conditional_t<V == 8, u32x4_t, u32x2_t> Vec;
+    typedef Vec Raw;
+    static GDN_DEV Raw load_raw(const void *S, int64_t i) {
+        if constexpr (V == 8) return load_u4<NT>(static_cast<const uint16_t *>(S) + i);
+        else return load_u2<NT>(static_cast<const uint16_t *>(S) + i);
     }
-    static GDN_DEV void store(void *S, int64_t i, float4 v) {
-        u32x2_t u;
-        u[0] = (uint32_t)f32_to_f16_rne(v.x) | ((uint32_t)f32_to_f16_rne(v.y) << 16);
-        u[1] = (uint32_t)f32_to_f16_rne(v.z) | ((uint32_t)f32_to_f16_rne(v.w) << 16);
-        store_u2<NT>(static_cast<uint16_t *>(S) + i, u);
+    static GDN_DEV void unpack(Raw u, float (&x)[V]) {
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+            x[2 * j] = f16_to_f32((uint16_t)(u[j] & 0xFFFF));
+            x[2 * j + 1] = f16_to_f32((uint16_t)(u[j] >> 16));
+        }
+    }
+    static GDN_DEV void load(const void *S, int64_t i, float (&x)[V]) { unpack(load_raw(S, i), x); }
+    static GDN_DEV void store(void *S, int64_t i, const float (&x)[V]) {
+        Vec u;
+#pragma unroll
+        for (int j = 0; j < W; ++j)
+            u[j] = (uint32_t)f32_to_f16_rne(x[2 * j]) | ((uint32_t)f32_to_f16_rne(x[2 * j + 1]) << 16);
+        if constexpr (V == 8) store_u4<NT>(static_cast<uint16_t *>(S) + i, u);
+        else store_u2<NT>(static_cast<uint16_t *>(S) + i, u);
     }
 };
 
@@ -52,34 +77,77 @@ GDN_DEV float4 f4_add(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
+// Sum of acc over the row groups of the workgroup, for this thread's V
+// columns (the lanes rg * TPR + cgi of every wave hold the same columns).
+// SHFL: first within each wave by lane exchanges (xor TPR, 2 TPR, ... 32),
+// then the 4 wave sums in LDS, in wave order; otherwise every row group's
+// partial goes through LDS and each thread adds them in row-group order.
+// ALL: every thread receives the sum; otherwise only row group 0 does.
+template <int TPR, int RG, int V, bool SHFL, bool ALL>
+GDN_DEV void row_group_sum(float (&acc)[V], float *red, int rg, int cgi) {
+    if constexpr (SHFL) {
+        constexpr int W = 4;  // waves
+#pragma unroll
+        for (int m = TPR; m < 64; m <<= 1)
+#pragma unroll
+            for (int j = 0; j < V; ++j) acc[j] += __shfl_xor(acc[j], m);
+        const int wave = (int)threadIdx.x >> 6;
+        if (((int)threadIdx.x & 63) < TPR)
+#pragma unroll
+            for (int j = 0; j < V; ++j) red[(wave * TPR + cgi) * V + j] = acc[j];
+        __syncthreads();
+        if (!ALL && rg != 0) return;
+#pragma unroll
+        for (int j = 0; j < V; ++j) acc[j] = red[cgi * V + j];
+#pragma unroll
+        for (int w = 1; w < W; ++w)
+#pragma unroll
+            for (int j = 0; j < V; ++j) acc[j] += red[(w * TPR + cgi) * V + j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) red[(rg * TPR + cgi) * V + j] = acc[j];
+        __syncthreads();
+        if (!ALL && rg != 0) return;
+#pragma unroll
+        for (int j = 0; j < V; ++j) acc[j] = red[cgi * V + j];
+#pragma unroll
+        for (int r = 1; r < RG; ++r)
+#pragma unroll
+            for (int j = 0; j < V; ++j) acc[j] += red[(r * TPR + cgi) * V + j];
+    }
+}
+
 // MINW: minimum waves per SIMD the register allocation must allow.
 // NT:   non-temporal state traffic.
 // CS:   column splits -- CS workgroups per (sequence, head), each owning
 //       DV/CS value columns (the update of column j reads only column j).
-template <int DK, int DV, int NARROW, int MINW, bool NT, int CS>
+// SHFL: row-group reduction through lane exchanges first (row_group_sum).
+// V:    value columns per thread (StateIO).
+template <int DK, int DV, int NARROW, int V, int MINW, bool NT, int CS, bool SHFL>
 __global__ __launch_bounds__(256, MINW) void delta_decode_kernel(
     void *S, const float *__restrict__ q, const float *__restrict__ k,
     const float *__restrict__ v, const float *__restrict__ g, const float *__restrict__ beta,
     float *__restrict__ o, int Hv, int Hk, float q_scale) {
-    constexpr int TPR = DV / CS / 4;   // threads per state row (segment)
+    using IO = StateIO<NARROW, NT, V>;
+    constexpr int TPR = DV / CS / V;   // threads per state row (segment)
     constexpr int RG = 256 / TPR;      // row groups
     constexpr int RPT = DK / RG;       // rows per thread
-    static_assert(TPR >= 1 && RPT >= 1 && DK % RG == 0, "unsupported head shape");
-    __shared__ float4 red[RG][TPR];
+    static_assert(TPR >= 1 && RPT >= 1 && DK % RG == 0 && 64 % TPR == 0, "unsupported head shape");
+    __shared__ float red[(SHFL ? 4 : RG) * TPR * V];
 
     const int bh = blockIdx.x / CS;
     const int b = bh / Hv, h = bh % Hv;
     const int kh = h / (Hv / Hk);
     const int cgi = threadIdx.x % TPR;
     const int rg = threadIdx.x / TPR;
-    const int c = (blockIdx.x % CS) * (DV / CS) + cgi * 4;
+    const int c = (blockIdx.x % CS) * (DV / CS) + cgi * V;
     const int64_t sbase = (int64_t)bh * DK * DV;
     const float *kp = k + ((int64_t)b * Hk + kh) * DK;
     const float *qp = q + ((int64_t)b * Hk + kh) * DK;
 
-    float4 s[RPT];
+    float s[RPT][V];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = StateIO<NARROW, NT>::load(S, sbase + (int64_t)(rg + RG * i) * DV + c);
+    for (int i = 0; i < RPT; ++i) IO::load(S, sbase + (int64_t)(rg + RG * i) * DV + c, s[i]);
     float kj[RPT], qj[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -88,39 +156,51 @@ __global__ __launch_bounds__(256, MINW) void delta_decode_kernel(
     }
     const float decay = expf(g[bh]);
     const float bt = beta[bh];
-    const float4 vv = *reinterpret_cast<const float4 *>(v + (int64_t)bh * DV + c);
+    float vv[V];
+#pragma unroll
+    for (int j = 0; j < V; j += 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(v + (int64_t)bh * DV + c + j);
+        vv[j] = t.x;
+        vv[j + 1] = t.y;
+        vv[j + 2] = t.z;
+        vv[j + 3] = t.w;
+    }
 
     // S *= decay ; partial kv = sum_rows S[j][c] k[j]
-    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+    float kv[V];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-        s[i] = make_float4(s[i].x * decay, s[i].y * decay, s[i].z * decay, s[i].w * decay);
-        kv = f4_fma(kj[i], s[i], kv);
-    }
-    red[rg][cgi] = kv;
-    __syncthreads();
-    kv = red[0][cgi];
+    for (int j = 0; j < V; ++j) kv[j] = 0.f;
 #pragma unroll
-    for (int r = 1; r < RG; ++r) kv = f4_add(kv, red[r][cgi]);
-    const float4 delta = make_float4((vv.x - kv.x) * bt, (vv.y - kv.y) * bt,
-                                     (vv.z - kv.z) * bt, (vv.w - kv.w) * bt);
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            s[i][j] = s[i][j] * decay;
+            kv[j] = fmaf(kj[i], s[i][j], kv[j]);
+        }
+    row_group_sum<TPR, RG, V, SHFL, true>(kv, red, rg, cgi);
+    float delta[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) delta[j] = (vv[j] - kv[j]) * bt;
 
     // S += k (x) delta ; store S ; partial o = sum_rows S[j][c] q[j]
-    float4 op = make_float4(0.f, 0.f, 0.f, 0.f);
+    float op[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) op[j] = 0.f;
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-        s[i] = f4_fma(kj[i], delta, s[i]);
-        StateIO<NARROW, NT>::store(S, sbase + (int64_t)(rg + RG * i) * DV + c, s[i]);
-        op = f4_fma(qj[i], s[i], op);
+#pragma unroll
+        for (int j = 0; j < V; ++j) s[i][j] = fmaf(kj[i], delta[j], s[i][j]);
+        IO::store(S, sbase + (int64_t)(rg + RG * i) * DV + c, s[i]);
+#pragma unroll
+        for (int j = 0; j < V; ++j) op[j] = fmaf(qj[i], s[i][j], op[j]);
     }
     __syncthreads();  // everyone has read red[] for kv
-    red[rg][cgi] = op;
-    __syncthreads();
+    row_group_sum<TPR, RG, V, SHFL, false>(op, red, rg, cgi);
     if (rg == 0) {
-        float4 acc = red[0][cgi];
 #pragma unroll
-        for (int r = 1; r < RG; ++r) acc = f4_add(acc, red[r][cgi]);
-        *reinterpret_cast<float4 *>(o + (int64_t)bh * DV + c) = acc;
+        for (int j = 0; j < V; j += 4)
+            *reinterpret_cast<float4 *>(o + (int64_t)bh * DV + c + j) =
+                make_float4(op[j], op[j + 1], op[j + 2], op[j + 3]);
     }
 }
 
@@ -265,23 +345,38 @@ hipError_t launch_gdn_step_fused(const float *x, const float *conv_in, float *co
 }
 
 // Production configuration of the decode kernel, measured on MI355X over 24
-// rotating 128 MiB states (B=64, 32 heads, 128x128): 2 column splits with
-// non-temporal state traffic run 47.1 us per layer (5.77 TB/s) against
-// 55.4 us for one workgroup per head with cached traffic.
+// rotating states (B=64, 32 heads, 128x128):
+//  * fp32 state: 2 column splits with non-temporal state traffic, 47.1 us
+//    per layer (5.77 TB/s) against 55.4 us for one workgroup per head with
+//    cached traffic; lane exchanges in the reductions change nothing
+//    measurable (46.48 against 46.56 us), so the LDS reduction stays.
+//  * fp16 state: 2 column splits, lane exchanges first, 24.4 us (5.6 TB/s)
+//    against 24.9 us with the LDS reduction alone.  Rejected: 8 columns per
+//    lane (16-byte accesses, 29.0 us), one or four workgroups per head
+//    (25.7 / 38.8 us), and a persistent form that loads the next head's
+//    state while it works on the current one (27-32 us; fp32 48-52 us).
 constexpr int kDecodeMinW = 1;
 constexpr bool kDecodeNT = true;
-constexpr int kDecodeCS = 2;
+template <int NARROW> struct DecodeCfg;
+template <> struct DecodeCfg<kF32> { static constexpr int CS = 2; static constexpr bool SHFL = false; };
+template <> struct DecodeCfg<kF16> { static constexpr int CS = 2; static constexpr bool SHFL = true; };
 
-template <int NARROW, int MINW, bool NT, int CS>
+template <int NARROW>
 hipError_t launch_decode_cfg(void *S, const float *q, const float *k, const float *v,
                              const float *g, const float *beta, float *o, int B, int Hv, int Hk,
                              int dk, int dv, float q_scale, hipStream_t st) {
+    constexpr int CS = DecodeCfg<NARROW>::CS;
+    constexpr bool SHFL = DecodeCfg<NARROW>::SHFL;
+    // fits(DK, DV, cs, vec): at least 4 threads per row, row groups <= rows
+#define GDN_FITS(DK, DV, cs, vec) ((DV) / (cs) / (vec) >= 4 && 256 / ((DV) / (cs) / (vec)) <= (DK))
 #define GDN_DEC(DK, DV)                                                                      \
     if (dk == DK && dv == DV) {                                                              \
-        constexpr int cs = (CS * 1024 <= DK * DV && DV / CS >= 4) ? CS : 1;                  \
+        constexpr int vec = 4;                                                               \
+        constexpr int cs = GDN_FITS(DK, DV, CS, vec) ? CS : 1;                               \
+        static_assert(GDN_FITS(DK, DV, cs, vec), "decode shape");                            \
         dim3 grid((unsigned)(B * Hv * cs)), block(256);                                      \
-        delta_decode_kernel<DK, DV, NARROW, MINW, NT, cs><<<grid, block, 0, st>>>(            \
-            S, q, k, v, g, beta, o, Hv, Hk, q_scale);                                        \
+        delta_decode_kernel<DK, DV, NARROW, vec, kDecodeMinW, kDecodeNT, cs, SHFL>           \
+            <<<grid, block, 0, st>>>(S, q, k, v, g, beta, o, Hv, Hk, q_scale);               \
         return hipGetLastError();                                                            \
     }
     GDN_DEC(128, 128)
@@ -294,6 +389,7 @@ hipError_t launch_decode_cfg(void *S, const float *q, const float *k, const floa
     GDN_DEC(64, 32)
     GDN_DEC(32, 64)
 #undef GDN_DEC
+#undef GDN_FITS
     return hipErrorInvalidValue;
 }
 
@@ -303,11 +399,9 @@ hipError_t launch_delta_decode(int narrow_state, void *S, const float *q, const 
                                hipStream_t st) {
     if (B <= 0 || Hv <= 0) return hipSuccess;
     if (narrow_state == kF32)
-        return launch_decode_cfg<kF32, kDecodeMinW, kDecodeNT, kDecodeCS>(
-            S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
+        return launch_decode_cfg<kF32>(S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
     if (narrow_state == kF16)
-        return launch_decode_cfg<kF16, kDecodeMinW, kDecodeNT, kDecodeCS>(
-            S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
+        return launch_decode_cfg<kF16>(S, q, k, v, g, beta, o, B, Hv, Hk, dk, dv, q_scale, st);
     return hipErrorInvalidValue;
 }
 
