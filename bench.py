@@ -487,17 +487,40 @@ def hybrid_step_bytes(cfg, weight_bytes, B, pos):
     return weight_bytes + B * cfg.hidden * 2 + kv + state
 
 
-def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_STEPS, real_context=False):
+def hybrid_prefill_flop(cfg, B, T):
+    """Dense FLOPs of a T-token prefill of B sequences: every matmul but the
+    LM head (2 x params x tokens; the LM head runs on the last position
+    only), the causal attention (q k^T and p v over T (T + 1) / 2 pairs per
+    query head) and the chunked delta rule (the prefill metric's per-chunk
+    count)."""
+    attn = cfg.layers // cfg.attn_every
+    gdn = cfg.layers - attn
+    H, I = cfg.hidden, cfg.inter
+    conv_dim = 2 * cfg.gdn_k_heads * 128 + cfg.gdn_v_heads * 128
+    vdim = cfg.gdn_v_heads * 128
+    gdn_params = H * (conv_dim + vdim + 2 * cfg.gdn_v_heads) + vdim * H
+    attn_params = H * (cfg.attn_q_heads * 512 + 2 * cfg.attn_kv_heads * 256) + cfg.attn_q_heads * 256 * H
+    mlp = 3 * H * I
+    params = gdn * gdn_params + attn * attn_params + cfg.layers * mlp
+    gemm = 2 * params * B * T + 2 * H * cfg.vocab * B
+    att = attn * B * cfg.attn_q_heads * 2 * 2 * 256 * (T * (T + 1) // 2)
+    delta = gdn * B * cfg.gdn_v_heads * ((T + 63) // 64) * PF_FLOP_PER_CHUNK_HEAD
+    return gemm + att + delta
+
+
+def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_STEPS, kind="prefilled"):
     """the Qwen3.5-4B-shaped hybrid model (24 GDN + 8
     attention layers, int8 per-output-channel weights, fp16 activations and
     KV cache), greedy decoding of `steps` tokens per sequence after a
-    `context`-token context, batch 1 and 16.  The context is represented by
-    drawn states (KV caches, recurrent and conv states), not by running a
-    prefill; tokens never leave the device (each step's argmax feeds the
-    next).  Timed with HIP events around the whole loop.  With real_context
-    the context is built instead by stepping `context` uniform-random tokens
-    through the model (a prefill by decode steps, untimed), so that the
-    decode rate after a real context can be compared with the drawn one."""
+    `context`-token context, batch 1 and 16; tokens never leave the device
+    (each step's argmax feeds the next), the decode loop timed with HIP
+    events around it.  The context:
+      prefilled  a prefill of `context` uniform-random token ids per
+                 sequence (kai_gdn_hybrid_prefill), timed on its own: the
+                 time to first token (the prefill's last position yields the
+                 first generated token);
+      drawn      drawn states (KV caches, recurrent and conv states);
+      stepped    the random ids stepped through the decode loop (untimed)."""
     from orionsbelt_amd import hybrid as hb
     rows = []
     for B in batches:
@@ -509,7 +532,26 @@ def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_S
         logits = torch.empty(B, cfg.vocab, dtype=torch.float32, device="cuda")
         for _ in range(3):  # warm-up steps, then a fresh context
             m.step(tok, nxt, logits)
-        if real_context:
+        extra = {}
+        if kind == "prefilled":
+            gen = torch.Generator(device="cuda")
+            gen.manual_seed(2026)
+            prompt = torch.randint(0, cfg.vocab, (B, context), dtype=torch.int32, device="cuda", generator=gen)
+            m.prefill(prompt[:, :256].contiguous(), nxt, logits)  # warm-up: buffers, code
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            m.prefill(prompt, tok, logits)  # the first generated token lands in tok
+            e.record()
+            e.synchronize()
+            pms = s.elapsed_time(e)
+            flop = hybrid_prefill_flop(cfg, B, context)
+            extra = {"ttft_ms": round(pms, 2), "prefill_tokens_per_s": round(B * context / (pms * 1e-3), 1),
+                     "prefill_flop": int(flop), "prefill_achieved_tflops": round(flop / (pms * 1e-3) / 1e12, 1)}
+            extra["prefill_mfma_frac"] = round(extra["prefill_achieved_tflops"] / BF16_PEAK_TFLOPS, 4)
+            log(f"  B={B}: prefill of {context} tokens per sequence in {pms:.1f} ms")
+            del prompt
+        elif kind == "stepped":
             m.reset(B, 0, 7)
             gen = torch.Generator(device="cuda")
             gen.manual_seed(2026)
@@ -526,6 +568,7 @@ def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_S
             del prompt
         else:
             m.reset(B, context, 7)
+        assert m.position == context
         bufs = [tok, nxt]
 
         def run():
@@ -536,7 +579,7 @@ def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_S
         per = ms / steps
         nbytes = sum(hybrid_step_bytes(cfg, m.weight_bytes, B, context + i) for i in range(steps)) / steps
         gbs = nbytes / (per * 1e-3) / 1e9
-        rows.append({"batch": B, "context": context, "context_kind": "stepped" if real_context else "drawn",
+        rows.append({"batch": B, "context": context, "context_kind": kind, **extra,
                      "steps": steps, "ms_per_step": round(per, 4),
                      "tokens_per_s": round(B / (per * 1e-3), 1), "bytes_per_step": int(nbytes),
                      "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -544,10 +587,11 @@ def bench_hybrid(torch, timer, batches=(1, 16), context=HYB_CONTEXT, steps=HYB_S
         m.close()
         del m, logits, tok, nxt, bufs
         torch.cuda.empty_cache()
-    kind = "a stepped" if real_context else "a drawn"
+    what = {"prefilled": "a prefilled", "stepped": "a stepped", "drawn": "a drawn"}[kind]
     return {"workload": f"hybrid decode loop, Qwen3.5-4B shape (32 layers: 24 GDN + 8 attention, hidden 2560, "
                         f"inter 9216, vocab 151936), int8 weights, fp16 activations and KV cache, greedy, "
-                        f"{steps} steps after {kind} {context}-token context (BASELINE configs[4])",
+                        f"{steps} steps after {what} {context}-token context of uniform-random ids "
+                        f"(BASELINE configs[4]); ttft_ms: the prefill's time, the first token included",
             "runs": rows}
 
 
@@ -772,9 +816,11 @@ def run_profile(which, L, ob, torch, timer, steps, warmup):
         pro, rn = bench_layer_glue(L, ob, torch, timer)
         log(f"gating prologue: {pro}\ngated rmsnorm: {rn}")
     elif which == "hybrid":
-        log(f"hybrid: {bench_hybrid(torch, timer, steps=steps)}")
+        log(f"hybrid (prefilled context): {bench_hybrid(torch, timer, steps=steps)}")
+    elif which == "hybrid_drawn":
+        log(f"hybrid (drawn context): {bench_hybrid(torch, timer, steps=steps, kind='drawn')}")
     elif which == "hybrid_real":
-        log(f"hybrid (stepped context): {bench_hybrid(torch, timer, steps=steps, real_context=True)}")
+        log(f"hybrid (stepped context): {bench_hybrid(torch, timer, steps=steps, kind='stepped')}")
     else:
         conv, decay = bench_stream(L, ob, torch, timer, reps=steps)
         log(f"{which}: {conv if which == 'conv' else decay}")
@@ -794,7 +840,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip prefill/conv/decay lines")
     ap.add_argument("--profile", choices=["decode", "prefill", "prefill_f16", "layer", "conv", "cumdecay",
-                                          "hybrid", "hybrid_real"],
+                                          "hybrid", "hybrid_drawn", "hybrid_real"],
                     help="run only this workload (and a 256 MiB device copy that calibrates "
                          "HBM byte counters) for rocprofv3; prints no JSON line")
     args = ap.parse_args()
@@ -852,7 +898,7 @@ def main():
         secondary["gating_prologue"], secondary["gated_rmsnorm"] = bench_layer_glue(L, ob, torch, timer)
         log(f"gating prologue: {secondary['gating_prologue']}\n"
             f"gated rmsnorm: {secondary['gated_rmsnorm']}")
-        log("hybrid decode loop, B=1 and B=16 after 32K ...")
+        log("hybrid model: 32K-token prefill, then the decode loop, B=1 and B=16 ...")
         secondary["hybrid_decode"] = bench_hybrid(torch, timer)
         log(f"hybrid decode: {secondary['hybrid_decode']}")
 

@@ -262,12 +262,15 @@ int kai_run_gdn_w8a16_gemm_hip(const uint16_t *x, const int8_t *Wq, const float 
 /* The same GEMM on pre-tiled weights, the form the hybrid loop uses: every
  * wave load is one contiguous 1 KB (lm_head 389 MB at about 6.5 TB/s).
  * kai_run_gdn_w8_tile_hip rearranges row-major Wq [N][K] into Wt (the same
- * N * K bytes); N % 64 == 0, K % 256 == 0, 1 <= M <= 16.  Narrow matrices
- * split k across blocks and the last block of each 64-channel group sums
- * the splits in a fixed order (deterministic); the workspace holds the
- * partials and one counter per group, must be zeroed once before its first
- * use (each call leaves the counters at zero), and calls that share it must
- * not overlap.  0 workspace bytes: none needed. */
+ * N * K bytes); N % 64 == 0, K % 256 == 0.  For 1 <= M <= 16 (decode),
+ * narrow matrices split k across blocks and the last block of each
+ * 64-channel group sums the splits in a fixed order (deterministic); the
+ * workspace holds the partials and one counter per group, must be zeroed
+ * once before its first use (each call leaves the counters at zero), and
+ * calls that share it must not overlap.  0 workspace bytes: none needed.
+ * M > 16 (a prompt's rows: the counterpart of the reference e2e loop's
+ * M > 1 gemm_int8_neon, gdn_e2e_decode.c:606-612) takes the prefill GEMM,
+ * 128 x 128 output tiles on fp16 MFMA, and no workspace. */
 int kai_run_gdn_w8_tile_hip(const int8_t *Wq, int8_t *Wt, int N, int K, void *stream);
 size_t kai_gdn_w8a16_gemm_tiled_workspace_bytes(int M, int N, int K);
 int kai_run_gdn_w8a16_gemm_tiled_hip(const uint16_t *x, const int8_t *Wt, const float *scale,

@@ -68,6 +68,21 @@ int kai_gdn_hybrid_reset(kai_gdn_hybrid *m, int batch, int context, unsigned lon
  * before anything is launched; so is a step when the KV cache is full. */
 int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits,
                         void *stream);
+/* Prefill: start `batch` sequences from empty states and run the `length`
+ * prompt tokens of each (tokens [batch][length] int32, device) through
+ * every layer at once -- all positions of a sequence per launch: int8 GEMMs
+ * on MFMA for the projections, the conv and gating glue, the chunked delta
+ * rule (kai_run_gdn_chunk_delta_rule_bf16_f32_hip) and causal attention that
+ * writes the KV cache -- leaving the recurrent states, conv caches and KV
+ * caches where kai_gdn_hybrid_step reads them, at position `length`.  The
+ * next tokens (greedy) and logits of each sequence's last position are
+ * written as by kai_gdn_hybrid_step.  batch <= max_batch, 1 <= length <
+ * max_context.  The first call allocates the prefill's activation buffers
+ * for max_context positions (freed by kai_gdn_hybrid_destroy).  The
+ * reference e2e program's --prefill mode runs its prompt the same way
+ * (gdn_e2e_decode.c:2644-2700, with the M > 1 GEMM of :606-612). */
+int kai_gdn_hybrid_prefill(kai_gdn_hybrid *m, const int32_t *tokens, int batch, int length,
+                           int32_t *next, float *logits, void *stream);
 /* Current position (context + steps taken) and device bytes held. */
 int kai_gdn_hybrid_position(const kai_gdn_hybrid *m);
 size_t kai_gdn_hybrid_device_bytes(const kai_gdn_hybrid *m);

@@ -58,6 +58,7 @@ HIP_SYMBOLS = (
     "kai_gdn_hybrid_create",
     "kai_gdn_hybrid_reset",
     "kai_gdn_hybrid_step",
+    "kai_gdn_hybrid_prefill",
     "kai_gdn_hybrid_position",
     "kai_gdn_hybrid_device_bytes",
     "kai_gdn_hybrid_weight_bytes",
@@ -139,6 +140,7 @@ _SIGS = {
                                    ctypes.POINTER(_vp)]),
     "kai_gdn_hybrid_reset": (_i, [_vp, _i, _i, ctypes.c_ulonglong]),
     "kai_gdn_hybrid_step": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "kai_gdn_hybrid_prefill": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "kai_gdn_hybrid_position": (_i, [_vp]),
     "kai_gdn_hybrid_device_bytes": (_sz, [_vp]),
     "kai_gdn_hybrid_weight_bytes": (_sz, [_vp]),

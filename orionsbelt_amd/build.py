@@ -32,7 +32,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CC = os.environ.get("CC", "gcc")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-SOURCES = ["gdn_stream.hip", "gdn_decode.hip", "gdn_prefill.hip", "gdn_layer.hip", "gdn_state.hip", "gdn_model.hip", "gdn_hybrid.hip", "gdn_probe.hip", "kai_shim.hip"]
+SOURCES = ["gdn_stream.hip", "gdn_decode.hip", "gdn_prefill.hip", "gdn_layer.hip", "gdn_state.hip", "gdn_model.hip", "gdn_prefill_model.hip", "gdn_hybrid.hip", "gdn_probe.hip", "kai_shim.hip"]
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -67,6 +67,33 @@ GDN_DEV bf16x8_t as_bf16x8(u32x4_t w) { return __builtin_bit_cast(bf16x8_t, w); 
 
 GDN_DEV f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
 
+// ---- fp16 MFMA operands and int8 weights -------------------------------------
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Four int8 (one dword) -> four fp16, exactly.
+GDN_DEV void i8x4_to_f16(uint32_t w, f16x2_t &lo, f16x2_t &hi) {
+    const uint32_t t = w ^ 0x80808080u;  // u = q + 128 per byte
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, t, 0x04010400u);  // [u0, 0x64, u1, 0x64]
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, t, 0x04030402u);  // [u2, 0x64, u3, 0x64]
+    const f16x2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(f16x2_t, a) - bias;
+    hi = __builtin_bit_cast(f16x2_t, b) - bias;
+}
+// 16 int8 -> two MFMA operands of 8 fp16 (k = 0..7 and 8..15 of the 16).
+GDN_DEV void i8x16_to_f16(const u32x4_t &w, f16x8_t &k0, f16x8_t &k1) {
+    f16x2_t p[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) i8x4_to_f16(w[i], p[2 * i], p[2 * i + 1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        k0[2 * i] = p[i][0];
+        k0[2 * i + 1] = p[i][1];
+        k1[2 * i] = p[4 + i][0];
+        k1[2 * i + 1] = p[4 + i][1];
+    }
+}
+
 // ---- plain / non-temporal vector memory access ------------------------------
 typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
 

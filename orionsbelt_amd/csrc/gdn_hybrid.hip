@@ -26,6 +26,7 @@
 
 #include "gdn_common.h"
 #include "gdn_internal.h"
+#include "../../include/kai_gdn_hip.h"
 #include "../../include/kai_gdn_hybrid.h"
 
 namespace gdn {
@@ -150,27 +151,34 @@ __global__ __launch_bounds__(256) void addnorm_kernel(float *__restrict__ h, con
     }
 }
 
-// Attention prologue (Qwen3_5Attention.forward:656-681): block (slot, b),
+// Attention prologue (Qwen3_5Attention.forward:656-681): block (slot, row),
 // 256 threads = the head's dims.  Slots [0, Hq): query heads from qg
-// [B][Hq][512] (q = dims 0..255, gate = 256..511) -> q_norm -> rotary ->
-// q16; [Hq, Hq + Hkv): key heads -> k_norm -> rotary -> K cache at pos;
-// [Hq + Hkv, Hq + 2 Hkv): value heads -> V cache at pos.  Norm outputs are
-// rounded to fp16 (type_as) before the rotary embedding, which acts on dims
-// 0..63 with inv_freq[i] = 1 / theta^(2i / 64) and rotate_half.
+// [rows][Hq][512] (q = dims 0..255, gate = 256..511) -> q_norm -> rotary ->
+// q16 [rows][Hq][256]; [Hq, Hq + Hkv): key heads -> k_norm -> rotary -> K
+// cache; [Hq + Hkv, Hq + 2 Hkv): value heads -> V cache (and, with vT, the
+// transposed copy vT [Hkv][256][Tv] that the prefill attention reads).
+// Norm outputs are rounded to fp16 (type_as) before the rotary embedding,
+// which acts on dims 0..63 with inv_freq[i] = 1 / theta^(2i / 64) and
+// rotate_half.  Decode (seq < 0): row b is sequence b at position pos.
+// Prefill (seq >= 0): row t is position t of sequence seq.
 __global__ __launch_bounds__(256) void attn_prologue_kernel(
     const float *qg, const float *kx, const float *vx, const float *q_norm, const float *k_norm,
-    uint16_t *q16, uint16_t *Kc, uint16_t *Vc, int Hq, int Hkv, int Tmax, int pos, float theta,
-    float eps) {
+    uint16_t *q16, uint16_t *Kc, uint16_t *Vc, int Hq, int Hkv, int Tmax, int seq, int pos, float theta,
+    float eps, uint16_t *vT, int Tv) {
     __shared__ float red[4];
     __shared__ float rot[64];
-    const int slot = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int slot = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+    const int b = seq < 0 ? row : seq;
+    const int p = seq < 0 ? pos : row;
     if (slot >= Hq + Hkv) {  // value head: copy into the cache
         const int kv = slot - Hq - Hkv;
-        Vc[(((size_t)b * Hkv + kv) * Tmax + pos) * 256 + d] = f32_to_f16_rne(vx[((size_t)b * Hkv + kv) * 256 + d]);
+        const uint16_t v = f32_to_f16_rne(vx[((size_t)row * Hkv + kv) * 256 + d]);
+        Vc[(((size_t)b * Hkv + kv) * Tmax + p) * 256 + d] = v;
+        if (vT) vT[((size_t)kv * 256 + d) * Tv + p] = v;
         return;
     }
     const bool is_q = slot < Hq;
-    const float x = is_q ? qg[((size_t)b * Hq + slot) * 512 + d] : kx[((size_t)b * Hkv + (slot - Hq)) * 256 + d];
+    const float x = is_q ? qg[((size_t)row * Hq + slot) * 512 + d] : kx[((size_t)row * Hkv + (slot - Hq)) * 256 + d];
     const float *wn = is_q ? q_norm : k_norm;
     const float inv = 1.0f / sqrtf(block_sum(x * x, red) / 256.0f + eps);
     const float xn = f16_to_f32(f32_to_f16_rne(x * inv * (1.0f + wn[d])));
@@ -180,13 +188,55 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     if (d < 64) {
         const int i = d & 31;
         const float inv_freq = 1.0f / powf(theta, (float)(2 * i) / 64.0f);
-        const float f = inv_freq * (float)pos;
+        const float f = inv_freq * (float)p;
         const float c = cosf(f), s = sinf(f);
         y = d < 32 ? xn * c - rot[d + 32] * s : xn * c + rot[d - 32] * s;
     }
     const uint16_t o = f32_to_f16_rne(y);
-    if (is_q) q16[((size_t)b * Hq + slot) * 256 + d] = o;
-    else Kc[((size_t)b * Hkv + (slot - Hq)) * Tmax * 256 + kv_tiled_offset(pos, d)] = o;  // K is tiled
+    if (is_q) q16[((size_t)row * Hq + slot) * 256 + d] = o;
+    else Kc[((size_t)b * Hkv + (slot - Hq)) * Tmax * 256 + kv_tiled_offset(p, d)] = o;  // K is tiled
+}
+
+// The GDN output's gated RMSNorm for the prefill (the decode step's
+// step 4 in gdn_step_fused_kernel, on the prefill's bf16 output): rows of
+// 128, o bf16 [rows][128], z fp32 [rows][128] -> out16 fp16 =
+// w * (o / sqrt(mean(o^2) + eps)) * silu(z).  32 lanes per row, 4 values
+// each; 8 rows per block.
+__global__ __launch_bounds__(256) void prefill_gated_norm_kernel(const uint16_t *__restrict__ o,
+                                                                 const float *__restrict__ z,
+                                                                 const float *__restrict__ w,
+                                                                 uint16_t *__restrict__ out16, size_t rows,
+                                                                 float eps) {
+#pragma clang fp contract(off)
+    const size_t row = (size_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int c = (threadIdx.x & 31) * 4;
+    if (row >= rows) return;  // whole 32-lane groups leave together
+    const uint2 ob = *reinterpret_cast<const uint2 *>(o + row * 128 + c);
+    const float4 o4 = make_float4(bf16_to_f32((uint16_t)(ob.x & 0xFFFF)), bf16_to_f32((uint16_t)(ob.x >> 16)),
+                                  bf16_to_f32((uint16_t)(ob.y & 0xFFFF)), bf16_to_f32((uint16_t)(ob.y >> 16)));
+    float q2 = o4.x * o4.x + o4.y * o4.y + o4.z * o4.z + o4.w * o4.w;
+#pragma unroll
+    for (int s = 16; s >= 1; s >>= 1) q2 += __shfl_xor(q2, s, 32);
+    const float inv = 1.0f / sqrtf(q2 / 128.0f + eps);
+    const float4 zz = *reinterpret_cast<const float4 *>(z + row * 128 + c);
+    const float4 ww = *reinterpret_cast<const float4 *>(w + c);
+    auto gn = [&](float ov, float zv, float wv) { return (wv * (ov * inv)) * (zv / (1.0f + expf(-zv))); };
+    uint2 r;
+    r.x = (uint32_t)f32_to_f16_rne(gn(o4.x, zz.x, ww.x)) | ((uint32_t)f32_to_f16_rne(gn(o4.y, zz.y, ww.y)) << 16);
+    r.y = (uint32_t)f32_to_f16_rne(gn(o4.z, zz.z, ww.z)) | ((uint32_t)f32_to_f16_rne(gn(o4.w, zz.w, ww.w)) << 16);
+    *reinterpret_cast<uint2 *>(out16 + row * 128 + c) = r;
+}
+
+// conv weights [C][4] (HF) -> [4][C] (the kai conv's tap-major layout)
+__global__ __launch_bounds__(256) void conv_w_transpose_kernel(const float *__restrict__ w, float *__restrict__ wt,
+                                                               int C) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= C) return;
+    const float4 v = *reinterpret_cast<const float4 *>(w + (size_t)c * 4);
+    wt[c] = v.x;
+    wt[(size_t)C + c] = v.y;
+    wt[(size_t)2 * C + c] = v.z;
+    wt[(size_t)3 * C + c] = v.w;
 }
 
 // next[b] = the first index of the largest logit of row b.  Block (j, b)
@@ -274,6 +324,7 @@ struct Layer {
     float *ln_in = nullptr, *ln_post = nullptr;
     Mat in, out;  // GDN: [qkv | z | b | a], out_proj; attention: [q | k | v], o_proj
     float *conv_w = nullptr, *dt_bias = nullptr, *A_log = nullptr, *norm_w = nullptr;
+    float *conv_wt = nullptr;                    // conv_w tap-major [4][conv_dim], for the prefill
     float *q_norm = nullptr, *k_norm = nullptr;
     Mat gate_up, down;
     float *S = nullptr;                          // [B][Hv][128][128]
@@ -319,6 +370,14 @@ struct kai_gdn_hybrid {
     float *gemm_part = nullptr, *attn_ws = nullptr;
     uint32_t *gemm_cnt = nullptr;  // zero between launches
     uint32_t *norm_cnt = nullptr;  // the fused add + norm's grid counter, zero between launches
+    // prefill buffers, allocated by the first prefill for max_context rows
+    struct Prefill {
+        int rows = 0, tv = 0;  // capacity (positions) and the V^T row length
+        float *h = nullptr, *mix = nullptr, *qkv = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
+        float *conv = nullptr, *g = nullptr, *beta = nullptr, *kx = nullptr, *vx = nullptr, *hist = nullptr;
+        uint16_t *x16 = nullptr, *act16 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+        uint16_t *q16 = nullptr, *vT = nullptr;
+    } pf;
     std::vector<void *> allocs;
     size_t bytes = 0, weight_bytes = 0;
     int batch = 0, pos = 0;
@@ -487,6 +546,9 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
                                          {Hv, base + kAp}}, H, seed, tmp));
                 TRY(make_fused(m, L.out, {{H, base + kOut}}, m->value_dim, seed, tmp));
                 TRY(make_vec(m, &L.conv_w, (size_t)m->conv_dim * 4, seed, base + kConvW, 0.5f, 0.f));
+                TRY(alloc_t(m, &L.conv_wt, (size_t)m->conv_dim * 4));
+                conv_w_transpose_kernel<<<(m->conv_dim + 255) / 256, 256>>>(L.conv_w, L.conv_wt, m->conv_dim);
+                TRY(hipGetLastError());
                 TRY(make_vec(m, &L.dt_bias, Hv, seed, base + kDtBias, 0.5f, 1.0f));
                 TRY(make_vec(m, &L.A_log, Hv, seed, base + kALog, 1.3862944f, 1.3862944f));  // U(0, ln 16)
                 TRY(make_vec(m, &L.norm_w, 128, seed, base + kNormW, 0.1f, 1.0f));
@@ -578,8 +640,8 @@ hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     TRY(gemm(m, m->x16, L.in, segments({{m->qg, nq, nq}, {m->kx, nkv, nq + nkv}, {m->vx, nkv, nq + 2 * nkv}}),
              st));
     attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, B), 256, 0, st>>>(m->qg, m->kx, m->vx, L.q_norm, L.k_norm, m->q16,
-                                                                 L.Kc, L.Vc, Hq, Hkv, m->tmax, m->pos,
-                                                                 c.rope_theta, c.rms_eps);
+                                                                 L.Kc, L.Vc, Hq, Hkv, m->tmax, -1, m->pos,
+                                                                 c.rope_theta, c.rms_eps, nullptr, 0);
     TRY(hipGetLastError());
     // o * sigmoid(gate) -> fp16 in the span combine; gate = dims 256..511 of each qg head
     TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, nullptr, B, Hq, Hkv, m->tmax, m->pos + 1, 1.0f / 16.0f,
@@ -614,6 +676,127 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
     TRY(hipGetLastError());
     ++m->pos;
     m->parity ^= 1;
+    return hipSuccess;
+}
+
+// ---- prefill -------------------------------------------------------------------
+
+hipError_t prefill_alloc(kai_gdn_hybrid *m) {
+    if (m->pf.rows) return hipSuccess;
+    const kai_gdn_hybrid_config &c = m->cfg;
+    const size_t R = (size_t)c.max_context;
+    const int H = c.hidden, C = m->conv_dim, V = m->value_dim, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads,
+              Hq = c.attn_q_heads, Hkv = c.attn_kv_heads;
+    kai_gdn_hybrid::Prefill &p = m->pf;
+    p.tv = (int)((R + 63) / 64 * 64);
+    const size_t x16w = std::max({(size_t)H, (size_t)V, (size_t)Hq * 256});
+    TRY(alloc_t(m, &p.h, R * H));
+    TRY(alloc_t(m, &p.mix, R * H));
+    TRY(alloc_t(m, &p.qkv, R * std::max((size_t)C, (size_t)Hq * 512)));
+    TRY(alloc_t(m, &p.z, R * V));
+    TRY(alloc_t(m, &p.a, R * Hv));
+    TRY(alloc_t(m, &p.b, R * Hv));
+    TRY(alloc_t(m, &p.conv, R * C));
+    TRY(alloc_t(m, &p.g, R * Hv));
+    TRY(alloc_t(m, &p.beta, R * Hv));
+    TRY(alloc_t(m, &p.kx, R * Hkv * 256));
+    TRY(alloc_t(m, &p.vx, R * Hkv * 256));
+    TRY(alloc_t(m, &p.hist, (size_t)3 * C));
+    TRY(alloc_t(m, &p.x16, R * x16w));
+    TRY(alloc_t(m, &p.act16, R * c.inter));
+    TRY(alloc_t(m, &p.q, R * Hk * 128));
+    TRY(alloc_t(m, &p.k, R * Hk * 128));
+    TRY(alloc_t(m, &p.v, R * V));
+    TRY(alloc_t(m, &p.o, R * V));
+    TRY(alloc_t(m, &p.q16, R * Hq * 256));
+    TRY(alloc_t(m, &p.vT, (size_t)Hkv * 256 * p.tv));
+    // V^T past a prefill's length is read (with weight 0): keep it finite
+    TRY(hipMemset(p.vT, 0, (size_t)Hkv * 256 * p.tv * sizeof(uint16_t)));
+    p.rows = (int)R;
+    return hipDeviceSynchronize();
+}
+
+hipError_t w8p(const uint16_t *x, int ldx, const Mat &w, int M, const W8Out &o, hipStream_t st) {
+    return launch_w8p(x, ldx, w.q, w.s, M, w.N, w.K, o, st);
+}
+
+// One sequence's prompt through every layer at once: T rows of sequence b.
+// Leaves its states (recurrent state, conv cache, K/V cache) where the
+// decode step reads them and the normalised last row in x16 row b.
+hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, hipStream_t st) {
+    const kai_gdn_hybrid_config &c = m->cfg;
+    const int H = c.hidden, C = m->conv_dim, V = m->value_dim, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads,
+              Hq = c.attn_q_heads, Hkv = c.attn_kv_heads, I = c.inter;
+    kai_gdn_hybrid::Prefill &p = m->pf;
+    embed_kernel<<<T, 256, 0, st>>>(tokens, m->embed, p.h, H, c.vocab);
+    TRY(hipGetLastError());
+    addnorm_kernel<<<T, 256, 0, st>>>(p.h, nullptr, m->layers[0].ln_in, p.x16, H, c.rms_eps);
+    TRY(hipGetLastError());
+    W8Out swiglu{};
+    swiglu.mode = kW8SwiGLU;
+    swiglu.x16 = p.act16;
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+        Layer &L = m->layers[l];
+        if (!L.attn) {
+            TRY(w8p(p.x16, H, L.in, T, segments({{p.qkv, C, C}, {p.z, V, C + V}, {p.b, Hv, C + V + Hv},
+                                                  {p.a, Hv, C + V + 2 * Hv}}), st));
+            // the decode step's conv cache: the last four conv inputs
+            TRY(launch_conv_state_from_inputs(p.qkv, L.conv_state[0] + (size_t)b * C * 4, 1, T, C, st));
+            TRY(hipMemsetAsync(p.hist, 0, (size_t)3 * C * sizeof(float), st));
+            TRY(launch_conv_k4(p.qkv, L.conv_wt, p.conv, p.hist, T, C, true, st));
+            TRY(launch_gating_prologue(true, p.conv, p.a, p.b, L.A_log, L.dt_bias, p.q, p.k, p.v, p.g, p.beta, T,
+                                       Hk, Hv, st));
+            float *S = L.S + (size_t)b * Hv * 128 * 128;
+            TRY(hipMemsetAsync(S, 0, (size_t)Hv * 128 * 128 * sizeof(float), st));
+            const int rc = kai_run_gdn_chunk_delta_rule_bf16_f32_hip(p.q, p.k, p.v, p.g, p.beta, p.o, S, 1, T, Hv,
+                                                                    Hk, 1.0f / sqrtf(128.0f), st);
+            if (rc) return (hipError_t)rc;
+            const size_t rows = (size_t)T * Hv;
+            prefill_gated_norm_kernel<<<(unsigned)((rows + 7) / 8), 256, 0, st>>>(p.o, p.z, L.norm_w, p.x16, rows,
+                                                                                  c.rms_eps);
+            TRY(hipGetLastError());
+            TRY(w8p(p.x16, V, L.out, T, segments({{p.mix, H, H}}), st));
+        } else {
+            const int nq = Hq * 512, nkv = Hkv * 256;
+            TRY(w8p(p.x16, H, L.in, T, segments({{p.qkv, nq, nq}, {p.kx, nkv, nq + nkv}, {p.vx, nkv, nq + 2 * nkv}}),
+                    st));
+            attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, T), 256, 0, st>>>(p.qkv, p.kx, p.vx, L.q_norm, L.k_norm, p.q16,
+                                                                        L.Kc, L.Vc, Hq, Hkv, m->tmax, b, 0,
+                                                                        c.rope_theta, c.rms_eps, p.vT, p.tv);
+            TRY(hipGetLastError());
+            const size_t kvrow = (size_t)b * Hkv * m->tmax * 256;
+            TRY(launch_attn_prefill(p.q16, L.Kc + kvrow, p.vT, p.qkv + 256, nq, p.x16, T, Hq, Hkv, m->tmax, p.tv,
+                                    1.0f / 16.0f, st));
+            TRY(w8p(p.x16, Hq * 256, L.out, T, segments({{p.mix, H, H}}), st));
+        }
+        addnorm_kernel<<<T, 256, 0, st>>>(p.h, p.mix, L.ln_post, p.x16, H, c.rms_eps);
+        TRY(hipGetLastError());
+        TRY(w8p(p.x16, H, L.gate_up, T, swiglu, st));
+        TRY(w8p(p.act16, I, L.down, T, segments({{p.mix, H, H}}), st));
+        const float *next_norm = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : m->final_norm;
+        addnorm_kernel<<<T, 256, 0, st>>>(p.h, p.mix, next_norm, p.x16, H, c.rms_eps);
+        TRY(hipGetLastError());
+    }
+    return hipMemcpyAsync(m->x16 + (size_t)b * H, p.x16 + (size_t)(T - 1) * H, (size_t)H * sizeof(uint16_t),
+                          hipMemcpyDeviceToDevice, st);
+}
+
+hipError_t prefill(kai_gdn_hybrid *m, const int32_t *tokens, int batch, int T, int32_t *next, float *logits,
+                   hipStream_t st) {
+    const kai_gdn_hybrid_config &c = m->cfg;
+    TRY(prefill_alloc(m));
+    // a step may still run on another stream: the states below are rewritten
+    TRY(hipDeviceSynchronize());
+    m->batch = batch;
+    m->pos = 0;
+    m->parity = 0;
+    for (int b = 0; b < batch; ++b) TRY(prefill_seq(m, tokens + (size_t)b * T, b, T, st));
+    float *lg = logits ? logits : m->logits;
+    TRY(gemm(m, m->x16, m->lm, segments({{lg, c.vocab, c.vocab}}), st));
+    argmax_kernel<<<dim3(kArgBlocks, batch), 256, 0, st>>>(lg, next ? next : m->next, c.vocab, m->arg_part,
+                                                           m->arg_cnt);
+    TRY(hipGetLastError());
+    m->pos = T;
     return hipSuccess;
 }
 
@@ -733,6 +916,14 @@ extern "C" int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int
         return (int)hipErrorInvalidValue;
     if (m->pos >= m->cfg.max_context) return (int)hipErrorInvalidValue;  // the KV cache is full
     return (int)gdn::step(m, tokens, next, logits, (hipStream_t)stream);
+}
+
+extern "C" int kai_gdn_hybrid_prefill(kai_gdn_hybrid *m, const int32_t *tokens, int batch, int length,
+                                      int32_t *next, float *logits, void *stream) {
+    if (!m || !tokens || batch < 1 || batch > m->cfg.max_batch || length < 1 || length >= m->cfg.max_context ||
+        !device_ptr(tokens) || (next && !device_ptr(next)) || (logits && !device_ptr(logits)))
+        return (int)hipErrorInvalidValue;
+    return (int)gdn::prefill(m, tokens, batch, length, next, logits, (hipStream_t)stream);
 }
 
 extern "C" int kai_gdn_hybrid_position(const kai_gdn_hybrid *m) { return m ? m->pos : -1; }

@@ -165,6 +165,22 @@ hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, in
                       W8fShape shape = W8fShape{0, 0, 0});
 // Per-output-channel symmetric int8 quantisation of W[N][K] fp32.
 hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, int K, hipStream_t st);
+
+// ---- hybrid model prefill (gdn_prefill_model.hip) ---------------------------
+
+// The model's int8 GEMM for many rows: x [M][ldx] fp16 (16-byte aligned
+// rows), weights tiled by launch_w8f_tile (N % 64 == 0, K % 64 == 0); `out`
+// as for launch_w8f in kW8Segments or kW8SwiGLU mode.
+hipError_t launch_w8p(const uint16_t *x, int ldx, const int8_t *W, const float *scale, int M, int N, int K,
+                      const W8Out &out, hipStream_t st);
+// Causal attention of one sequence's T positions: q16 [T][Hq][256] fp16,
+// Kc [Hkv][Tmax][256] tiled by 16 positions (kv_tiled_offset), vT
+// [Hkv][256][Tv] fp16 (V transposed; Tv % 64 == 0, Tv >= T, finite past T),
+// gate rows [T] of gate_row floats (head h's gate at h * 512 + d);
+// out16 [T][Hq][256] = fp16(softmax(q k^T * scaling) v * sigmoid(gate)).
+hipError_t launch_attn_prefill(const uint16_t *q16, const uint16_t *Kc, const uint16_t *vT, const float *gate,
+                               int gate_row, uint16_t *out16, int T, int Hq, int Hkv, int Tmax, int Tv,
+                               float scaling, hipStream_t st);
 // Attention decode over an fp16 KV cache (head_dim 256, Hq / Hkv <= 4):
 // out [B][Hq][256] fp32; `workspace` holds attn_workspace_bytes(B, Hq, L),
 // or attn_workspace_bytes_tiled(B, Hq, L) for a k_tiled launch (whose

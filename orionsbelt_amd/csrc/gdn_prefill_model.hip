@@ -1,0 +1,349 @@
+// gdn_prefill_model.hip -- the many-row matmul and the causal attention of
+// the hybrid model's prefill (include/kai_gdn_hybrid.h) for gfx950.
+//
+// Prefill GEMM: y[m][n] = scale[n] sum_k x[m][k] Wq[n][k] for M rows (a
+// whole prompt), on the same pre-tiled int8 weights as the decode GEMM
+// (gdn_model.hip, w8f_tile_kernel) -- the M > 1 counterpart of the
+// reference e2e loop's gemm_int8_neon (gdn_e2e_decode.c:606-612).  Block
+// tile 128 rows x 128 channels, k in steps of 64, 4 waves as 2 x 2 (64 x 64
+// each, 16 MFMA tiles of 16x16x32 fp16).  Per step a thread stages 4 x 16
+// bytes of activations and 2 x 16 bytes of weights in registers while the
+// waves multiply the previous step from LDS; the weights are widened to
+// fp16 (exactly) on their way into LDS, so every MFMA operand is one
+// 16-byte LDS read.  LDS rows are 64 k + 8 pad halves (144 bytes): the
+// 16-byte reads of 8 consecutive rows then cover the 32 banks once.  The
+// weight is the A operand, as in the decode GEMM, so the epilogue has the
+// same shape: a lane holds 4 consecutive channels of one row (one 16-byte
+// store; SwiGLU pairs gate and up lanes 32 apart).
+//
+// Prefill attention: Qwen3_5Attention's causal softmax(q k^T / 16) v with
+// the sigmoid output gate (modeling_qwen3_5.py:629-701), GQA, head dim 256,
+// on the model's fp16 KV cache.  Block (32 positions, kv head), 8 waves: wave
+// w takes query head kv * rep + (w % 4) at positions +16 (w / 4) .. +15 and
+// walks the keys in blocks of 64 shared through LDS.  Scores on fp16 MFMA
+// 16x16x32 as S^T = K q^T (A = the 16-key x 32-dim fragment, which is one
+// contiguous 1 KB of the tiled K cache; B = the wave's queries), online
+// softmax in exp2 per query column, then O^T = V^T P^T with P taken from the
+// score registers as the B operand (the 8 keys a lane holds, 4g .. 4g+3 and
+// 16 + 4g .. 16 + 4g+3, permute the k index of both operands alike) and
+// V^T read from a transposed copy of V written by the prologue.
+#include "gdn_common.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+namespace {
+
+constexpr int kPBM = 128;    // activation rows per block
+constexpr int kPBN = 128;    // channels per block (two 64-channel groups of the tiled weights)
+constexpr int kPPitch = 72;  // halves per LDS row: 64 k + 8
+
+struct W8pStage {
+    uint16_t x[kPBM * kPPitch];
+    uint16_t w[kPBN * kPPitch];
+};
+
+__global__ __launch_bounds__(256, 2) void w8p_kernel(const uint16_t *__restrict__ X, int ldx,
+                                                     const int8_t *__restrict__ W, const float *__restrict__ scale,
+                                                     int M, int N, int K, W8Out out) {
+    __shared__ __align__(16) W8pStage st[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int wm = wave & 1, wn = wave >> 1;  // rows 64 wm .., channels 64 wn .. of the block
+    const int n0 = blockIdx.x * kPBN, m0 = blockIdx.y * kPBM;
+    const int steps = K / 64;
+    const bool two = n0 + 64 < N;        // the block's second channel group exists
+    const bool active = wn == 0 || two;  // this wave's channels exist (wave-uniform)
+
+    // staging: activation chunk c = tid + 256 i is row c / 8, k 8 (c % 8) .. +7
+    // (rows past M read row M - 1, never stored); weight chunk tid of each
+    // group's 4 KB step block (tile tid / 64, tiled lane tid % 64)
+    const uint16_t *xp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i;
+        xp[i] = X + (size_t)min(m0 + (c >> 3), M - 1) * ldx + (c & 7) * 8;
+    }
+    const int8_t *wp0 = W + (size_t)(n0 / 64) * steps * 4096 + tid * 16;
+    const int8_t *wp1 = two ? wp0 + (size_t)steps * 4096 : wp0;
+    u32x4_t xr[4], wr[2];
+    auto gload = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[i] = *reinterpret_cast<const u32x4_t *>(xp[i] + s * 64);
+        wr[0] = *reinterpret_cast<const u32x4_t *>(wp0 + (size_t)s * 4096);
+        wr[1] = *reinterpret_cast<const u32x4_t *>(wp1 + (size_t)s * 4096);
+    };
+    const int wq = tid & 63, wrow = 16 * (tid >> 6) + (wq & 15), wk = 16 * (wq >> 4);
+    auto lstore = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i;
+            *reinterpret_cast<u32x4_t *>(&st[b].x[(c >> 3) * kPPitch + (c & 7) * 8]) = xr[i];
+        }
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+            f16x8_t lo, hi;
+            i8x16_to_f16(wr[gi], lo, hi);
+            uint16_t *d = &st[b].w[(64 * gi + wrow) * kPPitch + wk];
+            *reinterpret_cast<f16x8_t *>(d) = lo;
+            *reinterpret_cast<f16x8_t *>(d + 8) = hi;
+        }
+    };
+
+    f32x4_t acc[4][4];  // [channel tile j][row tile i]
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][i] = zero4();
+    auto compute = [&](int b) {
+        if (!active) return;
+#pragma unroll
+        for (int kk = 0; kk < 64; kk += 32) {
+            f16x8_t a[4], bx[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                a[j] = *reinterpret_cast<const f16x8_t *>(&st[b].w[(64 * wn + 16 * j + r) * kPPitch + kk + 8 * g]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                bx[i] = *reinterpret_cast<const f16x8_t *>(&st[b].x[(64 * wm + 16 * i + r) * kPPitch + kk + 8 * g]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], bx[i], acc[j][i], 0, 0, 0);
+        }
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        if (s + 1 < steps) gload(s + 1);
+        compute(s & 1);
+        if (s + 1 < steps) lstore((s + 1) & 1);
+        __syncthreads();
+    }
+    if (!active) return;
+
+    // C lane (g, r) of tile (j, i): channels n .. n+3 (n = n0 + 64 wn + 16 j
+    // + 4 g) of row m0 + 64 wm + 16 i + r
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 64 * wn + 16 * j + 4 * g;
+        const f32x4_t sc = *reinterpret_cast<const f32x4_t *>(scale + n);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = m0 + 64 * wm + 16 * i + r;
+            const f32x4_t y = acc[j][i] * sc;
+            if (out.mode == kW8SwiGLU) {
+                // tile rows 0..7 are gate channels 8t .. 8t+7, rows 8..15 the up channels
+                f32x4_t up;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) up[e] = __shfl_xor(y[e], 32);
+                if (g < 2 && row < M) {
+                    uint32_t hv[2];
+#pragma unroll
+                    for (int e = 0; e < 4; e += 2) {
+                        const float a = y[e] / (1.0f + expf(-y[e])) * up[e];
+                        const float b = y[e + 1] / (1.0f + expf(-y[e + 1])) * up[e + 1];
+                        hv[e / 2] = (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+                    }
+                    const int cc = (n0 + 64 * wn + 16 * j) / 2 + 4 * g;
+                    *reinterpret_cast<uint2 *>(out.x16 + (size_t)row * (N / 2) + cc) = make_uint2(hv[0], hv[1]);
+                }
+            } else if (row < M && n < out.seg[out.nseg - 1].n_end) {  // channels past the last segment: padding
+                int sgi = 0, nb = 0;
+#pragma unroll
+                for (int q = 0; q < kW8MaxSegs - 1; ++q)
+                    if (q < out.nseg - 1 && n >= out.seg[q].n_end) {
+                        sgi = q + 1;
+                        nb = out.seg[q].n_end;
+                    }
+                float *dst = out.seg[0].dst;
+                int ld = out.seg[0].ld;
+#pragma unroll
+                for (int q = 1; q < kW8MaxSegs; ++q)
+                    if (q == sgi) {
+                        dst = out.seg[q].dst;
+                        ld = out.seg[q].ld;
+                    }
+                *reinterpret_cast<f32x4_t *>(dst + (size_t)row * ld + (n - nb)) = y;
+            }
+        }
+    }
+}
+
+// ---- causal prefill attention ------------------------------------------------
+
+constexpr int kApQ = 32;       // positions per block
+constexpr int kApK = 64;       // keys per step
+constexpr int kApD = 256;      // head dim
+constexpr int kApVPitch = 68;  // halves per V^T LDS row: 64 keys + 4 (8-byte reads of 16 rows hit 32 banks)
+
+__global__ __launch_bounds__(512) void attn_prefill_kernel(
+    const uint16_t *__restrict__ q16, const uint16_t *__restrict__ Kc, const uint16_t *__restrict__ vT,
+    const float *__restrict__ gate, int gate_row, uint16_t *__restrict__ out16, int T, int Hq, int Hkv, int Tmax,
+    int Tv, float sc_log2) {
+    __shared__ __align__(16) uint16_t ks[2][kApK * kApD];        // tiled as in the cache
+    __shared__ __align__(16) uint16_t vs[2][kApD * kApVPitch];  // [dim][key]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
+    const int kv = blockIdx.y;
+    const int rep = Hq / Hkv;
+    const bool live = (wave & 3) < rep;                   // wave-uniform
+    const int h = kv * rep + min(wave & 3, rep - 1);
+    const int qpos = qb * kApQ + 16 * (wave >> 2) + r;    // this lane's query (B column r)
+
+    // the wave's queries as B operands: dims 32 j + 8 g .. +7 of query r
+    f16x8_t qf[8];
+    {
+        const uint16_t *qp = q16 + ((size_t)min(qpos, T - 1) * Hq + h) * kApD + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qf[j] = *reinterpret_cast<const f16x8_t *>(qp + 32 * j);
+    }
+    f32x4_t o[16];  // O^T: dims 16 dt + 4 g + e of query r
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) o[dt] = zero4();
+    float m = -INFINITY, l = 0.f;  // running max (log2 units, all lanes of column r agree); partial sum
+
+    const int kend = min(T, qb * kApQ + kApQ);
+    const int nkb = (kend + kApK - 1) / kApK;
+    const uint16_t *kbase = Kc + (size_t)kv * Tmax * kApD;
+    const uint16_t *vbase = vT + (size_t)kv * kApD * Tv;
+    // staging: K group tid / 128 (16 keys, 8 KB contiguous), 64 bytes at
+    // (tid % 128) * 64; V^T row tid / 2, keys 32 (tid % 2) .. +31
+    u32x4_t kr[4], vr[4];
+    const int kgrp = tid >> 7, koff = (tid & 127) * 32;
+    const int vrow = tid >> 1, vhalf = (tid & 1) * 32;
+    auto gload = [&](int kb) {
+        // a group past the cache rows reads the last group instead (its
+        // keys are masked: every key >= T lies after every query)
+        const int t0 = min(kb * kApK + 16 * kgrp, Tmax - 16);
+        const uint16_t *kp = kbase + (size_t)t0 * kApD + koff;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const u32x4_t *>(kp + 8 * i);
+        const uint16_t *vp = vbase + (size_t)vrow * Tv + kb * kApK + vhalf;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[i] = *reinterpret_cast<const u32x4_t *>(vp + 8 * i);
+    };
+    auto lstore = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x4_t *>(&ks[b][kgrp * 4096 + koff + 8 * i]) = kr[i];
+        uint16_t *vd = &vs[b][vrow * kApVPitch + vhalf];  // 8-byte aligned rows
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *reinterpret_cast<u32x2_t *>(vd + 8 * i) = u32x2_t{vr[i][0], vr[i][1]};
+            *reinterpret_cast<u32x2_t *>(vd + 8 * i + 4) = u32x2_t{vr[i][2], vr[i][3]};
+        }
+    };
+    auto step = [&](int b, int kb) {
+        if (!live) return;
+        // S^T tiles: keys kb * 64 + 16 kt + 4 g + e, query r
+        f32x4_t s[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            s[kt] = zero4();
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    *reinterpret_cast<const f16x8_t *>(&ks[b][kt * 4096 + j * 512 + lane * 8]), qf[j], s[kt], 0, 0,
+                    0);
+        }
+        float mx = m;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int key = kb * kApK + 16 * kt + 4 * g + e;
+                const float v = key <= qpos ? s[kt][e] * sc_log2 : -INFINITY;
+                s[kt][e] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // key 0 precedes every query, so the first step leaves mx finite
+        const float alpha = __builtin_amdgcn_exp2f(m - mx);
+        m = mx;
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
+        f16x8_t pb[2];  // P^T fragments: keys 32 ks + {4g .. 4g+3, 16 + 4g .. 16 + 4g+3}
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p = __builtin_amdgcn_exp2f(s[kt][e] - mx);
+                l += p;
+                pb[kt >> 1][(kt & 1) * 4 + e] = (_Float16)p;
+            }
+#pragma unroll
+        for (int ksn = 0; ksn < 2; ++ksn)
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) {
+                const uint16_t *vp = &vs[b][(16 * dt + r) * kApVPitch + 32 * ksn + 4 * g];
+                const u32x2_t lo = *reinterpret_cast<const u32x2_t *>(vp);
+                const u32x2_t hi = *reinterpret_cast<const u32x2_t *>(vp + 16);
+                const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), pb[ksn], o[dt], 0, 0, 0);
+            }
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+        if (kb + 1 < nkb) gload(kb + 1);
+        step(kb & 1, kb);
+        if (kb + 1 < nkb) lstore((kb + 1) & 1);
+        __syncthreads();
+    }
+    if (!live || qpos >= T) return;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = 1.0f / l;
+    const float *gp = gate + (size_t)qpos * gate_row + (size_t)h * 512;
+    uint16_t *op = out16 + ((size_t)qpos * Hq + h) * kApD;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+        const int d = 16 * dt + 4 * g;
+        const f32x4_t gt = *reinterpret_cast<const f32x4_t *>(gp + d);
+        uint32_t hv[2];
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+            const float a = (o[dt][e] * inv) * (1.0f / (1.0f + expf(-gt[e])));
+            const float b = (o[dt][e + 1] * inv) * (1.0f / (1.0f + expf(-gt[e + 1])));
+            hv[e / 2] = (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+        }
+        *reinterpret_cast<uint2 *>(op + d) = make_uint2(hv[0], hv[1]);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_w8p(const uint16_t *x, int ldx, const int8_t *W, const float *scale, int M, int N, int K,
+                      const W8Out &out, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    if (N <= 0 || N % 64 || K <= 0 || K % 64 || ldx < K || ldx % 8 || (uintptr_t)x % 16 ||
+        (out.mode != kW8Segments && out.mode != kW8SwiGLU) || (out.mode == kW8SwiGLU && (N % 16 || !out.x16)) ||
+        (out.mode == kW8Segments && (out.nseg < 1 || out.nseg > kW8MaxSegs)))
+        return hipErrorInvalidValue;
+    const long long mb = (M + kPBM - 1) / kPBM;
+    if (mb > 65535) return hipErrorInvalidValue;
+    w8p_kernel<<<dim3((unsigned)((N + kPBN - 1) / kPBN), (unsigned)mb), 256, 0, st>>>(x, ldx, W, scale, M, N, K, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_prefill(const uint16_t *q16, const uint16_t *Kc, const uint16_t *vT, const float *gate,
+                               int gate_row, uint16_t *out16, int T, int Hq, int Hkv, int Tmax, int Tv,
+                               float scaling, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    if (Hkv <= 0 || Hq % Hkv || Hq / Hkv > 4 || Tmax % 16 || Tmax < T || Tv % kApK || Tv < T)
+        return hipErrorInvalidValue;
+    const float sc_log2 = scaling * 1.4426950408889634f;
+    attn_prefill_kernel<<<dim3((unsigned)((T + kApQ - 1) / kApQ), (unsigned)Hkv), 512, 0, st>>>(
+        q16, Kc, vT, gate, gate_row, out16, T, Hq, Hkv, Tmax, Tv, sc_log2);
+    return hipGetLastError();
+}
+
+}  // namespace gdn

@@ -771,11 +771,18 @@ extern "C" size_t kai_gdn_w8a16_gemm_tiled_workspace_bytes(int M, int N, int K) 
 extern "C" int kai_run_gdn_w8a16_gemm_tiled_hip(const uint16_t *x, const int8_t *Wt, const float *scale, float *y,
                                                 int M, int N, int K, void *workspace, size_t workspace_bytes,
                                                 void *stream) {
-    if (M < 0 || M > 16 || N < 0 || K <= 0 || N % 64 || K % 256) return (int)hipErrorInvalidValue;
+    if (M < 0 || N < 0 || K <= 0 || N % 64 || K % 256) return (int)hipErrorInvalidValue;
     if (M == 0 || N == 0) return 0;
     if (!x || !Wt || !scale || !y) return (int)hipErrorInvalidValue;
     if (!aligned(x, 16) || !aligned(Wt, 16) || !aligned(scale, 16) || !aligned(y, 16))
         return (int)hipErrorInvalidValue;
+    if (M > 16) {  // the prefill's many-row GEMM (no workspace)
+        gdn::W8Out o{};
+        o.seg[0] = gdn::W8Seg{y, N, N};
+        o.nseg = 1;
+        o.mode = gdn::kW8Segments;
+        return (int)gdn::launch_w8p(x, K, Wt, scale, M, N, K, o, (hipStream_t)stream);
+    }
     const size_t need = w8f_ws_bytes(M, N, K);
     if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 256))) return (int)hipErrorInvalidValue;
     float *part = static_cast<float *>(workspace);

@@ -50,6 +50,20 @@ class HybridModel:
             self._h, tokens.data_ptr(), None if next_tokens is None else next_tokens.data_ptr(),
             None if logits is None else logits.data_ptr(), st), "kai_gdn_hybrid_step")
 
+    def prefill(self, tokens, next_tokens=None, logits=None, stream=None) -> None:
+        """tokens [batch][length] int32 on the device: start `batch`
+        sequences from empty states and run their prompts; next_tokens and
+        logits of the last position as for step."""
+        assert tokens.is_cuda and tokens.dtype.itemsize == 4 and tokens.dim() == 2 and tokens.is_contiguous()
+        batch, length = tokens.shape
+        for t, n in ((next_tokens, batch), (logits, batch * self.cfg.vocab)):
+            assert t is None or (t.is_cuda and t.is_contiguous() and t.numel() >= n)
+        st = stream.cuda_stream if stream is not None else None
+        check(lib().kai_gdn_hybrid_prefill(
+            self._h, tokens.data_ptr(), batch, length, None if next_tokens is None else next_tokens.data_ptr(),
+            None if logits is None else logits.data_ptr(), st), "kai_gdn_hybrid_prefill")
+        self.batch = batch
+
     @property
     def position(self) -> int:
         return lib().kai_gdn_hybrid_position(self._h)

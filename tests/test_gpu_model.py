@@ -94,7 +94,11 @@ def gpu_gemm_tiled(L, x16, q, s, reps=1):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (5, 2560, 4096), (16, 12352, 2560), (3, 2560, 9216),
-                                   (16, 1024, 512), (1, 18432, 2560)])
+                                   (16, 1024, 512), (1, 18432, 2560),
+                                   # M > 16: the prefill GEMM (128-row blocks: ragged row tails,
+                                   # a half channel block when N % 128 == 64, the 4B shapes)
+                                   (17, 64, 256), (100, 192, 512), (300, 2560, 9216), (1000, 12352, 2560),
+                                   (129, 18432, 2560)])
 def test_w8a16_gemm_tiled_vs_oracle(L, M, N, K):
     """The tiled-weight GEMM (the hybrid loop's): against the oracle at the
     row-major GEMM's bar, deterministic over calls that share one workspace
@@ -119,7 +123,8 @@ def test_w8a16_gemm_tiled_rejects_bad_args(L):
     u = empty((16 * 4096,), torch.float32)
     assert L.kai_run_gdn_w8_tile_hip(P(t), P(u), 48, 256, stream()) != 0          # N % 64
     fn = L.kai_run_gdn_w8a16_gemm_tiled_hip
-    assert fn(P(t), P(u), P(t), P(t), 17, 64, 256, P(t), 1 << 20, stream()) != 0  # M > 16
+    assert fn(P(t), P(u), P(t), P(t), -1, 64, 256, P(t), 1 << 20, stream()) != 0  # M < 0
+    assert fn(P(t), P(u), P(t), P(t), 17, 64, 200, P(t), 1 << 20, stream()) != 0  # K % 256 (many rows)
     assert fn(P(t), P(u), P(t), P(t), 1, 48, 256, P(t), 1 << 20, stream()) != 0   # N % 64
     assert fn(P(t), P(u), P(t), P(t), 1, 64, 200, P(t), 1 << 20, stream()) != 0   # K % 256
     nb = L.kai_gdn_w8a16_gemm_tiled_workspace_bytes(4, 2560, 4096)
