@@ -89,6 +89,16 @@ int kai_run_gdn_gated_scan_bf16_hip(const float *g, const float *x, float *s,
                                     uint16_t *state, size_t seq, size_t channels,
                                     void *stream);
 
+/* GDN-2 decoupled-gating scan (gdn2_gated_scan_f32, gdn_sve.h:83-86):
+ *   s[t][c] = w[t][c] * x[t][c] + s[t-1][c] * (g[t][c] * b[t][c]),
+ * both products rounded before the sum (gdn_sve.c:861-874); state[]
+ * carried across calls.  The products are formed into library-owned device
+ * buffers (2 * seq * channels floats, kept for later calls), then the
+ * gated scan runs over them. */
+int kai_run_gdn2_gated_scan_f32_hip(const float *g, const float *b_gate, const float *w_gate,
+                                    const float *x, float *s, float *state, size_t seq,
+                                    size_t channels, void *stream);
+
 /* ---- matrix-state gated delta rule, single-token decode ------------------
  * Replaces the OpenCL gdn_delta_rule_decode (gpu/gdn_gpu_kernels.cl:158-206)
  * and its host oracle ref_delta_rule (gpu/gdn_gpu_validate.c:100-118), with

@@ -86,6 +86,26 @@ void orc_gated_scan_f32(const float *g, const float *x, float *s, float *state,
     }
 }
 
+void orc_gdn2_gated_scan_f32(const float *g, const float *b, const float *w, const float *x, float *s,
+                             float *state, size_t seq, size_t channels) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (seq * channels > 65536)
+#endif
+    for (long gg = 0; gg < ORC_GROUPS(channels); ++gg) {
+        const size_t c0 = (size_t)gg * ORC_CB, n = ORC_GROUP_WIDTH(gg, channels);
+        float acc[ORC_CB];
+        for (size_t j = 0; j < n; ++j) acc[j] = state[c0 + j];
+        for (size_t t = 0; t < seq; ++t) {
+            const size_t r = t * channels + c0;
+            for (size_t j = 0; j < n; ++j) {
+                acc[j] = w[r + j] * x[r + j] + acc[j] * (g[r + j] * b[r + j]);
+                s[r + j] = acc[j];
+            }
+        }
+        for (size_t j = 0; j < n; ++j) state[c0 + j] = acc[j];
+    }
+}
+
 static void conv_k4(const float *in, const float *w, float *out, float *hist,
                     size_t seq, size_t channels, int silu) {
 #ifdef _OPENMP

@@ -104,6 +104,12 @@ void orc_cumdecay_bf16(const float *a, uint16_t *decay, size_t seq, size_t chann
 /* gdn_sve.c:682-694 */
 void orc_gated_scan_bf16(const float *g, const float *x, float *s, uint16_t *state,
                          size_t seq, size_t channels);
+/* GDN-2 decoupled-gating scan, the portable branch gdn_sve.c:861-874:
+ *   acc = w[t][c] * x[t][c] + acc * (g[t][c] * b[t][c])  (no contraction)
+ * Pinned bit-exact against the reference build (oracle/_ref) and by its
+ * reduction to gated_scan_f32 when b = w = 1. */
+void orc_gdn2_gated_scan_f32(const float *g, const float *b, const float *w, const float *x, float *s,
+                             float *state, size_t seq, size_t channels);
 
 /* ---- matrix-state delta rule ------------------------------------------- */
 

@@ -99,6 +99,14 @@ def gated_scan_f32(g, x, state, seq, ch, L=None):
     return s, st
 
 
+def gdn2_scan_f32(g, b, w, x, state, seq, ch, L=None, name="orc_gdn2_gated_scan_f32"):
+    L = L or lib()
+    s = np.empty(seq * ch, np.float32)
+    st = np.array(state, np.float32, copy=True)
+    getattr(L, name)(P(g), P(b), P(w), P(x), P(s), P(st), _sz(seq), _sz(ch))
+    return s, st
+
+
 def conv_f32(inp, w, hist, seq, ch, silu=False, L=None):
     L = L or lib()
     out = np.empty(seq * ch, np.float32)

@@ -33,6 +33,7 @@ HIP_SYMBOLS = (
     "kai_run_gdn_cumdecay_bf16_hip",
     "kai_run_gdn_gated_scan_f16_hip",
     "kai_run_gdn_gated_scan_bf16_hip",
+    "kai_run_gdn2_gated_scan_f32_hip",
     "kai_run_gdn_delta_rule_decode_f32_hip",
     "kai_run_gdn_delta_rule_decode_f16state_hip",
     "kai_run_gdn_chunk_delta_rule_bf16_f32_hip",
@@ -72,7 +73,18 @@ HIP_SYMBOLS = (
     "kai_gdn_hip_probe_stream",
     "kai_gdn_hip_probe_mfma_bf16",
 )
-ALL_SYMBOLS = KAI_SYMBOLS + HIP_SYMBOLS
+# The reference's internal gdn_* ABI (include/gdn_sve.h).
+SVE_SYMBOLS = (
+    "gdn_cumdecay_f32",
+    "gdn_gated_scan_f32",
+    "gdn_causal_dwconv1d_f32",
+    "gdn_cumdecay_f16",
+    "gdn_gated_scan_f16",
+    "gdn_cumdecay_bf16",
+    "gdn_gated_scan_bf16",
+    "gdn2_gated_scan_f32",
+)
+ALL_SYMBOLS = KAI_SYMBOLS + HIP_SYMBOLS + SVE_SYMBOLS
 
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
@@ -104,6 +116,7 @@ _SIGS = {
     "kai_run_gdn_gated_scan_f32_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_gated_scan_f16_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_gated_scan_bf16_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn2_gated_scan_f32_hip": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_causal_dwconv1d_f32_k4_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_gemv_f32_f32_f32_hip": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),

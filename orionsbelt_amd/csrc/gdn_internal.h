@@ -19,6 +19,10 @@ hipError_t launch_conv_k4(const float *in, const float *w, float *out, float *hi
 hipError_t launch_gemv(const float *a, const float *b, float *c, size_t k, size_t n,
                        hipStream_t st);
 
+// GDN-2 gates for the gated scan: gp = g * b, xp = w * x (n elements).
+hipError_t launch_gdn2_gates(const float *g, const float *b, const float *w, const float *x, float *gp, float *xp,
+                             size_t n, hipStream_t st);
+
 // Scratch of the decoupled look-back scan: a monotonically increasing tile
 // counter, three status arrays of n_row_tiles * channels 64-bit words and an
 // error word.  Owned per device by the C-ABI layer, which serialises scan

@@ -8,6 +8,8 @@
 // one contiguous 256 B (or 1 KiB with float4) request.
 #include <type_traits>
 
+#include <algorithm>
+
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -497,6 +499,44 @@ hipError_t launch_conv_k4(const float *in, const float *w, float *out, float *hi
         if (silu) conv_k4_kernel<1, true, NT><<<grid, block, 0, st>>>(in, w, out, hist, seq, ch, seg_len);
         else conv_k4_kernel<1, false, NT><<<grid, block, 0, st>>>(in, w, out, hist, seq, ch, seg_len);
     }
+    return hipGetLastError();
+}
+
+// GDN-2 gates: gp = g * b, xp = w * x, each product rounded once (the
+// reference's portable branch, gdn_sve.c:861-874, rounds both before the
+// scan's sum).  Four elements per thread when the arrays allow.
+namespace {
+template <bool VEC4>
+__global__ __launch_bounds__(256) void gdn2_gates_kernel(const float *__restrict__ g, const float *__restrict__ b,
+                                                         const float *__restrict__ w, const float *__restrict__ x,
+                                                         float *__restrict__ gp, float *__restrict__ xp, size_t n) {
+#pragma clang fp contract(off)
+    const size_t stride = (size_t)gridDim.x * 256;
+    if constexpr (VEC4) {
+        for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n / 4; i += stride) {
+            const float4 gv = reinterpret_cast<const float4 *>(g)[i], bv = reinterpret_cast<const float4 *>(b)[i];
+            const float4 wv = reinterpret_cast<const float4 *>(w)[i], xv = reinterpret_cast<const float4 *>(x)[i];
+            reinterpret_cast<float4 *>(gp)[i] = make_float4(gv.x * bv.x, gv.y * bv.y, gv.z * bv.z, gv.w * bv.w);
+            reinterpret_cast<float4 *>(xp)[i] = make_float4(wv.x * xv.x, wv.y * xv.y, wv.z * xv.z, wv.w * xv.w);
+        }
+    } else {
+        for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+            gp[i] = g[i] * b[i];
+            xp[i] = w[i] * x[i];
+        }
+    }
+}
+}  // namespace
+
+hipError_t launch_gdn2_gates(const float *g, const float *b, const float *w, const float *x, float *gp, float *xp,
+                             size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const uintptr_t al = (uintptr_t)g | (uintptr_t)b | (uintptr_t)w | (uintptr_t)x | (uintptr_t)gp | (uintptr_t)xp;
+    const bool vec4 = n % 4 == 0 && al % 16 == 0;
+    const size_t work = vec4 ? n / 4 : n;
+    const unsigned blocks = (unsigned)std::min<size_t>((work + 255) / 256, 8192);
+    if (vec4) gdn2_gates_kernel<true><<<blocks, 256, 0, st>>>(g, b, w, x, gp, xp, n);
+    else gdn2_gates_kernel<false><<<blocks, 256, 0, st>>>(g, b, w, x, gp, xp, n);
     return hipGetLastError();
 }
 

@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "gdn_internal.h"
+#include "../../include/gdn_sve.h"
 #include "../../include/kai_gdn_hip.h"
 #include "../../include/kai/ukernels/gdn/kai_gdn_causal_dwconv1d_f32_k4_sve.h"
 #include "../../include/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.h"
@@ -71,6 +72,8 @@ struct DeviceCtx {
     // the last scan launch: its stream, and whether it may still be running
     hipStream_t scan_stream = nullptr;
     bool scan_pending = false;
+    // GDN-2 gate products (g * b, w * x) feeding the gated scan
+    DevBuf gdn2_tmp;
     // prefill carry buffer (segment transitions and start states)
     DevBuf chunk_ws;
     hipStream_t pf_stream = nullptr;  // stream of the last prefill
@@ -143,13 +146,10 @@ hipError_t scan_reserve(DeviceCtx *c, size_t words) {
     return hipSuccess;
 }
 
-hipError_t run_scan(int mode, int narrow, const float *g, const float *x, void *out,
-                    void *state, size_t seq, size_t ch, hipStream_t st) {
-    if (seq == 0 || ch == 0) return hipSuccess;
-    DeviceCtx *c;
-    hipError_t e = get_ctx(&c);
-    if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lk(c->mu);
+// A scan launch on `st`; called with c->mu held.
+hipError_t run_scan_locked(DeviceCtx *c, int mode, int narrow, const float *g, const float *x, void *out,
+                           void *state, size_t seq, size_t ch, hipStream_t st) {
+    hipError_t e;
     const size_t nr = gdn::scan_row_tiles(seq, mode);
     e = scan_reserve(c, nr * ch);
     if (e != hipSuccess) return e;
@@ -180,6 +180,41 @@ hipError_t run_scan(int mode, int narrow, const float *g, const float *x, void *
     c->scan_stream = st;
     c->scan_pending = true;
     return hipSuccess;
+}
+
+hipError_t run_scan(int mode, int narrow, const float *g, const float *x, void *out,
+                    void *state, size_t seq, size_t ch, hipStream_t st) {
+    if (seq == 0 || ch == 0) return hipSuccess;
+    DeviceCtx *c;
+    hipError_t e = get_ctx(&c);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(c->mu);
+    return run_scan_locked(c, mode, narrow, g, x, out, state, seq, ch, st);
+}
+
+// GDN-2 scan: the gate products into the device's gdn2 buffers, then the
+// gated scan over them.  The buffers are shared by every call on the device,
+// so a call waits for a scan still running on another stream (it may be
+// reading them), and growth waits for the device.
+hipError_t run_gdn2(const float *g, const float *b, const float *w, const float *x, float *s, float *state,
+                    size_t seq, size_t ch, hipStream_t st) {
+    if (seq == 0 || ch == 0) return hipSuccess;
+    DeviceCtx *c;
+    hipError_t e = get_ctx(&c);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(c->mu);
+    const size_t n = seq * ch;
+    if (c->scan_pending && (st != c->scan_stream || 2 * n * sizeof(float) > c->gdn2_tmp.cap)) {
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) return e;
+        c->scan_pending = false;
+    }
+    e = c->gdn2_tmp.reserve(2 * n * sizeof(float));
+    if (e != hipSuccess) return e;
+    float *gp = static_cast<float *>(c->gdn2_tmp.p), *xp = gp + n;
+    e = gdn::launch_gdn2_gates(g, b, w, x, gp, xp, n, st);
+    if (e != hipSuccess) return e;
+    return run_scan_locked(c, 1, gdn::kF32, gp, xp, s, state, seq, ch, st);
 }
 
 // ---- cumulative decay without allocation -----------------------------------
@@ -376,7 +411,7 @@ extern "C" size_t kai_gdn_hip_device_bytes_held(void) {
     DeviceCtx *c;
     if (get_ctx(&c) != hipSuccess) return 0;
     std::lock_guard<std::mutex> lk(c->mu);
-    size_t n = 256 + c->chunk_ws.cap;  // 256: the scan counter and error word
+    size_t n = 256 + c->chunk_ws.cap + c->gdn2_tmp.cap;  // 256: the scan counter and error word
     for (const DevBuf &s : c->stage) n += s.cap;
     return n + 3 * c->scan_words * sizeof(unsigned long long);
 }
@@ -892,4 +927,94 @@ extern "C" void kai_run_gdn_gemv_f32_f32_f32_1x4_neon(const float *a, const floa
                            (float *)args[2].dev, k, n, c->stream),
           "gemv launch");
     finish(c, args, 3);
+}
+
+// ===========================================================================
+// The reference's gdn_* ABI (include/gdn_sve.h): synchronous, host or device
+// pointers, like the kai symbols above.
+// ===========================================================================
+
+extern "C" void gdn_cumdecay_f32(const float *a, float *decay, size_t seq, size_t channels) {
+    kai_run_gdn_cumdecay_f32_sve(a, decay, seq, channels);
+}
+
+extern "C" void gdn_gated_scan_f32(const float *g, const float *x, float *s, float *state, size_t seq,
+                                   size_t channels) {
+    kai_run_gdn_gated_scan_f32_sve(g, x, s, state, seq, channels);
+}
+
+extern "C" void gdn_causal_dwconv1d_f32(const float *in, const float *w, float *out, float *hist, size_t seq,
+                                        size_t channels) {
+    kai_run_gdn_causal_dwconv1d_f32_k4_sve(in, w, out, hist, seq, channels);
+}
+
+namespace {
+void sync_narrow_decay(int narrow, const float *a, void *decay, size_t seq, size_t channels) {
+    if (seq == 0 || channels == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    const size_t n = seq * channels;
+    Arg args[2] = {stage_arg(c, 0, a, n * sizeof(float), true, false),
+                   stage_arg(c, 1, decay, n * sizeof(uint16_t), false, true)};
+    check(run_scan(0, narrow, (const float *)args[0].dev, nullptr, args[1].dev, nullptr, seq, channels, c->stream),
+          "cumdecay launch");
+    finish(c, args, 2);
+    scan_settled(c);
+}
+
+void sync_narrow_scan(int narrow, const float *g, const float *x, float *s, void *state, size_t seq,
+                      size_t channels) {
+    if (seq == 0 || channels == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    const size_t n = seq * channels * sizeof(float);
+    Arg args[4] = {stage_arg(c, 0, g, n, true, false), stage_arg(c, 1, x, n, true, false),
+                   stage_arg(c, 2, s, n, false, true),
+                   stage_arg(c, 3, state, channels * sizeof(uint16_t), true, true)};
+    check(run_scan(1, narrow, (const float *)args[0].dev, (const float *)args[1].dev, args[2].dev, args[3].dev,
+                   seq, channels, c->stream),
+          "gated_scan launch");
+    finish(c, args, 4);
+    scan_settled(c);
+}
+}  // namespace
+
+extern "C" void gdn_cumdecay_f16(const float *a, GDN_SVE_F16 *decay, size_t seq, size_t channels) {
+    sync_narrow_decay(gdn::kF16, a, decay, seq, channels);
+}
+extern "C" void gdn_cumdecay_bf16(const float *a, uint16_t *decay, size_t seq, size_t channels) {
+    sync_narrow_decay(gdn::kBF16, a, decay, seq, channels);
+}
+extern "C" void gdn_gated_scan_f16(const float *g, const float *x, float *s, GDN_SVE_F16 *state, size_t seq,
+                                   size_t channels) {
+    sync_narrow_scan(gdn::kF16, g, x, s, state, seq, channels);
+}
+extern "C" void gdn_gated_scan_bf16(const float *g, const float *x, float *s, uint16_t *state, size_t seq,
+                                    size_t channels) {
+    sync_narrow_scan(gdn::kBF16, g, x, s, state, seq, channels);
+}
+
+extern "C" void gdn2_gated_scan_f32(const float *g, const float *b_gate, const float *w_gate, const float *x,
+                                    float *s, float *state, size_t seq, size_t channels) {
+    if (seq == 0 || channels == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    const size_t n = seq * channels * sizeof(float);
+    Arg args[6] = {stage_arg(c, 0, g, n, true, false),      stage_arg(c, 1, b_gate, n, true, false),
+                   stage_arg(c, 2, w_gate, n, true, false), stage_arg(c, 3, x, n, true, false),
+                   stage_arg(c, 4, s, n, false, true),
+                   stage_arg(c, 5, state, channels * sizeof(float), true, true)};
+    check(run_gdn2((const float *)args[0].dev, (const float *)args[1].dev, (const float *)args[2].dev,
+                   (const float *)args[3].dev, (float *)args[4].dev, (float *)args[5].dev, seq, channels, c->stream),
+          "gdn2 gated_scan launch");
+    finish(c, args, 6);
+    scan_settled(c);
+}
+
+extern "C" int kai_run_gdn2_gated_scan_f32_hip(const float *g, const float *b_gate, const float *w_gate,
+                                               const float *x, float *s, float *state, size_t seq, size_t channels,
+                                               void *stream) {
+    if (seq == 0 || channels == 0) return 0;
+    if (!g || !b_gate || !w_gate || !x || !s || !state) return (int)hipErrorInvalidValue;
+    return (int)run_gdn2(g, b_gate, w_gate, x, s, state, seq, channels, (hipStream_t)stream);
 }

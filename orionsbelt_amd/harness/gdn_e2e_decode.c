@@ -12,11 +12,17 @@
  * with the reference's CSV headers, so its parser (bench/convert_e2e_decode.py)
  * reads these rows.  The reference's per-phase CPU timers have no counterpart
  * in one GPU step: those columns print nan.  Added:
+ *   --prefill M          process M prompt tokens in one pass
+ *                        (kai_gdn_hybrid_prefill) and report TTFT and prefill
+ *                        throughput (:2644-2730: 2 warm-up passes, then one
+ *                        measured; its CSV header; the per-layer-type split
+ *                        prints nan, the GPU runs the pass as one stream of
+ *                        kernels)
  *   --batch B            sequences decoded together (default 1, at most 16)
  *   --ctx L              a drawn context of L positions before the timed
  *                        tokens (KV caches, recurrent and conv states)
- * The reference's other flags (--pure-gdn, --prefill, --verify-*, --naive)
- * select CPU code paths that do not exist here; they are reported and ignored.
+ * The reference's other flags (--pure-gdn, --verify-*, --naive) select CPU
+ * code paths that do not exist here; they are reported and ignored.
  *
  * As in the reference: 3 warm-up tokens, then a reset and the measured
  * tokens, each timed on its own (HIP events around the step, synchronised),
@@ -88,8 +94,67 @@ static double timed_step(runner *r) {
     return ms * 1e3;
 }
 
+/* --prefill M: M uniform-random prompt tokens per sequence through every
+ * layer in one pass; 2 warm-up passes, then the measured one (HIP events
+ * around the call, synchronised). */
+static int run_prefill(int M, int batch, int csv) {
+    kai_gdn_hybrid_config cfg = kai_gdn_hybrid_qwen35_4b(batch, M + 1);
+    kai_gdn_hybrid *m = NULL;
+    KAI_OK(kai_gdn_hybrid_create(&cfg, 12345, &m));
+    hipStream_t st;
+    hipEvent_t e0, e1;
+    HIP_OK(hipStreamCreate(&st));
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+    const size_t n = (size_t)batch * (size_t)M;
+    int32_t *host = malloc(sizeof(int32_t) * n), *tok = NULL, *next = NULL;
+    if (!host) {
+        fprintf(stderr, "Error: out of host memory\n");
+        return 1;
+    }
+    uint32_t seed = 42u;
+    for (size_t i = 0; i < n; ++i) {
+        seed = seed * 1664525u + 1013904223u;
+        host[i] = (int32_t)(seed % (uint32_t)cfg.vocab);
+    }
+    HIP_OK(hipMalloc((void **)&tok, sizeof(int32_t) * n));
+    HIP_OK(hipMalloc((void **)&next, sizeof(int32_t) * 16));
+    HIP_OK(hipMemcpy(tok, host, sizeof(int32_t) * n, hipMemcpyHostToDevice));
+    if (!csv) {
+        printf(MODEL_NAME " MI355X prefill benchmark (M=%d)\n", M);
+        printf("  layers=%d (GDN=%d, full=%d), hidden=%d, int8 weights, batch=%d\n", cfg.layers,
+               cfg.layers - cfg.layers / cfg.attn_every, cfg.layers / cfg.attn_every, cfg.hidden, batch);
+        printf("  tokens/prefill=%d\n\n", M);
+    }
+    for (int r = 0; r < 2; ++r) KAI_OK(kai_gdn_hybrid_prefill(m, tok, batch, M, next, NULL, st));
+    HIP_OK(hipStreamSynchronize(st));
+    HIP_OK(hipEventRecord(e0, st));
+    KAI_OK(kai_gdn_hybrid_prefill(m, tok, batch, M, next, NULL, st));
+    HIP_OK(hipEventRecord(e1, st));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    const double total_us = ms * 1e3, ttft_ms = ms, tps = (double)n * 1e6 / total_us;
+    if (csv) {
+        printf("model,prefill_M,ttft_ms,tok_per_sec_prefill,gdn_us,full_us,ffn_us\n");
+        printf(MODEL_NAME ",%d,%.2f,%.2f,nan,nan,nan\n", M, ttft_ms, tps);
+    } else {
+        printf("Results (prefill M=%d, %d sequences):\n", M, batch);
+        printf("  TTFT (prefill total):  %.2f ms  (%.0f us)\n", ttft_ms, total_us);
+        printf("  Prefill throughput:    %.2f tok/s  (%.4f ms/tok)\n", tps, ttft_ms / (double)n);
+    }
+    free(host);
+    HIP_OK(hipFree(tok));
+    HIP_OK(hipFree(next));
+    HIP_OK(hipEventDestroy(e0));
+    HIP_OK(hipEventDestroy(e1));
+    HIP_OK(hipStreamDestroy(st));
+    kai_gdn_hybrid_destroy(m);
+    return 0;
+}
+
 int main(int argc, char **argv) {
-    int num_tokens = 8, csv = 0, batch = 1, ctx = 0, sweep = 0;
+    int num_tokens = 8, csv = 0, batch = 1, ctx = 0, sweep = 0, prefill_m = 0;
     const char *ctx_lens_str = NULL;
     for (int i = 1; i < argc; ++i) {
         if (strcmp(argv[i], "--tokens") == 0 && i + 1 < argc)
@@ -110,14 +175,13 @@ int main(int argc, char **argv) {
             printf("  --ctx-sweep L1,L2,...  Decode cost at growing context lengths\n");
             printf("  --batch B         Sequences decoded together (default 1, at most 16)\n");
             printf("  --ctx L           Drawn context of L positions before the timed tokens\n");
+            printf("  --prefill M       Process M tokens in one pass (measures TTFT / prefill cost)\n");
             return 0;
         } else if (strcmp(argv[i], "--pure-gdn") == 0 || strcmp(argv[i], "--naive") == 0 ||
                    strncmp(argv[i], "--verify-", 9) == 0) {
             fprintf(stderr, "Warning: '%s' selects a CPU code path of the reference; ignored\n", argv[i]);
         } else if (strcmp(argv[i], "--prefill") == 0 && i + 1 < argc) {
-            fprintf(stderr, "Warning: '--prefill %s' is not built here (the context is drawn); ignored\n",
-                    argv[i + 1]);
-            ++i;
+            prefill_m = atoi(argv[++i]);
         } else {
             fprintf(stderr, "Warning: unrecognized argument '%s' (ignored)\n", argv[i]);
         }
@@ -130,6 +194,11 @@ int main(int argc, char **argv) {
         fprintf(stderr, "Error: --batch must be in 1..16 and --ctx >= 0\n");
         return 1;
     }
+    if (prefill_m < 0) {
+        fprintf(stderr, "Error: --prefill must be >= 1 (got %d)\n", prefill_m);
+        return 1;
+    }
+    if (prefill_m > 0) return run_prefill(prefill_m, batch, csv);
     /* context lengths of the sweep (default: the reference's list, :2447-2449) */
     int lens[64], nlens = 0;
     if (sweep) {

@@ -19,7 +19,7 @@ def declared_symbols():
             if f.endswith(".h"):
                 txt = open(os.path.join(root, f)).read()
                 txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-                names.update(re.findall(r"\b(kai_[a-z0-9_]+)\s*\(", txt))
+                names.update(re.findall(r"\b((?:kai|gdn2?)_[a-z0-9_]+)\s*\(", txt))
     return names
 
 
@@ -63,6 +63,22 @@ def test_kai_prototypes_identical_to_reference(hdr, name):
         pytest.skip("reference tree not present")
     ours = os.path.join(INCLUDE, "kai", "ukernels", "gdn", hdr)
     assert _proto(ours, name) == _proto(ref, name)
+
+
+@pytest.mark.parametrize("name", ["gdn_cumdecay_f32", "gdn_gated_scan_f32", "gdn_causal_dwconv1d_f32",
+                                  "gdn_cumdecay_f16", "gdn_gated_scan_f16", "gdn_cumdecay_bf16",
+                                  "gdn_gated_scan_bf16", "gdn2_gated_scan_f32"])
+def test_gdn_sve_prototypes_match_reference(name):
+    """include/gdn_sve.h against the reference's gdn_sve.h:30-86: the same
+    parameters in the same order, once this header's spelling macros
+    (restrict, and __fp16 where the compiler has it) are read as the
+    reference writes them."""
+    ref = "/root/reference/src/orionsbelt/engines/cpu/kernels/gdn_sve.h"
+    if not os.path.exists(ref):
+        pytest.skip("reference tree not present")
+    ours = _proto(os.path.join(INCLUDE, "gdn_sve.h"), name)
+    ours = ours.replace("GDN_SVE_RESTRICT", "restrict").replace("GDN_SVE_F16", "__fp16")
+    assert ours == _proto(ref, name)
 
 
 def test_c_harnesses_built():

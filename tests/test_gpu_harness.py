@@ -5,13 +5,15 @@ observable contract (kleidiai_submission/test_kai_gdn.c:84-96,665-675:
 bench_kai_gdn.c:249-256,298: `--repeats N`, `--csv` and the CSV header that
 scripts/verify_kleidiai_kernels.sh:74-79 parses).
 
-Three programs:
+Programs:
 - orionsbelt_amd/bin/test_kai_gdn: this build's harness (host and device
   pointer suites);
 - oracle/_ref/test_kai_gdn_on_hip: the reference's own test_kai_gdn.c,
   compiled unchanged against include/ and linked to the HIP library
   (oracle/Makefile), when that build exists;
-- orionsbelt_amd/bin/bench_kai_gdn: the bench harness, CSV mode."""
+- orionsbelt_amd/bin/bench_kai_gdn: the bench harness, CSV mode;
+- oracle/_ref/test_gdn_{mixed,2_scan,sve}_on_hip: the reference's tests of
+  its gdn_sve.h kernels, compiled unchanged against this library."""
 import os
 import subprocess
 
@@ -56,6 +58,43 @@ def test_reference_test_program_on_hip_library():
     r = run(exe)
     check_test_output(r)
     print(r.stdout.strip().splitlines()[-3:])
+
+
+@pytest.mark.parametrize("prog", ["test_gdn_mixed_on_hip", "test_gdn2_scan_on_hip"])
+def test_reference_gdn_sve_tests_on_hip_library(prog):
+    """The reference's tests of its gdn_sve.h kernels (test_gdn_mixed.c:
+    fp16/bf16 decay and scan against its fp32 reference, bounds and a
+    determinism check; test_gdn2_scan.c: the GDN-2 scan against its float
+    and double references, the reduction to GDN-1, state continuity and
+    determinism), compiled unchanged and linked to this library by
+    oracle/Makefile."""
+    exe = os.path.join(REPO, "oracle", "_ref", prog)
+    if not os.access(exe, os.X_OK):
+        pytest.skip(f"oracle/_ref/{prog} not built (needs the reference tree at build time)")
+    r = run(exe)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
+    assert "ALL TESTS PASSED" in r.stdout
+    print(r.stdout.strip().splitlines()[-1])
+
+
+def test_reference_gdn_sve_report_on_hip_library():
+    """test_gdn_sve.c prints the scan, decay and conv against its
+    precision-matched float reference and has no pass/fail exit, so its
+    verdict lines are read here: at its shape (64 rows, one row tile of each
+    scan) the scan and the decay are bit-identical to the reference's
+    sequential loops, and the conv over two chunks equals the conv over the
+    whole sequence."""
+    exe = os.path.join(REPO, "oracle", "_ref", "test_gdn_sve_on_hip")
+    if not os.access(exe, os.X_OK):
+        pytest.skip("oracle/_ref/test_gdn_sve_on_hip not built (needs the reference tree at build time)")
+    r = run(exe)
+    assert r.returncode == 0, r.stderr[-2000:]
+    print(r.stdout)
+    out = r.stdout
+    assert "gated_scan bit-identical to matched reference: YES" in out
+    assert "cumdecay bit-identical to matched reference: YES" in out
+    assert "conv streaming bit-identical: YES" in out
+    assert "nan" not in out.lower()
 
 
 def test_kai_bench_harness_csv():

@@ -289,7 +289,7 @@ def test_hybrid_config5_batch16_ctx32k(hb):
 def test_e2e_driver_runs(hb):
     """The C driver (orionsbelt_amd/bin/gdn_e2e_decode, the reference e2e
     program's interface) decodes at the 4B shape and prints the reference's
-    CSV rows: the decode report and a context sweep."""
+    CSV rows: the decode report, a context sweep and the prefill report."""
     import os
     import subprocess
     exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "orionsbelt_amd", "bin",
@@ -307,6 +307,14 @@ def test_e2e_driver_runs(hb):
     assert lines[0].startswith("model,ctx_len,gdn_layer_us,full_attn_us,ffn_us,total_us")
     assert [ln.split(",")[1] for ln in lines[1:]] == ["1", "300"]
     assert all(float(ln.split(",")[5]) > 0 for ln in lines[1:])
+    # --prefill M: the reference's prefill report (gdn_e2e_decode.c:2708-2710)
+    r = subprocess.run([exe, "--csv", "--prefill", "1000", "--batch", "2"], capture_output=True, text=True,
+                       timeout=240)
+    assert r.returncode == 0, r.stderr
+    head, row = r.stdout.strip().splitlines()[-2:]
+    assert head == "model,prefill_M,ttft_ms,tok_per_sec_prefill,gdn_us,full_us,ffn_us"
+    f = row.split(",")
+    assert f[0] == "Qwen3.5-4B" and f[1] == "1000" and float(f[2]) > 0 and float(f[3]) > 0
 
 
 def test_hybrid_real_head_counts_vs_oracle(hb, fixture):

@@ -328,3 +328,90 @@ def test_kai_degenerate_no_writes(L):
 
 def test_no_scan_watchdog_errors(L):
     assert L.kai_gdn_hip_check_device_error() == 0
+
+
+# ---------------------------------------------------------------------------
+# The reference's gdn_* ABI (include/gdn_sve.h) and the GDN-2 scan
+# ---------------------------------------------------------------------------
+
+def _sz(n):
+    import ctypes
+    return ctypes.c_size_t(n)
+
+
+def test_gdn_sve_abi_host_pointers(L):
+    """The eight gdn_* symbols with host buffers, at the reference tests'
+    shape (64 rows: one row tile, so bit-exact against the oracle; 2051
+    channels: a ragged last tile)."""
+    seq, ch = 64, 2051
+    n = seq * ch
+    rs = np.random.RandomState(3)
+    a = rs.uniform(0.9, 1.0, n).astype(np.float32)
+    g = rs.uniform(0.5, 0.99, n).astype(np.float32)
+    x = rs.uniform(-1, 1, n).astype(np.float32)
+    b = rs.uniform(0, 1, n).astype(np.float32)
+    w = rs.uniform(0, 1, n).astype(np.float32)
+    st = rs.uniform(-0.5, 0.5, ch).astype(np.float32)
+    out = np.empty(n, np.float32)
+    L.gdn_cumdecay_f32(np_ptr(a), np_ptr(out), _sz(seq), _sz(ch))
+    assert np.array_equal(bits(out), bits(orc.cumdecay_f32(a, seq, ch)))
+    s, st_got = np.empty(n, np.float32), st.copy()
+    L.gdn_gated_scan_f32(np_ptr(g), np_ptr(x), np_ptr(s), np_ptr(st_got), _sz(seq), _sz(ch))
+    rs_, rst = orc.gated_scan_f32(g, x, st, seq, ch)
+    assert np.array_equal(bits(s), bits(rs_)) and np.array_equal(bits(st_got), bits(rst))
+    wc, h = rs.uniform(-0.5, 0.5, 4 * ch).astype(np.float32), rs.uniform(-0.5, 0.5, 3 * ch).astype(np.float32)
+    o, h_got = np.empty(n, np.float32), h.copy()
+    L.gdn_causal_dwconv1d_f32(np_ptr(x), np_ptr(wc), np_ptr(o), np_ptr(h_got), _sz(seq), _sz(ch))
+    ro, rh = orc.conv_f32(x, wc, h, seq, ch)
+    assert np.array_equal(bits(o), bits(ro)) and np.array_equal(bits(h_got), bits(rh))
+    for fmt in ("f16", "bf16"):
+        d16 = np.empty(n, np.uint16)
+        getattr(L, f"gdn_cumdecay_{fmt}")(np_ptr(a), np_ptr(d16), _sz(seq), _sz(ch))
+        assert np.array_equal(d16, orc.cumdecay_narrow(a, seq, ch, fmt)), fmt
+        st16 = (orc.f32_to_bf16_bits(st) if fmt == "bf16" else st.astype(np.float16).view(np.uint16)).copy()
+        s16, st16_got = np.empty(n, np.float32), st16.copy()
+        getattr(L, f"gdn_gated_scan_{fmt}")(np_ptr(g), np_ptr(x), np_ptr(s16), np_ptr(st16_got), _sz(seq),
+                                            _sz(ch))
+        r1, r2 = orc.gated_scan_narrow(g, x, st16, seq, ch, fmt)
+        assert np.array_equal(bits(s16), bits(r1)) and np.array_equal(st16_got, r2), fmt
+    s2, st2 = np.empty(n, np.float32), st.copy()
+    L.gdn2_gated_scan_f32(np_ptr(g), np_ptr(b), np_ptr(w), np_ptr(x), np_ptr(s2), np_ptr(st2), _sz(seq), _sz(ch))
+    r1, r2 = orc.gdn2_scan_f32(g, b, w, x, st, seq, ch)
+    assert np.array_equal(bits(s2), bits(r1)) and np.array_equal(bits(st2), bits(r2))
+
+
+@pytest.mark.parametrize("seq,ch", [(64, 2051), (65, 33), (1000, 2048), (4096, 8192)])
+def test_gdn2_scan_device_vs_oracle(L, seq, ch):
+    """kai_run_gdn2_gated_scan_f32_hip against the oracle (bit-exact within a
+    64-row tile, the kai rule across tiles), and with b = w = 1 equal to the
+    gated scan kernel on the same g, x bit for bit (g * 1 and 1 * x are
+    exact, so the GDN-2 scan reduces to GDN-1, test_gdn2_scan.c:29)."""
+    import orionsbelt_amd as ob
+    torch = torch_mod()
+    n = seq * ch
+    rs = np.random.RandomState(seq + ch)
+    g = rs.uniform(-0.99, 0.99, n).astype(np.float32)
+    b = rs.uniform(0, 1, n).astype(np.float32)
+    w = rs.uniform(0, 1, n).astype(np.float32)
+    x = rs.uniform(-2, 2, n).astype(np.float32)
+    st = rs.uniform(-1, 1, ch).astype(np.float32)
+    dg, db, dw, dx, dst = dev(g), dev(b), dev(w), dev(x), dev(st)
+    ds = empty(n, torch.float32)
+    ob.check(L.kai_run_gdn2_gated_scan_f32_hip(P(dg), P(db), P(dw), P(dx), P(ds), P(dst), seq, ch, stream()), "gdn2")
+    s, st2 = host(ds), host(dst)
+    r1, r2 = orc.gdn2_scan_f32(g, b, w, x, st, seq, ch)
+    if seq <= 64:
+        assert np.array_equal(bits(s), bits(r1)) and np.array_equal(bits(st2), bits(r2))
+    else:
+        assert_kai_close(s, r1, 1e-4, 5e-4, "gdn2 scan")
+        assert_kai_close(st2, r2, 1e-4, 5e-4, "gdn2 scan state")
+    one = dev(np.ones(n, np.float32))
+    dst1 = dev(st)
+    ds1 = empty(n, torch.float32)
+    ob.check(L.kai_run_gdn2_gated_scan_f32_hip(P(dg), P(one), P(one), P(dx), P(ds1), P(dst1), seq, ch, stream()),
+             "gdn2 ones")
+    s_ref, st_ref = run_scan(L, g, x, st, seq, ch)
+    if seq <= 64:
+        assert np.array_equal(bits(host(ds1)), bits(s_ref)) and np.array_equal(bits(host(dst1)), bits(st_ref))
+    else:  # the look-back's carry may associate differently between the two launches
+        assert_kai_close(host(ds1), s_ref, 1e-5, 1e-5, "gdn2 with b = w = 1 vs the gated scan")

@@ -126,6 +126,38 @@ def test_ref_sve_narrow_sweep_bit_identical():
                 assert bits_equal(r1[0], r2[0]) and np.array_equal(r1[1], r2[1]), (seq, ch, fmt)
 
 
+def test_gdn2_scan_vs_reference_and_closed_forms():
+    """orc_gdn2_gated_scan_f32 against the live gdn_sve.c build (bit for
+    bit, ragged channel counts, sizes above the OpenMP threshold); with
+    b = w = 1 it is the GDN-1 scan bit for bit (test_gdn2_scan.c:29); with
+    w = 0 the state decays by the products g * b alone."""
+    rs = np.random.RandomState(9)
+    L = orc.ref_sve()
+    for seq in REF_SEQS + [100]:
+        for ch in REF_CHANS + [2051]:
+            n = seq * ch
+            g = rs.uniform(-0.99, 0.99, n).astype(np.float32)
+            b = rs.uniform(0, 1, n).astype(np.float32)
+            w = rs.uniform(0, 1, n).astype(np.float32)
+            x = rs.uniform(-2, 2, n).astype(np.float32)
+            st = rs.uniform(-1, 1, ch).astype(np.float32)
+            r1 = orc.gdn2_scan_f32(g, b, w, x, st, seq, ch)
+            if L is not None:
+                r2 = orc.gdn2_scan_f32(g, b, w, x, st, seq, ch, L=L, name="gdn2_gated_scan_f32")
+                assert bits_equal(r1[0], r2[0]) and bits_equal(r1[1], r2[1]), (seq, ch)
+            ones = np.ones(n, np.float32)
+            a1 = orc.gdn2_scan_f32(g, ones, ones, x, st, seq, ch)
+            a2 = orc.gated_scan_f32(g, x, st, seq, ch)
+            assert bits_equal(a1[0], a2[0]) and bits_equal(a1[1], a2[1]), (seq, ch)
+    seq, ch = 5, 3
+    g = np.full(seq * ch, 0.5, np.float32)
+    b = np.full(seq * ch, 0.5, np.float32)
+    st = np.array([1.0, -2.0, 4.0], np.float32)
+    s, stf = orc.gdn2_scan_f32(g, b, np.zeros(seq * ch, np.float32), np.ones(seq * ch, np.float32), st, seq, ch)
+    expect = np.array([[v * 0.25 ** (t + 1) for v in st] for t in range(seq)], np.float32).ravel()
+    assert bits_equal(s, expect) and bits_equal(stf, expect[-ch:])
+
+
 def test_degenerate_writes_nothing():
     """seq=0 / channels=0 leave outputs and state untouched
     (test_kai_gdn.c:520-637)."""
