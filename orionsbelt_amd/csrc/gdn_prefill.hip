@@ -248,6 +248,12 @@ GDN_DEV constexpr int fidx(int rt, int kb) { return rt < 2 ? rt : 2 * rt - 2 + k
 // M blocks (a >= b), fp32 row-major 16x16.
 GDN_DEV constexpr int mbi(int a, int b) { return a * (a + 1) / 2 + b; }
 
+// Floats per column of an M block in LDS: 16 rows + 4 pad, so that the
+// 16-byte accesses of lanes that walk the columns (a 16-float stride would
+// put every second column on the same four banks) cover the 32 banks once
+// per 8 lanes.
+constexpr int kMbPitch = 20;
+
 struct Smem {
     uint16_t Kb[3][C * D];   // k rows of chunks n, n+1, n+2
     uint16_t Qb[2][C * D];   // q rows (output segments)
@@ -256,8 +262,8 @@ struct Smem {
     Gates gt[2];
     u32x4_t Af[2][6][64];    // A fragments (output segments), two chunks
     u32x4_t Tf[2][6][64];    // (T - I) fragments, two chunks
-    float Mb[10][256];       // M blocks of the next chunk, fp32 column-major:
-                             // Mb[.][16 j + i] = M[i][j]
+    float Mb[10][16 * kMbPitch];  // M blocks of the next chunk, fp32 column-major:
+                                  // Mb[.][kMbPitch j + i] = M[i][j]
     float hg[4][2][C];       // per helper wave: G log2(e) and beta of its chunk
 };
 
@@ -425,7 +431,7 @@ template <int A> GDN_DEV void write_m(Smem &sm, const f32x4_t (&acc)[A + 1], con
             m[e] = lower ? Bi[e] * gm * acc[b][e] : 0.f;
         }
         // column-major: lane (g, r) holds rows 4g .. 4g+3 of column r
-        *reinterpret_cast<f32x4_t *>(&sm.Mb[mbi(A, b)][16 * r + 4 * g]) = m;
+        *reinterpret_cast<f32x4_t *>(&sm.Mb[mbi(A, b)][kMbPitch * r + 4 * g]) = m;
     }
 }
 // K Q^T tiles (b, a) for q row blocks A0 < A1 and b <= a: lane (g, r),
@@ -546,10 +552,10 @@ GDN_DEV void t_subst(Smem &sm, u32x4_t (&Tf)[6][64], TRegs &tr, int lane) {
     const int a = lane >> 4, j = lane & 15;
     f32x4_t mcol[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) mcol[q] = lds_f4(&sm.Mb[mbi(a, a)][16 * j + 4 * q]);
+    for (int q = 0; q < 4; ++q) mcol[q] = lds_f4(&sm.Mb[mbi(a, a)][kMbPitch * j + 4 * q]);
     constexpr int off_a[6] = {1, 2, 3, 2, 3, 3}, off_b[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
-    for (int i = 0; i < 6; ++i) tr.MC[i] = lds_f4(&sm.Mb[mbi(off_a[i], off_b[i])][16 * r + 4 * g]);
+    for (int i = 0; i < 6; ++i) tr.MC[i] = lds_f4(&sm.Mb[mbi(off_a[i], off_b[i])][kMbPitch * r + 4 * g]);
     // lane (a, j) computes row j of T_aa
     {
         float x[16];

@@ -6,15 +6,16 @@
 // (gdn_model.hip, w8f_tile_kernel) -- the M > 1 counterpart of the
 // reference e2e loop's gemm_int8_neon (gdn_e2e_decode.c:606-612).  Block
 // tile 128 rows x 128 channels, k in steps of 64, 4 waves as 2 x 2 (64 x 64
-// each, 16 MFMA tiles of 16x16x32 fp16).  Per step a thread stages 4 x 16
+// each, four 32x32x16 fp16 MFMA tiles: the larger MFMA shape delivers about
+// 1.5 times the 16x16x32 rate on gfx950).  Per step a thread stages 4 x 16
 // bytes of activations and 2 x 16 bytes of weights in registers while the
 // waves multiply the previous step from LDS; the weights are widened to
 // fp16 (exactly) on their way into LDS, so every MFMA operand is one
 // 16-byte LDS read.  LDS rows are 64 k + 8 pad halves (144 bytes): the
 // 16-byte reads of 8 consecutive rows then cover the 32 banks once.  The
-// weight is the A operand, as in the decode GEMM, so the epilogue has the
-// same shape: a lane holds 4 consecutive channels of one row (one 16-byte
-// store; SwiGLU pairs gate and up lanes 32 apart).
+// weight is the A operand, so a lane's accumulators hold runs of 4
+// consecutive channels of one row (16-byte stores), and the interleaved
+// gate/up rows put each gate channel and its up channel in the same lane.
 //
 // Prefill attention: Qwen3_5Attention's causal softmax(q k^T / 16) v with
 // the sigmoid output gate (modeling_qwen3_5.py:629-701), GQA, head dim 256,
@@ -47,7 +48,6 @@ __global__ __launch_bounds__(256, 2) void w8p_kernel(const uint16_t *__restrict_
                                                      int M, int N, int K, W8Out out) {
     __shared__ __align__(16) W8pStage st[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 4, r = lane & 15;
     const int wm = wave & 1, wn = wave >> 1;  // rows 64 wm .., channels 64 wn .. of the block
     const int n0 = blockIdx.x * kPBN, m0 = blockIdx.y * kPBM;
     const int steps = K / 64;
@@ -65,81 +65,114 @@ __global__ __launch_bounds__(256, 2) void w8p_kernel(const uint16_t *__restrict_
     }
     const int8_t *wp0 = W + (size_t)(n0 / 64) * steps * 4096 + tid * 16;
     const int8_t *wp1 = two ? wp0 + (size_t)steps * 4096 : wp0;
-    u32x4_t xr[4], wr[2];
-    auto gload = [&](int s) {
+    // Two register stages: the loads of step s + 2 are issued before the
+    // waves multiply step s, so each load has two steps' compute to land.
+    struct Stage {
+        u32x4_t x[4], w[2];
+    };
+    auto gload = [&](int s, Stage &r) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[i] = *reinterpret_cast<const u32x4_t *>(xp[i] + s * 64);
-        wr[0] = *reinterpret_cast<const u32x4_t *>(wp0 + (size_t)s * 4096);
-        wr[1] = *reinterpret_cast<const u32x4_t *>(wp1 + (size_t)s * 4096);
+        for (int i = 0; i < 4; ++i) r.x[i] = *reinterpret_cast<const u32x4_t *>(xp[i] + s * 64);
+        r.w[0] = *reinterpret_cast<const u32x4_t *>(wp0 + (size_t)s * 4096);
+        r.w[1] = *reinterpret_cast<const u32x4_t *>(wp1 + (size_t)s * 4096);
     };
     const int wq = tid & 63, wrow = 16 * (tid >> 6) + (wq & 15), wk = 16 * (wq >> 4);
-    auto lstore = [&](int b) {
+    auto lstore = [&](int b, const Stage &r) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<u32x4_t *>(&st[b].x[(c >> 3) * kPPitch + (c & 7) * 8]) = xr[i];
+            *reinterpret_cast<u32x4_t *>(&st[b].x[(c >> 3) * kPPitch + (c & 7) * 8]) = r.x[i];
         }
 #pragma unroll
         for (int gi = 0; gi < 2; ++gi) {
             f16x8_t lo, hi;
-            i8x16_to_f16(wr[gi], lo, hi);
+            i8x16_to_f16(r.w[gi], lo, hi);
             uint16_t *d = &st[b].w[(64 * gi + wrow) * kPPitch + wk];
             *reinterpret_cast<f16x8_t *>(d) = lo;
             *reinterpret_cast<f16x8_t *>(d + 8) = hi;
         }
     };
 
-    f32x4_t acc[4][4];  // [channel tile j][row tile i]
+    // 32x32x16 fp16 MFMA: A lane l = W row (channel) l % 32, k 8 (l / 32)
+    // .. +7; B lane l = x row l % 32, the same k; C element e of lane l =
+    // channel 8 (e / 4) + 4 (l / 32) + e % 4, row l % 32
+    typedef float f32x16_t __attribute__((ext_vector_type(16)));
+    f32x16_t acc[2][2];  // [channel tile jt][row tile it], 32 x 32 each
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[j][i] = zero4();
+        for (int it = 0; it < 2; ++it)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[jt][it][e] = 0.f;
+    const int l32 = lane & 31, h2 = lane >> 5;
     auto compute = [&](int b) {
         if (!active) return;
 #pragma unroll
-        for (int kk = 0; kk < 64; kk += 32) {
-            f16x8_t a[4], bx[4];
+        for (int kk = 0; kk < 64; kk += 16) {
+            f16x8_t a[2], bx[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                a[j] = *reinterpret_cast<const f16x8_t *>(&st[b].w[(64 * wn + 16 * j + r) * kPPitch + kk + 8 * g]);
+            for (int jt = 0; jt < 2; ++jt)
+                a[jt] = *reinterpret_cast<const f16x8_t *>(
+                    &st[b].w[(64 * wn + 32 * jt + l32) * kPPitch + kk + 8 * h2]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                bx[i] = *reinterpret_cast<const f16x8_t *>(&st[b].x[(64 * wm + 16 * i + r) * kPPitch + kk + 8 * g]);
+            for (int it = 0; it < 2; ++it)
+                bx[it] = *reinterpret_cast<const f16x8_t *>(
+                    &st[b].x[(64 * wm + 32 * it + l32) * kPPitch + kk + 8 * h2]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], bx[i], acc[j][i], 0, 0, 0);
+                for (int it = 0; it < 2; ++it)
+                    acc[jt][it] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[jt], bx[it], acc[jt][it], 0, 0, 0);
         }
     };
 
-    gload(0);
-    lstore(0);
+    // step s: registers R[s % 2], LDS buffer s % 2; the loop is unrolled by
+    // two so that every register stage is a fixed set of registers
+    // Loads are issued on every turn (past the last step they re-read it:
+    // in bounds, never stored), so that every path has the same loads in
+    // flight and the compiler waits only for the older stage.
+    Stage R0, R1;
+    const int last = steps - 1;
+    gload(0, R0);
+    gload(min(1, last), R1);
+    lstore(0, R0);
     __syncthreads();
-    for (int s = 0; s < steps; ++s) {
-        if (s + 1 < steps) gload(s + 1);
-        compute(s & 1);
-        if (s + 1 < steps) lstore((s + 1) & 1);
+    for (int s = 0; s < steps; s += 2) {
+        // even step s: R0 is free (stored at the previous turn)
+        gload(min(s + 2, last), R0);
+        compute(0);
+        if (s + 1 < steps) lstore(1, R1);
+        __syncthreads();
+        if (s + 1 >= steps) break;
+        // odd step s + 1: R1 is free
+        gload(min(s + 3, last), R1);
+        compute(1);
+        if (s + 2 < steps) lstore(0, R0);
         __syncthreads();
     }
     if (!active) return;
 
-    // C lane (g, r) of tile (j, i): channels n .. n+3 (n = n0 + 64 wn + 16 j
-    // + 4 g) of row m0 + 64 wm + 16 i + r
+    // lane l of tile (jt, it): for q = 0..3, channels n .. n+3 (n = n0 + 64 wn
+    // + 32 jt + 8 q + 4 (l / 32)) of row m0 + 64 wm + 32 it + l % 32
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + 64 * wn + 16 * j + 4 * g;
-        const f32x4_t sc = *reinterpret_cast<const f32x4_t *>(scale + n);
+    for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = m0 + 64 * wm + 16 * i + r;
-            const f32x4_t y = acc[j][i] * sc;
-            if (out.mode == kW8SwiGLU) {
-                // tile rows 0..7 are gate channels 8t .. 8t+7, rows 8..15 the up channels
-                f32x4_t up;
+        for (int it = 0; it < 2; ++it) {
+            const int row = m0 + 64 * wm + 32 * it + l32;
+            if (row >= M) continue;
+            const int nt = n0 + 64 * wn + 32 * jt;  // the tile's first channel
 #pragma unroll
-                for (int e = 0; e < 4; ++e) up[e] = __shfl_xor(y[e], 32);
-                if (g < 2 && row < M) {
+            for (int q = 0; q < 4; ++q) {
+                const int n = nt + 8 * q + 4 * h2;
+                const f32x4_t sc = *reinterpret_cast<const f32x4_t *>(scale + n);
+                const f32x4_t y = f32x4_t{acc[jt][it][4 * q], acc[jt][it][4 * q + 1], acc[jt][it][4 * q + 2],
+                                          acc[jt][it][4 * q + 3]} * sc;
+                if (out.mode == kW8SwiGLU) {
+                    // 16-channel groups: 8 gate channels (q even), then their 8 up channels (q + 1)
+                    if (q & 1) continue;
+                    const f32x4_t su = *reinterpret_cast<const f32x4_t *>(scale + n + 8);
+                    const f32x4_t up = f32x4_t{acc[jt][it][4 * q + 4], acc[jt][it][4 * q + 5],
+                                               acc[jt][it][4 * q + 6], acc[jt][it][4 * q + 7]} * su;
                     uint32_t hv[2];
 #pragma unroll
                     for (int e = 0; e < 4; e += 2) {
@@ -147,29 +180,28 @@ __global__ __launch_bounds__(256, 2) void w8p_kernel(const uint16_t *__restrict_
                         const float b = y[e + 1] / (1.0f + expf(-y[e + 1])) * up[e + 1];
                         hv[e / 2] = (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
                     }
-                    const int cc = (n0 + 64 * wn + 16 * j) / 2 + 4 * g;
+                    const int cc = (nt + 16 * (q >> 1)) / 2 + 4 * h2;
                     *reinterpret_cast<uint2 *>(out.x16 + (size_t)row * (N / 2) + cc) = make_uint2(hv[0], hv[1]);
+                } else if (n < out.seg[out.nseg - 1].n_end) {  // channels past the last segment: padding
+                    int sgi = 0, nb = 0;
+#pragma unroll
+                    for (int qq = 0; qq < kW8MaxSegs - 1; ++qq)
+                        if (qq < out.nseg - 1 && n >= out.seg[qq].n_end) {
+                            sgi = qq + 1;
+                            nb = out.seg[qq].n_end;
+                        }
+                    float *dst = out.seg[0].dst;
+                    int ld = out.seg[0].ld;
+#pragma unroll
+                    for (int qq = 1; qq < kW8MaxSegs; ++qq)
+                        if (qq == sgi) {
+                            dst = out.seg[qq].dst;
+                            ld = out.seg[qq].ld;
+                        }
+                    *reinterpret_cast<f32x4_t *>(dst + (size_t)row * ld + (n - nb)) = y;
                 }
-            } else if (row < M && n < out.seg[out.nseg - 1].n_end) {  // channels past the last segment: padding
-                int sgi = 0, nb = 0;
-#pragma unroll
-                for (int q = 0; q < kW8MaxSegs - 1; ++q)
-                    if (q < out.nseg - 1 && n >= out.seg[q].n_end) {
-                        sgi = q + 1;
-                        nb = out.seg[q].n_end;
-                    }
-                float *dst = out.seg[0].dst;
-                int ld = out.seg[0].ld;
-#pragma unroll
-                for (int q = 1; q < kW8MaxSegs; ++q)
-                    if (q == sgi) {
-                        dst = out.seg[q].dst;
-                        ld = out.seg[q].ld;
-                    }
-                *reinterpret_cast<f32x4_t *>(dst + (size_t)row * ld + (n - nb)) = y;
             }
         }
-    }
 }
 
 // ---- causal prefill attention ------------------------------------------------
@@ -210,26 +242,27 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
     const int nkb = (kend + kApK - 1) / kApK;
     const uint16_t *kbase = Kc + (size_t)kv * Tmax * kApD;
     const uint16_t *vbase = vT + (size_t)kv * kApD * Tv;
-    // staging: K group tid / 128 (16 keys, 8 KB contiguous), 64 bytes at
-    // (tid % 128) * 64; V^T row tid / 2, keys 32 (tid % 2) .. +31
+    // staging: K 16-byte chunk tid + 512 i of the block's 32 KB (group i:
+    // 16 keys, 8 KB contiguous in the cache), consecutive lanes on
+    // consecutive chunks so the LDS stores do not collide; V^T row tid / 2,
+    // keys 32 (tid % 2) .. +31
     u32x4_t kr[4], vr[4];
-    const int kgrp = tid >> 7, koff = (tid & 127) * 32;
     const int vrow = tid >> 1, vhalf = (tid & 1) * 32;
     auto gload = [&](int kb) {
         // a group past the cache rows reads the last group instead (its
         // keys are masked: every key >= T lies after every query)
-        const int t0 = min(kb * kApK + 16 * kgrp, Tmax - 16);
-        const uint16_t *kp = kbase + (size_t)t0 * kApD + koff;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const u32x4_t *>(kp + 8 * i);
+        for (int i = 0; i < 4; ++i) {
+            const int t0 = min(kb * kApK + 16 * i, Tmax - 16);
+            kr[i] = *reinterpret_cast<const u32x4_t *>(kbase + (size_t)t0 * kApD + tid * 8);
+        }
         const uint16_t *vp = vbase + (size_t)vrow * Tv + kb * kApK + vhalf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) vr[i] = *reinterpret_cast<const u32x4_t *>(vp + 8 * i);
     };
     auto lstore = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4_t *>(&ks[b][kgrp * 4096 + koff + 8 * i]) = kr[i];
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t *>(&ks[b][i * 4096 + tid * 8]) = kr[i];
         uint16_t *vd = &vs[b][vrow * kApVPitch + vhalf];  // 8-byte aligned rows
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -265,9 +298,13 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
         // key 0 precedes every query, so the first step leaves mx finite
         const float alpha = __builtin_amdgcn_exp2f(m - mx);
         m = mx;
-        l *= alpha;
+        // once the running maxima settle, alpha is 1 in every lane: skip
+        // the 64 multiplies of O (x * 1 = x, so the result is the same)
+        if (__ballot(alpha != 1.0f)) {
+            l *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
+            for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
+        }
         f16x8_t pb[2];  // P^T fragments: keys 32 ks + {4g .. 4g+3, 16 + 4g .. 16 + 4g+3}
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
