@@ -226,6 +226,33 @@ def test_gated_scan_continuity(L):
 
 
 @pytest.mark.parametrize("fmt", ["f16", "bf16"])
+@pytest.mark.parametrize("seq,ch", [(128, 512), (1024, 2048), (4096, 8192)])
+def test_cumdecay_narrow_whole_tiles(L, fmt, seq, ch):
+    """The narrow decay on shapes of whole tiles (128 rows x 256 channels),
+    which take the kernel's unpredicated form, up to the bench's
+    [4096][8192].  The first row tile is bit-exact against the oracle's
+    narrow decay.  Past it, the carry into a tile may take either look-back route
+    (a published inclusive value or composed aggregates), which can move
+    the fp32 value by an ulp between launches; so there every element is
+    within one narrow ulp of the fp32 kernel's output rounded by the
+    reference's rule (a misplaced row or channel would be far off).  Measured:
+    8 (f16) and 4 (bf16) of 2.1M elements one ulp off at [1024][2048], 114
+    and 456 of 33.6M at [4096][8192]."""
+    rng = np.random.RandomState(seq + ch)
+    a = rng.uniform(0.97, 1.0, seq * ch).astype(np.float32)
+    got = run_cumdecay(L, a, seq, ch, fmt)
+    head = 128 * ch
+    assert np.array_equal(got[:head], orc.cumdecay_narrow(a[:head], 128, ch, fmt)), (seq, ch, fmt)
+    f32 = run_cumdecay(L, a, seq, ch, "f32")
+    want = orc.f32_to_bf16_bits(f32) if fmt == "bf16" else f32.astype(np.float16).view(np.uint16)
+    diff = np.abs(got.astype(np.int32) - want.astype(np.int32))  # all values positive
+    bad = np.flatnonzero(diff > 1)
+    assert bad.size == 0, (seq, ch, fmt, bad.size, [(int(i // ch), int(i % ch), int(got[i]), int(want[i]))
+                                                     for i in bad[:6]])
+    print(f"narrow decay [{seq}][{ch}] {fmt}: {int((diff == 1).sum())} of {diff.size} one ulp off the fp32 run")
+
+
+@pytest.mark.parametrize("fmt", ["f16", "bf16"])
 def test_mixed_precision_variants(L, fmt, golden):
     d = golden("sve_mixed.npz")
     T, C = (int(x) for x in d["shape"])
