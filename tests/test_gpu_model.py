@@ -97,8 +97,11 @@ def gpu_gemm_tiled(L, x16, q, s, reps=1):
                                    (16, 1024, 512), (1, 18432, 2560),
                                    # M > 16: the prefill GEMM (128-row blocks: ragged row tails,
                                    # a half channel block when N % 128 == 64, the 4B shapes)
-                                   (17, 64, 256), (100, 192, 512), (300, 2560, 9216), (1000, 12352, 2560),
-                                   (129, 18432, 2560)])
+                                   (17, 64, 256), (100, 192, 512), (300, 2560, 9216), (129, 18432, 2560),
+                                   # M >= 512: its 256 x 256 form (ragged rows, blocks with 1-3 of
+                                   # their four 64-channel groups)
+                                   (1000, 12352, 2560), (513, 2560, 9216), (600, 192, 512),
+                                   (2048, 10240, 2560)])
 def test_w8a16_gemm_tiled_vs_oracle(L, M, N, K):
     """The tiled-weight GEMM (the hybrid loop's): against the oracle at the
     row-major GEMM's bar, deterministic over calls that share one workspace
