@@ -730,6 +730,8 @@ GDN_DEV void zero_upper_halves(Smem &sm, int tid) {
 //            fragments of chunk n+1 (rows {0, 3} and {1, 2}), and hw3 waits
 //            for its loads; hw2 issues the loads of the q rows of chunk n+2,
 //            which it waits for at the end of the next phase 1.
+// In a transition segment (no q) hw2 loads chunk n+1's v rows in phase 2
+// instead of hw3 in phase 1, and waits for them before the phase ends.
 // Every load thus has at least a whole phase to land.
 template <bool WITH_Q>
 GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n1, int hw, int lane) {
@@ -789,7 +791,7 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
             load_rows_n<16>(sm.Kb[kslot(n + 2, n0)], a.k, a.Hk, kh, b, c2, a.T, 0, lane);
             load_gates_all(sm, pslot(n + 2, n0), a.g, b, h, a.Hv, c2, a.T, 0, lane);
             load_gates_all(sm, pslot(n + 2, n0), a.beta, b, h, a.Hv, c2, a.T, 1, lane);
-            load_rows_n<16>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 0, lane);
+            if (WITH_Q) load_rows_n<16>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 0, lane);
         } else if (more) {
             __builtin_amdgcn_s_setprio(2);
             kk(n + 1, hw == 1);
@@ -801,7 +803,15 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
             if (more) t_subst(sm, sm.Tf[pslot(n + 1, n0)], tr, lane);
         } else if (hw == 2) {
             // into the slot chunk n's q leaves (read in phase 1 only)
-            if (WITH_Q) load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
+            if (WITH_Q) {
+                load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
+            } else {
+                // transition segments: the v rows of chunk n+1 (whose slot
+                // chunk n-1 left), here rather than with helper 3's loads in
+                // phase 1, which bound that phase; phase 2 outlasts them
+                load_rows_n<16>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 0, lane);
+                wait_vmem0();
+            }
         } else {
             if (WITH_Q && more) qk(n + 1, hw == 3);
             if (hw == 3) wait_vmem0();  // k rows, gates of chunk n+2, v rows of n+1
