@@ -389,8 +389,10 @@ GDN_DEV bf16x8_t frag_ld(const u32x4_t &p) { return as_bf16x8(p); }
 // Gates of chunk c for this lane's token (lane = row of the chunk), both
 // zeroed past the sequence end (HF pads the last chunk with zeros): G log2(e)
 // and beta go to the helper's own copy hg[hw] (read back by this wave only);
-// with `write` the wave also stores the state waves' per-chunk gates.
-GDN_DEV void chunk_gates(Smem &sm, int slot, int c, int T, float q_scale, int hw, int lane, bool write) {
+// `write` selects which of the state waves' per-chunk gates the wave also
+// stores: bit 0 beta and e^G, bit 1 e^{G_last - G}, scale e^G and e^{G_last}
+// (the two helpers that form M each store half).
+GDN_DEV void chunk_gates(Smem &sm, int slot, int c, int T, float q_scale, int hw, int lane, int write) {
     // no fused multiply-adds: every inlined copy (prologue, loop, each
     // helper) must round the gates identically
 #pragma clang fp contract(off)
@@ -403,13 +405,18 @@ GDN_DEV void chunk_gates(Smem &sm, int slot, int c, int T, float q_scale, int hw
     sm.hg[hw][1][lane] = bv;
     if (write) {
         Gates &gt = sm.gt[slot];
-        const float Gl2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G2), 63));
         const float eg = __builtin_amdgcn_exp2f(G2);
-        gt.bt[lane] = bv;
-        gt.eg[lane] = eg;
-        gt.egl[lane] = __builtin_amdgcn_exp2f(Gl2 - G2);
-        gt.seg[lane] = q_scale * eg;
-        if (lane == 0) gt.gam = __builtin_amdgcn_exp2f(Gl2);
+        if (write & 1) {
+            gt.bt[lane] = bv;
+            gt.eg[lane] = eg;
+        }
+        if (write & 2) {
+            const float Gl2 =
+                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G2), 63));
+            gt.egl[lane] = __builtin_amdgcn_exp2f(Gl2 - G2);
+            gt.seg[lane] = q_scale * eg;
+            if (lane == 0) gt.gam = __builtin_amdgcn_exp2f(Gl2);
+        }
     }
     lds_fence();
 }
@@ -741,7 +748,7 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
     TRegs tr;
     auto kk = [&](int c, bool rows03) {
         const int ps = pslot(c, n0);
-        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, rows03);
+        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, rows03 ? 1 : 2);
         const float *G2 = sm.hg[hw][0], *Bt = sm.hg[hw][1];
         const uint16_t *K = sm.Kb[kslot(c, n0)];
         if (rows03) gram_rows<0, 3, true, false>(sm, sm.Af[ps], K, K, G2, Bt, a.q_scale, lane, g, r);
@@ -749,7 +756,7 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
     };
     auto qk = [&](int c, bool rows03) {
         const int ps = pslot(c, n0);
-        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, false);
+        chunk_gates(sm, ps, c, a.T, a.q_scale, hw, lane, 0);
         const float *G2 = sm.hg[hw][0], *Bt = sm.hg[hw][1];
         const uint16_t *K = sm.Kb[kslot(c, n0)];
         const uint16_t *Q = sm.Qb[ps];
