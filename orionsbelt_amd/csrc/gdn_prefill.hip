@@ -1253,9 +1253,12 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
     }
 }
 
-// Segments.  P: enough that a pass fills the device (about 256 workgroups),
-// at least kMinSegChunks chunks per segment on average, at most kMaxSegs;
-// P = 2 would only serialise, so it falls back to 1.  Lengths: segment 0
+// Segments.  P: at most what fills the device in one pass (about 256
+// workgroups), at least kMinSegChunks chunks per segment on average, at most
+// kMaxSegs, and the count whose best plan has the lowest modelled time
+// (plan_segments); P = 2 would only serialise, so it is never chosen, and
+// one segment (the plain recurrence) is kept when no plan beats it.
+// Lengths: segment 0
 // runs with outputs in pass 1 only; segments 1 .. P-2 run their transition
 // in pass 1 (kCostTrans per chunk, relative to a chunk with outputs) and
 // rerun with outputs in pass 2 after composing their start state
@@ -1267,7 +1270,11 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
 // chunk 7.4K cycles, a transition chunk 9.5K, a composition step 9.3K);
 // against the earlier 1.17 / 1.12 / 0.5 they plan 2% faster calls at
 // T = 16K, 32 heads.
-constexpr int kMinSegChunks = 8;
+// 4 chunks per segment at least: against 8, short sequences gain more from
+// the parallel segments than they lose to transitions (T = 1K: 53.3 against
+// 56.6 us, 2K: 68.7 against 77.9 us, 4K: 93.1 against 94.5 us; 3 is as good
+// at 1K and worse at 2K)
+constexpr int kMinSegChunks = 4;
 constexpr int kTargetWgs = 256;
 constexpr double kCostTrans = 1.28, kCostStep = 1.26, kCostPrologue = 1.0;
 
@@ -1299,18 +1306,10 @@ double plan_cost(int P, const int *len) {
     return t1 + t2;
 }
 
-void plan_segments(int B, int Hv, int NC, SegPlan &pl) {
-    const int bh = B * Hv;
-    int P = 1 + (kTargetWgs + bh - 1) / bh;
-    P = min(P, NC / kMinSegChunks);
-    P = min(P, kMaxSegs);
-    if (P < 3) {
-        pl.P = 1;
-        pl.bnd[0] = 0;
-        pl.bnd[1] = NC;
-        return;
-    }
-    int best[kMaxSegs], len[kMaxSegs];
+// The lengths of the cheapest plan with P segments (P >= 3); its modelled
+// cost, or +inf when no plan exists.
+double plan_lengths(int P, int NC, int *best) {
+    int len[kMaxSegs];
     double best_cost = 1e30;
     const int m_max = min(NC, 2 * NC / (P - 1) + 1);  // the cap is near NC / (P - 1)
     for (int M = 1; M <= m_max; ++M) {
@@ -1335,9 +1334,36 @@ void plan_segments(int B, int Hv, int NC, SegPlan &pl) {
             for (int p = 0; p < P; ++p) best[p] = len[p];
         }
     }
-    pl.P = P;
+    return best_cost;
+}
+
+// P is searched up to the number that fills the device once (each pass
+// launches (P - 1) x B x Hv workgroups): the composition chain grows with
+// P, so with few heads fewer segments than that plan faster (at Hv = 4,
+// T = 16K: 23 segments at a modelled 47 chunk times, against 86 for 64).
+void plan_segments(int B, int Hv, int NC, SegPlan &pl) {
+    const int bh = B * Hv;
+    int pmax = 1 + (kTargetWgs + bh - 1) / bh;
+    pmax = min(pmax, NC / kMinSegChunks);
+    pmax = min(pmax, kMaxSegs);
+    int best[kMaxSegs], len[kMaxSegs];
+    double best_cost = (double)NC;  // one segment: the plain recurrence
+    int best_p = 1;
+    for (int P = 3; P <= pmax; ++P) {
+        const double cost = plan_lengths(P, NC, len);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best_p = P;
+            for (int p = 0; p < P; ++p) best[p] = len[p];
+        }
+    }
+    pl.P = best_p;
     pl.bnd[0] = 0;
-    for (int p = 0; p < P; ++p) pl.bnd[p + 1] = pl.bnd[p] + best[p];
+    if (best_p == 1) {
+        pl.bnd[1] = NC;
+        return;
+    }
+    for (int p = 0; p < best_p; ++p) pl.bnd[p + 1] = pl.bnd[p] + best[p];
 }
 
 // The plan of the last shape asked for on this thread (a layer calls the

@@ -116,18 +116,22 @@ def test_generated_substitution_steps_up_to_date():
 
 
 def test_prefill_workspace_query_needs_no_device():
-    """The carry-buffer query is host arithmetic over the segment plan: one
-    segment (no carry) for short sequences and for batches that fill the
-    device by themselves, then P = 1 + ceil(256 / (B*Hv)) segments of
-    three 128x128 fp32 slots per (sequence, head), flat in T."""
+    """The carry-buffer query is host arithmetic over the segment plan:
+    three 128x128 fp32 slots per (sequence, head, segment), no carry for
+    one segment (short sequences, and batches that fill the device by
+    themselves), flat in T once the plan stops growing.  The planner picks
+    the segment count whose plan has the lowest modelled time, up to what
+    fills the device (1 + ceil(256 / (B*Hv))) with at least 4 chunks per
+    segment: 9 for 32 heads from T = 8K, 4 at T = 1K; 24 for 4 heads at
+    T = 16K, where 64 would compose too long a chain."""
     import orionsbelt_amd as ob
     L = ob.lib()
     slot = 3 * 128 * 128 * 4
-    assert L.kai_gdn_hip_prefill_workspace_bytes(1, 1024, 32) == 0
+    assert L.kai_gdn_hip_prefill_workspace_bytes(1, 640, 4) == 0
     assert L.kai_gdn_hip_prefill_workspace_bytes(16, 32768, 32) == 0
+    assert L.kai_gdn_hip_prefill_workspace_bytes(1, 1024, 32) == 4 * 32 * slot
     for T in (8192, 16384, 131072):
         assert L.kai_gdn_hip_prefill_workspace_bytes(1, T, 32) == 9 * 32 * slot
-    # few heads: P = 65 capped at 8 chunks per segment (256 chunks -> 32)
-    assert L.kai_gdn_hip_prefill_workspace_bytes(1, 16384, 4) == 32 * 4 * slot
+    assert L.kai_gdn_hip_prefill_workspace_bytes(1, 16384, 4) == 24 * 4 * slot
     for bad in ((0, 16384, 32), (1, 0, 32), (1, 16384, 0), (-1, 16384, 32)):
         assert L.kai_gdn_hip_prefill_workspace_bytes(*bad) == 0
