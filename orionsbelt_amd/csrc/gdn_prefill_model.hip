@@ -210,92 +210,102 @@ __global__ __launch_bounds__(256, 2) void w8p_kernel(const uint16_t *__restrict_
 }
 
 // The large-tile form: block 256 rows x 256 channels, 8 waves as 2 x 4
-// (128 rows x 64 channels each: 4 x 2 tiles of 32x32x16 fp16 MFMA).  Only
-// the activations go through LDS; each wave loads its weight fragments
-// straight from the tiled layout into registers and widens them there, so a
-// step's LDS traffic is the 32 KB of activation rows written once and read
-// by the four channel waves.  Lane l of a 32-channel MFMA tile reads, from
+// (128 rows x 64 channels each: 4 x 2 tiles of 32x32x16 fp16 MFMA).  Both
+// operands of a 64-k step reach LDS by DMA (global_load_lds, 1 KB per wave
+// instruction): the 256 activation rows (32 KB) and the four 4 KB weight
+// tiles of the block's channel groups, copied as they lie.  The buffers
+// form a ring of three steps held in separate arrays, so that the compiler
+// can tell the slot being filled from the slot being read and does not wait
+// for the DMA before every LDS read; the loads of step s + 2 are issued
+// into the slot step s - 1 used, and one wait on the vector memory counter
+// before each barrier makes step s + 1's tiles complete.  An activation row
+// is 128 B; its 16-byte piece p sits in slot p ^ ((row / 2) % 8), so that
+// the 16 rows a quarter-wave reads cover all 64 banks.  The weights are
+// widened to fp16 from LDS.  Lane l of a 32-channel MFMA tile reads, from
 // 16-row weight tile 2 jt + (l % 32) / 16, row l % 16 and the 16-byte
 // pieces g' = l / 32 and l / 32 + 2 of the 64-k step (k 16 g' .. +15); MFMA
 // kk (4 per step) takes 8 of them: k = 32 (kk / 2) + 16 (l / 32) + 8 (kk %
 // 2) .. +7, and the activation (B) lanes read the same k.
+// Measured at M = 32768 on the 4B shapes: 12-19% faster than the same tile
+// with the weights loaded into registers and the activations staged through
+// registers (gate|up 1060-1086 against 933-965 TFLOP/s), bit-identical.
 constexpr int kPBM2 = 256;
 constexpr int kPBN2 = 256;
-// Rows from which the large-tile form is used: 20-27% faster than the
-// 128 x 128 form at M = 32768 on the 4B shapes (gate|up 3.18 against
-// 3.85 ms, down 1.60 against 2.06 ms); below two row blocks its tile
-// would be mostly padding.
+// Rows from which the large-tile form is used: below two row blocks its
+// tile would be mostly padding.
 constexpr int kW8pLargeRows = 512;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+// LDS index (halves) of the 16-byte piece `piece` of activation row `row`
+GDN_DEV int dswz(int row, int piece) { return row * 64 + ((piece ^ ((row >> 1) & 7)) << 3); }
+// wait until at most N vector memory operations of this wave are outstanding
+template <int N> GDN_DEV void wait_vm() { __builtin_amdgcn_s_waitcnt((N & 15) | 0x0F70 | ((N >> 4) << 14)); }
+// barrier that waits for this wave's LDS operations only (not for its DMA)
+GDN_DEV void lds_bar() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __global__ __launch_bounds__(512, 1) void w8p2_kernel(const uint16_t *__restrict__ X, int ldx,
                                                       const int8_t *__restrict__ W, const float *__restrict__ scale,
                                                       int M, int N, int K, W8Out out) {
-    __shared__ __align__(16) uint16_t xs[2][kPBM2 * kPPitch];
+    __shared__ __align__(16) uint16_t xa[kPBM2 * 64];
+    __shared__ __align__(16) uint16_t xb[kPBM2 * 64];
+    __shared__ __align__(16) uint16_t xc[kPBM2 * 64];
+    __shared__ __align__(16) int8_t wa[4 * 4096];
+    __shared__ __align__(16) int8_t wb[4 * 4096];
+    __shared__ __align__(16) int8_t wc[4 * 4096];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;  // rows 128 wm .., channels 64 wn .. of the block
+    const int wm = wave & 1, wn = wave >> 1;
     const int n0 = blockIdx.x * kPBN2, m0 = blockIdx.y * kPBM2;
     const int steps = K / 64;
-    const int cg = n0 / 64 + wn;             // this wave's 64-channel weight group
-    const bool active = cg < N / 64;         // wave-uniform
+    const int cg = n0 / 64 + wn;
+    const bool active = cg < N / 64;
     const int l32 = lane & 31, h2 = lane >> 5;
-
-    // activation staging: chunk c = tid + 512 i is row c / 8, k 8 (c % 8) .. +7
-    const uint16_t *xp[4];
+    const uint16_t *xsrc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int c = tid + 512 * i;
-        xp[i] = X + (size_t)min(m0 + (c >> 3), M - 1) * ldx + (c & 7) * 8;
+        const int row = 32 * wave + 8 * i + (lane >> 3);
+        const int piece = (lane & 7) ^ ((row >> 1) & 7);
+        xsrc[i] = X + (size_t)min(m0 + row, M - 1) * ldx + piece * 8;
     }
-    // weight pieces: tile jt's 16-row tile 2 jt + (l32 >> 4), row l32 & 15, pieces h2 and h2 + 2
-    const int8_t *wp = W + (size_t)(active ? cg : 0) * steps * 4096 + (l32 >> 4) * 1024 + (16 * h2 + (l32 & 15)) * 16;
-    struct XStage {
-        u32x4_t x[4];
-    };
-    struct WStage {
-        u32x4_t w[2][2];  // [jt][piece]
-    };
-    auto xload = [&](int s, XStage &r) {
+    // weight DMA: wave w moves kilobytes 2w and 2w + 1 of the block's four
+    // 4 KB group tiles (group (2w + i) / 4, absent groups re-read group 0)
+    const int8_t *wsrc[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r.x[i] = *reinterpret_cast<const u32x4_t *>(xp[i] + s * 64);
-    };
-    auto wload = [&](int s, WStage &r) {
+    for (int i = 0; i < 2; ++i) {
+        const int kb = 2 * wave + i, g = kb >> 2;
+        const int gg = n0 / 64 + g < N / 64 ? n0 / 64 + g : 0;
+        wsrc[i] = W + (size_t)gg * steps * 4096 + (kb & 3) * 1024 + lane * 16;
+    }
+    auto dma = [&](int s, uint16_t *xbuf, int8_t *wbuf) {
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt)
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(xsrc[i] + s * 64, (lds_void_t *)(xbuf + (32 * wave + 8 * i) * 64), 16, 0, 0);
 #pragma unroll
-            for (int pc = 0; pc < 2; ++pc)
-                r.w[jt][pc] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4_t *>(wp + (size_t)s * 4096 + jt * 2048 + pc * 512));
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(wsrc[i] + (size_t)s * 4096, (lds_void_t *)(wbuf + (2 * wave + i) * 1024), 16, 0, 0);
     };
-    auto lstore = [&](int b, const XStage &r) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 512 * i;
-            *reinterpret_cast<u32x4_t *>(&xs[b][(c >> 3) * kPPitch + (c & 7) * 8]) = r.x[i];
-        }
-    };
-
-    f32x16_t acc[2][4];  // [channel tile jt][row tile it]
+    const int woff = wn * 4096 + (l32 >> 4) * 1024 + (16 * h2 + (l32 & 15)) * 16;
+    f32x16_t acc[2][4];
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
         for (int it = 0; it < 4; ++it)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[jt][it][e] = 0.f;
-    auto compute = [&](int b, const WStage &r) {
-        if (!active) return;
+    auto compute = [&](const uint16_t *buf, const int8_t *wbuf) {
 #pragma unroll
         for (int pc = 0; pc < 2; ++pc) {
-            f16x8_t a[2][2];  // [jt][kk % 2]
+            f16x8_t a[2][2];
 #pragma unroll
-            for (int jt = 0; jt < 2; ++jt) i8x16_to_f16(r.w[jt][pc], a[jt][0], a[jt][1]);
+            for (int jt = 0; jt < 2; ++jt)
+                i8x16_to_f16(*reinterpret_cast<const u32x4_t *>(wbuf + woff + jt * 2048 + pc * 512), a[jt][0], a[jt][1]);
 #pragma unroll
             for (int k2 = 0; k2 < 2; ++k2) {
                 const int kk = 2 * pc + k2;
-                const int koff = 32 * (kk >> 1) + 16 * h2 + 8 * (kk & 1);
+                const int piece = 4 * (kk >> 1) + 2 * h2 + (kk & 1);
                 f16x8_t bx[4];
 #pragma unroll
                 for (int it = 0; it < 4; ++it)
-                    bx[it] = *reinterpret_cast<const f16x8_t *>(&xs[b][(128 * wm + 32 * it + l32) * kPPitch + koff]);
+                    bx[it] = *reinterpret_cast<const f16x8_t *>(&buf[dswz(128 * wm + 32 * it + l32, piece)]);
 #pragma unroll
                 for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
@@ -304,32 +314,27 @@ __global__ __launch_bounds__(512, 1) void w8p2_kernel(const uint16_t *__restrict
             }
         }
     };
-
-    // step s: activations in registers X[s % 2] then LDS buffer s % 2,
-    // weights in W[s % 2]; loads of step s + 2 are issued as step s is
-    // multiplied (past the last step they re-read it: in bounds, unused)
-    XStage X0, X1;
-    WStage W0, W1;
     const int last = steps - 1;
-    xload(0, X0);
-    wload(0, W0);
-    xload(min(1, last), X1);
-    wload(min(1, last), W1);
-    lstore(0, X0);
-    __syncthreads();
-    for (int s = 0; s < steps; s += 2) {
-        xload(min(s + 2, last), X0);
-        compute(0, W0);
-        wload(min(s + 2, last), W0);
-        if (s + 1 < steps) lstore(1, X1);
-        __syncthreads();
-        if (s + 1 >= steps) break;
-        xload(min(s + 3, last), X1);
-        compute(1, W1);
-        wload(min(s + 3, last), W1);
-        if (s + 2 < steps) lstore(0, X0);
-        __syncthreads();
+    dma(0, xa, wa);
+    dma(min(1, last), xb, wb);
+    wait_vm<6>();  // step 0 landed
+    lds_bar();
+    // step s: its tiles in ring slot s % 3; the tiles of step s + 2 go into
+    // the slot step s - 1 used; step s + 1's tiles must land before the
+    // barrier that ends step s (after them come the 6 loads of step s + 2)
+#define W8P2_STEP(S, CX, CW, NX, NW)             \
+    dma(min((S) + 2, last), NX, NW);             \
+    compute(CX, CW);                             \
+    wait_vm<6>();                                \
+    lds_bar();                                   \
+    if ((S) + 1 >= steps) break;
+    for (int s = 0;; s += 3) {
+        W8P2_STEP(s, xa, wa, xc, wc)
+        W8P2_STEP(s + 1, xb, wb, xa, wa)
+        W8P2_STEP(s + 2, xc, wc, xb, wb)
     }
+#undef W8P2_STEP
+    wait_vm<0>();
     if (!active) return;
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
