@@ -99,9 +99,10 @@ def gpu_gemm_tiled(L, x16, q, s, reps=1):
                                    # a half channel block when N % 128 == 64, the 4B shapes)
                                    (17, 64, 256), (100, 192, 512), (300, 2560, 9216), (129, 18432, 2560),
                                    # M >= 512: its 256 x 256 form (ragged rows, blocks with 1-3 of
-                                   # their four 64-channel groups)
+                                   # their four 64-channel groups; 4, 8 and 12 k steps end its
+                                   # three-step buffer ring after its first, second and third slot)
                                    (1000, 12352, 2560), (513, 2560, 9216), (600, 192, 512),
-                                   (2048, 10240, 2560)])
+                                   (2048, 10240, 2560), (520, 64, 256), (777, 320, 768)])
 def test_w8a16_gemm_tiled_vs_oracle(L, M, N, K):
     """The tiled-weight GEMM (the hybrid loop's): against the oracle at the
     row-major GEMM's bar, deterministic over calls that share one workspace
