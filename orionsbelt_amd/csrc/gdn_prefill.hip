@@ -726,6 +726,154 @@ GDN_DEV void zero_upper_halves(Smem &sm, int tid) {
     }
 }
 
+// A transition chunk for column tiles c0 .. c0 + 16 NCT - 1 of the
+// 256-column state [C | Phi] (C from 0 driven by V, Phi from I with V = 0),
+// no output.  Phase 1: P = K X.
+template <int NCT>
+GDN_DEV void trans_phase1(Smem &sm, const f32x4_t (&X)[8][NCT], f32x4_t (&P)[4][NCT], int n, int n0, int lane) {
+    TileOffs to;
+    {
+        const int ln = opaque_lane(lane);
+        to = tile_offs(ln >> 4, ln & 15);
+    }
+    const uint16_t *K = sm.Kb[kslot(n, n0)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) P[i][ct] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) {
+        bf16x8_t xf[NCT];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) xf[ct] = frag_acc(X[2 * kb][ct], X[2 * kb + 1][ct]);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const bf16x8_t kf = nat_frag(K, to, rt, kb);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) P[rt][ct] = mfma_16x16x32_bf16(kf, xf[ct], P[rt][ct]);
+        }
+        // one k-block of bf16 state fragments live at a time (registers)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Phase 2: R = beta (V - e^G P), v = R + (T - I) R, and the state update.
+template <int NCT>
+GDN_DEV void trans_phase2(Smem &sm, f32x4_t (&X)[8][NCT], f32x4_t (&P)[4][NCT], int n, int n0, int c0, bool is_phi,
+                          int lane) {
+    const int g = lane >> 4;
+    TileOffs to;
+    {
+        const int ln = opaque_lane(lane);
+        to = tile_offs(ln >> 4, ln & 15);
+    }
+    const uint16_t *K = sm.Kb[kslot(n, n0)];
+    const uint16_t *V = sm.Vb[pslot(n, n0)];
+    const Gates &gt = sm.gt[pslot(n, n0)];
+    // R = beta (V - e^G P)  (Phi columns: V = 0)
+    if (is_phi) {
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const f32x4_t bt = lds_f4(&gt.bt[16 * rt + 4 * g]);
+            const f32x4_t eg = lds_f4(&gt.eg[16 * rt + 4 * g]);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) P[rt][ct][e] = -bt[e] * eg[e] * P[rt][ct][e];
+        }
+    } else {
+        int voff[NCT];
+        {
+            const int ln = opaque_lane(lane);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) voff[ct] = acc_off(c0 / 16 + ct, ln >> 4, ln & 15);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const f32x4_t bt = lds_f4(&gt.bt[16 * rt + 4 * g]);
+            const f32x4_t eg = lds_f4(&gt.eg[16 * rt + 4 * g]);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                const f32x4_t vv = acc_tile(V, voff[ct], rt);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) P[rt][ct][e] = bt[e] * (vv[e] - eg[e] * P[rt][ct][e]);
+            }
+        }
+    }
+    // v = R + (T - I) R (R as a hi + lo pair), one column tile at a time
+    // (registers)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        bf16x8_t rh[2], rl[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) frag_acc_split(P[2 * kb][ct], P[2 * kb + 1][ct], rh[kb], rl[kb]);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int kb = 0; kb <= (rt >> 1); ++kb) {
+                const bf16x8_t tf = frag_ld(sm.Tf[pslot(n, n0)][fidx(rt, kb)][lane]);
+                P[rt][ct] = mfma_16x16x32_bf16(tf, rh[kb], P[rt][ct]);
+                P[rt][ct] = mfma_16x16x32_bf16(tf, rl[kb], P[rt][ct]);
+            }
+    }
+    {
+        const float gam = gt.gam;
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) X[rt][ct][e] *= gam;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const f32x4_t slo = lds_f4(&gt.egl[32 * kb + 4 * g]);
+            const f32x4_t shi = lds_f4(&gt.egl[32 * kb + 16 + 4 * g]);
+            bf16x8_t vg[NCT];
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) vg[ct] = frag_acc_scaled(P[2 * kb][ct], P[2 * kb + 1][ct], slo, shi);
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt) {
+                const bf16x8_t kt = kt_frag(K, to, rt, kb);
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) X[rt][ct] = mfma_16x16x32_bf16(kt, vg[ct], X[rt][ct]);
+            }
+        }
+    }
+}
+
+// The state's columns in a transition segment: the state waves 0 .. 3 hold
+// 48 columns each (waves 0, 1: C columns 0 .. 95; waves 2, 3: Phi columns
+// 0 .. 95), helpers 1 and 2 the last 32 columns of C and of Phi, in the
+// phases where their helper work leaves room (no q in such a segment).
+constexpr int kTransCols = 48;
+constexpr int kTransHelperCols = D - 2 * kTransCols;
+
+// Initial transition state for column tiles from c0: 0 (C) or I (Phi).
+template <int NCT>
+GDN_DEV void trans_init(f32x4_t (&X)[8][NCT], int c0, bool is_phi, int g, int r) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) X[rt][ct][e] = (is_phi && srow(rt, g, e) == c0 + 16 * ct + r) ? 1.f : 0.f;
+}
+
+// State waves of a transition segment.
+template <int NCT>
+GDN_DEV void state_loop_trans(Smem &sm, f32x4_t (&X)[8][NCT], int n0, int n1, int c0, bool is_phi, int lane) {
+    lds_barrier();
+    lds_barrier();
+    lds_barrier();
+    for (int n = n0; n < n1; ++n) {
+        f32x4_t P[4][NCT];
+        trans_phase1<NCT>(sm, X, P, n, n0, lane);
+        lds_barrier();  // X
+        trans_phase2<NCT>(sm, X, P, n, n0, c0, is_phi, lane);
+        lds_barrier();  // Y
+    }
+}
+
 // Helper waves (hw = wave - 4) of a segment over chunks [n0, n1).  WITH_Q:
 // output segment (q rows, K Q^T and the A fragments).  The barrier sequence
 // matches the state loops'.  In iteration n (the state waves on chunk n):
@@ -737,11 +885,20 @@ GDN_DEV void zero_upper_halves(Smem &sm, int tid) {
 //            fragments of chunk n+1 (rows {0, 3} and {1, 2}), and hw3 waits
 //            for its loads; hw2 issues the loads of the q rows of chunk n+2,
 //            which it waits for at the end of the next phase 1.
-// In a transition segment (no q) hw2 loads chunk n+1's v rows in phase 2
-// instead of hw3 in phase 1, and waits for them before the phase ends.
+// In a transition segment (no q) hw3 loads chunk n+1's v rows in phase 2
+// instead of in phase 1, and waits for them before the phase ends.
 // Every load thus has at least a whole phase to land.
-template <bool WITH_Q>
-GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n1, int hw, int lane) {
+// SNCT > 0 (a transition segment): helpers 1 and 2, which issue no loads
+// there, also run SNCT column tiles of the state from column c0 (C for
+// helper 1, Phi for helper 2).
+template <bool WITH_Q, int SNCT = 0>
+GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n1, int hw, int lane,
+                         f32x4_t (&X)[8][SNCT > 0 ? SNCT : 1], int c0 = 0) {
+    // with SNCT > 0 only helpers 1 and 2 run this instance: helper 0's role
+    // and helper 2's loads are dead code in it, so that their registers (T's
+    // rows kept across the phases) and the state's are never live together
+    const bool with_state = SNCT > 0;
+    const bool h0 = SNCT == 0 && hw == 0, h2 = SNCT == 0 && hw == 2;
     const int g = lane >> 4, r = lane & 15;
     const int kh = h / (a.Hv / a.Hk);
     const int NC = a.NC;
@@ -782,14 +939,14 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
     if (hw == 1) kk(n0, true);
     else if (hw == 2) kk(n0, false);
     else if (WITH_Q && hw == 3) qk(n0, true);
-    else if (WITH_Q && hw == 0) qk(n0, false);
+    else if (WITH_Q && h0) qk(n0, false);
     lds_barrier();
-    if (hw == 0) t_subst(sm, sm.Tf[pslot(n0, n0)], tr, lane);
+    if (h0) t_subst(sm, sm.Tf[pslot(n0, n0)], tr, lane);
     lds_barrier();
     for (int n = n0; n < n1; ++n) {
         const bool more = n + 1 < n1;
         const int c2 = min(n + 2, NC - 1), c1 = min(n + 1, NC - 1);
-        if (hw == 0) {
+        if (h0) {
             __builtin_amdgcn_s_setprio(3);
             t_chain(sm.Tf[pslot(n, n0)], tr, lane);
             __builtin_amdgcn_s_setprio(0);
@@ -804,23 +961,26 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
             kk(n + 1, hw == 1);
             __builtin_amdgcn_s_setprio(0);
         }
-        if (hw == 2) wait_vmem0();  // q rows of chunk n+1
+        [[maybe_unused]] f32x4_t P[4][SNCT > 0 ? SNCT : 1];
+        if constexpr (SNCT > 0)
+            if (with_state) trans_phase1<SNCT>(sm, X, P, n, n0, lane);
+        if (h2) wait_vmem0();  // q rows of chunk n+1
         lds_barrier();              // X
-        if (hw == 0) {
+        if (h0) {
             if (more) t_subst(sm, sm.Tf[pslot(n + 1, n0)], tr, lane);
-        } else if (hw == 2) {
+        } else if (WITH_Q && h2) {
             // into the slot chunk n's q leaves (read in phase 1 only)
-            if (WITH_Q) {
-                load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
-            } else {
-                // transition segments: the v rows of chunk n+1 (whose slot
-                // chunk n-1 left), here rather than with helper 3's loads in
-                // phase 1, which bound that phase; phase 2 outlasts them
-                load_rows_n<16>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 0, lane);
-                wait_vmem0();
-            }
+            load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
         } else {
+            // transition segments: the v rows of chunk n+1 (whose slot chunk
+            // n-1 left), here rather than with the phase-1 loads, which bound
+            // that phase; phase 2 outlasts them.  Only helper 3 issues loads
+            // there: a wave that reads LDS after its own DMA waits for that
+            // DMA first
+            if (!WITH_Q && hw == 3) load_rows_n<16>(sm.Vb[pslot(n + 1, n0)], a.v, a.Hv, h, b, c1, a.T, 0, lane);
             if (WITH_Q && more) qk(n + 1, hw == 3);
+            if constexpr (SNCT > 0)
+                if (with_state) trans_phase2<SNCT>(sm, X, P, n, n0, c0, hw == 2, lane);
             if (hw == 3) wait_vmem0();  // k rows, gates of chunk n+2, v rows of n+1
         }
         lds_barrier();  // Y
@@ -971,117 +1131,6 @@ GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int 
     }
 }
 
-// State waves of a transition segment: 64 columns of the 256-column state
-// [C | Phi] (waves 0, 1: C from 0 driven by V; waves 2, 3: Phi from I with
-// V = 0), no output.
-GDN_DEV void state_loop_trans(Smem &sm, f32x4_t (&X)[8][4], const SegArgs &a, int n0, int n1, int c0,
-                              bool is_phi, int lane) {
-    const int g = lane >> 4;
-    lds_barrier();
-    lds_barrier();
-    lds_barrier();
-    for (int n = n0; n < n1; ++n) {
-        TileOffs to;
-        {
-            const int ln = opaque_lane(lane);
-            to = tile_offs(ln >> 4, ln & 15);
-        }
-        const uint16_t *K = sm.Kb[kslot(n, n0)];
-        const uint16_t *V = sm.Vb[pslot(n, n0)];
-        const Gates &gt = sm.gt[pslot(n, n0)];
-        f32x4_t P[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) P[i][ct] = zero4();
-#pragma unroll
-        for (int kb = 0; kb < D / 32; ++kb) {
-            bf16x8_t xf[4];
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) xf[ct] = frag_acc(X[2 * kb][ct], X[2 * kb + 1][ct]);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                const bf16x8_t kf = nat_frag(K, to, rt, kb);
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) P[rt][ct] = mfma_16x16x32_bf16(kf, xf[ct], P[rt][ct]);
-            }
-            // one k-block of bf16 state fragments live at a time (registers)
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        lds_barrier();  // X
-        // R = beta (V - e^G P)  (Phi columns: V = 0)
-        int voff[4];
-        {
-            const int ln = opaque_lane(lane);
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) voff[ct] = acc_off(c0 / 16 + ct, ln >> 4, ln & 15);
-        }
-        if (is_phi) {
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                const f32x4_t bt = lds_f4(&gt.bt[16 * rt + 4 * g]);
-                const f32x4_t eg = lds_f4(&gt.eg[16 * rt + 4 * g]);
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) P[rt][ct][e] = -bt[e] * eg[e] * P[rt][ct][e];
-            }
-        } else {
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                const f32x4_t bt = lds_f4(&gt.bt[16 * rt + 4 * g]);
-                const f32x4_t eg = lds_f4(&gt.eg[16 * rt + 4 * g]);
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                    const f32x4_t vv = acc_tile(V, voff[ct], rt);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) P[rt][ct][e] = bt[e] * (vv[e] - eg[e] * P[rt][ct][e]);
-                }
-            }
-        }
-        // v = R + (T - I) R (R as a hi + lo pair), one column tile at a time
-        // (registers)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            bf16x8_t rh[2], rl[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) frag_acc_split(P[2 * kb][ct], P[2 * kb + 1][ct], rh[kb], rl[kb]);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-                for (int kb = 0; kb <= (rt >> 1); ++kb) {
-                    const bf16x8_t tf = frag_ld(sm.Tf[pslot(n, n0)][fidx(rt, kb)][lane]);
-                    P[rt][ct] = mfma_16x16x32_bf16(tf, rh[kb], P[rt][ct]);
-                    P[rt][ct] = mfma_16x16x32_bf16(tf, rl[kb], P[rt][ct]);
-                }
-        }
-        {
-            const float gam = gt.gam;
-#pragma unroll
-            for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) X[rt][ct][e] *= gam;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const f32x4_t slo = lds_f4(&gt.egl[32 * kb + 4 * g]);
-                const f32x4_t shi = lds_f4(&gt.egl[32 * kb + 16 + 4 * g]);
-                bf16x8_t vg[4];
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) vg[ct] = frag_acc_scaled(P[2 * kb][ct], P[2 * kb + 1][ct], slo, shi);
-#pragma unroll
-                for (int rt = 0; rt < 8; ++rt) {
-                    const bf16x8_t kt = kt_frag(K, to, rt, kb);
-#pragma unroll
-                    for (int ct = 0; ct < 4; ++ct) X[rt][ct] = mfma_16x16x32_bf16(kt, vg[ct], X[rt][ct]);
-                }
-            }
-        }
-        lds_barrier();  // Y
-    }
-}
-
 // Start state of segment p >= 1 of pass 2, composed by the workgroup itself:
 // S_start(1) = the end state of segment 0 (in the carry); for q = 1 .. p-1,
 // S_start(q+1) = Phi_q S_start(q) + C_q.  Phi_{q+1} streams from the carry
@@ -1177,7 +1226,10 @@ GDN_DEV void run_output(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, i
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     zero_upper_halves(sm, tid);
     if (wave < NSW) state_loop_out(sm, S, a, b, h, n0, n1, 32 * wave, lane);
-    else helper_loop<true>(sm, a, b, h, n0, n1, wave - NSW, lane);
+    else {
+        f32x4_t none[8][1];
+        helper_loop<true>(sm, a, b, h, n0, n1, wave - NSW, lane, none);
+    }
 }
 
 // Pass 1: slot p = blockIdx.y < P-1.  Segment 0 runs the output recurrence
@@ -1206,20 +1258,25 @@ __global__ __launch_bounds__(NT) void prefill_pass1_kernel(SegArgs a) {
     } else {
         zero_upper_halves(sm, tid);
         if (wave < NSW) {
+            constexpr int NCT = kTransCols / 16;
             const bool is_phi = wave >= 2;
-            const int c0 = 64 * (wave & 1);
-            f32x4_t X[8][4];
-#pragma unroll
-            for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        X[rt][ct][e] = (is_phi && srow(rt, g, e) == c0 + 16 * ct + r) ? 1.f : 0.f;
-            state_loop_trans(sm, X, a, n0, n1, c0, is_phi, lane);
-            tiles_store<kF32, 4>(X, carry_slot(a.carry, b, h, a.Hv, a.P, p, is_phi ? kPhi : kCst), c0, g, r);
+            const int c0 = kTransCols * (wave & 1);
+            f32x4_t X[8][NCT];
+            trans_init<NCT>(X, c0, is_phi, g, r);
+            state_loop_trans<NCT>(sm, X, n0, n1, c0, is_phi, lane);
+            tiles_store<kF32, NCT>(X, carry_slot(a.carry, b, h, a.Hv, a.P, p, is_phi ? kPhi : kCst), c0, g, r);
+        } else if (wave == NSW + 1 || wave == NSW + 2) {
+            constexpr int NCT = kTransHelperCols / 16;
+            const int hw = wave - NSW;
+            const bool is_phi = hw == 2;
+            const int c0 = 2 * kTransCols;
+            f32x4_t X[8][NCT];
+            trans_init<NCT>(X, c0, is_phi, g, r);
+            helper_loop<false, NCT>(sm, a, b, h, n0, n1, hw, lane, X, c0);
+            tiles_store<kF32, NCT>(X, carry_slot(a.carry, b, h, a.Hv, a.P, p, is_phi ? kPhi : kCst), c0, g, r);
         } else {
-            helper_loop<false>(sm, a, b, h, n0, n1, wave - NSW, lane);
+            f32x4_t none[8][1];
+            helper_loop<false>(sm, a, b, h, n0, n1, wave - NSW, lane, none);
         }
     }
 }
@@ -1265,18 +1322,19 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
 // (kCostPrologue + kCostStep per transition composed); segment P-1 runs in
 // pass 2 only.  The lengths minimise the modelled pass 1 + pass 2 time:
 // transitions share one cap M, segment 0 takes kCostTrans * M, and the
-// pass-2 segments shrink with their composition cost.  The costs are
-// measured per-chunk times of the kernels (shader-clock counters: an output
-// chunk 7.4K cycles, a transition chunk 9.5K, a composition step 9.3K);
-// against the earlier 1.17 / 1.12 / 0.5 they plan 2% faster calls at
-// T = 16K, 32 heads.
+// pass-2 segments shrink with their composition cost.  The costs come from
+// the kernels' per-chunk times (shader-clock counters: an output chunk 7.4K
+// cycles, a composition step 9.3K) and, for the transition chunk since six
+// waves share its state, from timing plans of different costs: at T = 16K,
+// 32 heads, 1.10 measured 231.1 us against 234.4 (1.20), 232.4 (1.00) and
+// 238.5 (1.28, the cost when four waves held the state).
 // 4 chunks per segment at least: against 8, short sequences gain more from
 // the parallel segments than they lose to transitions (T = 1K: 53.3 against
 // 56.6 us, 2K: 68.7 against 77.9 us, 4K: 93.1 against 94.5 us; 3 is as good
 // at 1K and worse at 2K)
 constexpr int kMinSegChunks = 4;
 constexpr int kTargetWgs = 256;
-constexpr double kCostTrans = 1.28, kCostStep = 1.26, kCostPrologue = 1.0;
+constexpr double kCostTrans = 1.10, kCostStep = 1.26, kCostPrologue = 1.0;
 
 struct SegPlan {
     int P;

@@ -132,6 +132,6 @@ def test_prefill_workspace_query_needs_no_device():
     assert L.kai_gdn_hip_prefill_workspace_bytes(1, 1024, 32) == 4 * 32 * slot
     for T in (8192, 16384, 131072):
         assert L.kai_gdn_hip_prefill_workspace_bytes(1, T, 32) == 9 * 32 * slot
-    assert L.kai_gdn_hip_prefill_workspace_bytes(1, 16384, 4) == 24 * 4 * slot
+    assert L.kai_gdn_hip_prefill_workspace_bytes(1, 16384, 4) == 23 * 4 * slot
     for bad in ((0, 16384, 32), (1, 0, 32), (1, 16384, 0), (-1, 16384, 32)):
         assert L.kai_gdn_hip_prefill_workspace_bytes(*bad) == 0
