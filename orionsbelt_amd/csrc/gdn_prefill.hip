@@ -28,8 +28,9 @@
 //           segment 0, then reruns the recurrence from it, with o.
 //
 // Workgroup: 8 waves in two roles, one of each role per SIMD.
-//  - State waves 0..3 own 32 state columns each (64 in a transition
-//    segment) in VGPRs and run the S-dependent products of chunk n:
+//  - State waves 0..3 own 32 state columns each (48 of the 256 in a
+//    transition segment, where helpers 1 and 2 own the last 32 columns of
+//    C and of Phi) in VGPRs and run the S-dependent products of chunk n:
 //    P = K S and O = Q S (phase 1), then v = T diag(beta)(V - e^G P),
 //    o^T = e^G scale O^T + v^T A^T and the state update (phase 2).
 //  - Helper waves 4..7 prepare the S-independent operands one chunk ahead
@@ -44,9 +45,10 @@
 //  work of one role overlaps the latency-bound work of the other.
 //
 // Loads: helpers 2 and 3 move chunk tiles straight from HBM into LDS
-// (global_load_lds_dwordx4, 1 KiB per wave instruction) in phase 2 of
-// chunk n: the k and q rows, gates and betas of chunk n+2 and the v rows
-// of chunk n+1, and wait for them before the barrier that ends the chunk.
+// (global_load_lds_dwordx4, 1 KiB per wave instruction): the k and q rows,
+// gates and betas of chunk n+2 and the v rows of chunk n+1, each at least
+// one phase before the barrier that publishes it (helper 3 alone in a
+// transition segment).
 // Rows past the sequence end read its last row (their values are
 // multiplied by beta = 0 or never stored).
 //
