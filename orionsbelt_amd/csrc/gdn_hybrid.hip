@@ -361,6 +361,10 @@ struct kai_gdn_hybrid {
     gdn::Mat lm;
     // step buffers
     float *h = nullptr, *mix = nullptr, *mlp = nullptr;
+    // small batches: the residual stream alternates between h and h2, and
+    // the next matrix normalises its own input from the pending branch
+    float *h2 = nullptr, *hcur = nullptr, *hnext = nullptr;
+    const float *pend_add = nullptr, *pend_w = nullptr;
     float *qkv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr;
     float *qg = nullptr, *kx = nullptr, *vx = nullptr, *logits = nullptr;
     int32_t *next = nullptr;
@@ -369,7 +373,6 @@ struct kai_gdn_hybrid {
     uint16_t *x16 = nullptr, *act16 = nullptr, *q16 = nullptr, *o16 = nullptr;
     float *gemm_part = nullptr, *attn_ws = nullptr;
     uint32_t *gemm_cnt = nullptr;  // zero between launches
-    uint32_t *norm_cnt = nullptr;  // the fused add + norm's grid counter, zero between launches
     // prefill buffers, allocated by the first prefill for max_context rows
     struct Prefill {
         int rows = 0, tv = 0;  // capacity (positions) and the V^T row length
@@ -491,29 +494,43 @@ hipError_t gemm_to(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *y,
     return gemm(m, x, w, segments({{y, ld, w.N}}), st);
 }
 
-// Up to this many sequences, a residual branch's matrix ends with the
-// residual add and the next RMSNorm in its last block (kW8AddNorm): at
-// batch 1 that saves a 3.5 us launch per norm.  Above, one block per row
-// in a kernel of its own is faster than one block for every row.
-constexpr int kFuseNormRows = 2;
+// Up to this many sequences, the matrices that read the residual stream's
+// norm (the in-projections, gate|up, lm_head) form it themselves: every
+// block adds the pending branch and normalises the row into LDS while its
+// first weights are in flight (W8Out::nin_*).  That replaces the norm
+// kernel, and the residual add at the end of the branch matrices, at no
+// cost to the reading matrix.  Above, one block per row in a kernel of its
+// own is faster than every block normalising every row.
+bool norm_in(const kai_gdn_hybrid *m) { return m->batch <= kW8NormInRows && m->cfg.hidden <= kW8NormInMaxK; }
 
-// d = x W^T (the branch); h += d; x16 = fp16(rmsnorm(h) * (1 + norm_w))
+// d = x W^T (the branch); h += d; x16 = fp16(rmsnorm(h) * (1 + norm_w)),
+// or, for small batches, the add and the norm left to the next matrix
 hipError_t gemm_addnorm(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *d, const float *norm_w,
                         hipStream_t st) {
     const int B = m->batch, H = m->cfg.hidden;
-    if (B <= kFuseNormRows && H <= 4096) {
-        W8Out o = segments({{d, H, H}});
-        o.mode = kW8AddNorm;
-        o.h = m->h;
-        o.norm_w = norm_w;
-        o.eps = m->cfg.rms_eps;
-        o.x16 = m->x16;
-        o.norm_cnt = m->norm_cnt;
-        return gemm(m, x, w, o, st);
-    }
     TRY(gemm_to(m, x, w, d, H, st));
+    if (norm_in(m)) {
+        m->pend_add = d;
+        m->pend_w = norm_w;
+        return hipSuccess;
+    }
     addnorm_kernel<<<B, 256, 0, st>>>(m->h, d, norm_w, m->x16, H, m->cfg.rms_eps);
     return hipGetLastError();
+}
+
+// o = norm(h) W^T: from x16, or, for small batches, normalising the
+// residual stream (plus the pending branch) in the matrix's own blocks
+hipError_t gemm_in(kai_gdn_hybrid *m, const Mat &w, W8Out o, hipStream_t st) {
+    if (!norm_in(m)) return gemm(m, m->x16, w, o, st);
+    o.nin_h = m->hcur;
+    o.nin_add = m->pend_add;
+    o.nin_hout = m->pend_add ? m->hnext : nullptr;
+    o.nin_w = m->pend_w;
+    o.nin_eps = m->cfg.rms_eps;
+    TRY(gemm(m, nullptr, w, o, st));
+    if (m->pend_add) std::swap(m->hcur, m->hnext);
+    m->pend_add = nullptr;
+    return hipSuccess;
 }
 
 hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
@@ -576,6 +593,7 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         // step buffers
         const size_t wide16 = std::max({(size_t)H, (size_t)m->value_dim, (size_t)Hq * 256});
         TRY(alloc_t(m, &m->h, (size_t)Bm * H));
+        TRY(alloc_t(m, &m->h2, (size_t)Bm * H));
         TRY(alloc_t(m, &m->mix, (size_t)Bm * H));
         TRY(alloc_t(m, &m->mlp, (size_t)Bm * H));
         TRY(alloc_t(m, &m->qkv, (size_t)Bm * m->conv_dim));
@@ -592,8 +610,6 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
         TRY(hipMemset(m->arg_cnt, 0, (size_t)Bm * sizeof(uint32_t)));
         TRY(alloc_t(m, &m->x16, (size_t)Bm * wide16));
         TRY(alloc_t(m, &m->o16, (size_t)Bm * wide16));
-        TRY(alloc_t(m, &m->norm_cnt, 1));
-        TRY(hipMemset(m->norm_cnt, 0, sizeof(uint32_t)));
         TRY(alloc_t(m, &m->act16, (size_t)Bm * I));
         TRY(alloc_t(m, &m->q16, (size_t)Bm * Hq * 256));
         // GEMM split-K partials and counters: the largest over the model's matrices
@@ -624,7 +640,7 @@ hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
 hipError_t gdn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     const kai_gdn_hybrid_config &c = m->cfg;
     const int B = m->batch, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads, C = m->conv_dim, V = m->value_dim;
-    TRY(gemm(m, m->x16, L.in, segments({{m->qkv, C, C}, {m->zb, V, C + V}, {m->bb, Hv, C + V + Hv},
+    TRY(gemm_in(m, L.in, segments({{m->qkv, C, C}, {m->zb, V, C + V}, {m->bb, Hv, C + V + Hv},
                                         {m->ab, Hv, C + V + 2 * Hv}}), st));
     // conv update, gating prologue, delta rule, gated RMSNorm -> fp16: one kernel
     TRY(launch_gdn_step_fused(m->qkv, L.conv_state[m->parity], L.conv_state[m->parity ^ 1], L.conv_w, m->ab,
@@ -637,7 +653,7 @@ hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     const kai_gdn_hybrid_config &c = m->cfg;
     const int B = m->batch, Hq = c.attn_q_heads, Hkv = c.attn_kv_heads;
     const int nq = Hq * 512, nkv = Hkv * 256;
-    TRY(gemm(m, m->x16, L.in, segments({{m->qg, nq, nq}, {m->kx, nkv, nq + nkv}, {m->vx, nkv, nq + 2 * nkv}}),
+    TRY(gemm_in(m, L.in, segments({{m->qg, nq, nq}, {m->kx, nkv, nq + nkv}, {m->vx, nkv, nq + 2 * nkv}}),
              st));
     attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, B), 256, 0, st>>>(m->qg, m->kx, m->vx, L.q_norm, L.k_norm, m->q16,
                                                                  L.Kc, L.Vc, Hq, Hkv, m->tmax, -1, m->pos,
@@ -660,17 +676,23 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
     // each residual branch's matrix (out, down) adds the branch to h and
     // normalises h for the next matrix: the next layer's input norm, or the
     // final norm after the last layer
-    addnorm_kernel<<<B, 256, 0, st>>>(m->h, nullptr, m->layers[0].ln_in, m->x16, H, c.rms_eps);
-    TRY(hipGetLastError());
+    m->hcur = m->h;
+    m->hnext = m->h2;
+    m->pend_add = nullptr;
+    m->pend_w = m->layers[0].ln_in;
+    if (!norm_in(m)) {
+        addnorm_kernel<<<B, 256, 0, st>>>(m->h, nullptr, m->layers[0].ln_in, m->x16, H, c.rms_eps);
+        TRY(hipGetLastError());
+    }
     for (size_t l = 0; l < m->layers.size(); ++l) {
         Layer &L = m->layers[l];
         TRY(L.attn ? attn_mixer(m, L, st) : gdn_mixer(m, L, st));
-        TRY(gemm(m, m->x16, L.gate_up, swiglu, st));
+        TRY(gemm_in(m, L.gate_up, swiglu, st));
         const float *next_norm = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : m->final_norm;
         TRY(gemm_addnorm(m, m->act16, L.down, m->mlp, next_norm, st));
     }
     float *lg = logits ? logits : m->logits;
-    TRY(gemm(m, m->x16, m->lm, segments({{lg, c.vocab, c.vocab}}), st));
+    TRY(gemm_in(m, m->lm, segments({{lg, c.vocab, c.vocab}}), st));
     argmax_kernel<<<dim3(kArgBlocks, B), 256, 0, st>>>(lg, next ? next : m->next, c.vocab, m->arg_part,
                                                        m->arg_cnt);
     TRY(hipGetLastError());

@@ -134,12 +134,7 @@ hipError_t launch_w8_gemm(const uint16_t *x, const int8_t *W, const float *scale
 // splits > 1, `part` holds w8f_workspace_floats(M, N, K) floats and `cnt`
 // N / 64 counters that are zero before the first launch (each launch leaves
 // them zero); launches sharing them must not overlap.
-// kW8AddNorm: y -> seg[0].dst [M][N] (a residual branch d, row stride N);
-// then the grid's last block (norm_cnt, zero between launches) updates the
-// residual stream and normalises it for the next matrix, row by row:
-//   h += d;  x16 = fp16(h * rsqrt(mean(h^2) + eps) * (1 + norm_w))
-// (N <= 4096; the rows are done by one block, so meant for small M).
-enum W8Mode : int { kW8Segments = 0, kW8SwiGLU = 1, kW8AddNorm = 2 };
+enum W8Mode : int { kW8Segments = 0, kW8SwiGLU = 1 };
 constexpr int kW8MaxSegs = 4;
 struct W8Seg {
     float *dst;
@@ -151,11 +146,19 @@ struct W8Out {
     int nseg;
     int mode;
     uint16_t *x16;
-    float *h;              // kW8AddNorm: the residual stream [M][N]
-    const float *norm_w;   // kW8AddNorm: [N]
-    float eps;
-    uint32_t *norm_cnt;    // kW8AddNorm: one counter, zero between launches
+    // Normalised input (the decode GEMM, M <= kW8NormInRows, K <= kW8NormInMaxK):
+    // with nin_h set, the matrix's input is fp16(rmsnorm(h') * (1 + nin_w))
+    // with h' = nin_h + nin_add (nin_add may be null), formed by every block
+    // in LDS with the residual norm's arithmetic; the block of the first
+    // channel group writes h' to nin_hout (when set).  x is then unused.
+    const float *nin_h;
+    const float *nin_add;
+    float *nin_hout;
+    const float *nin_w;
+    float nin_eps;
 };
+constexpr int kW8NormInRows = 2;
+constexpr int kW8NormInMaxK = 4096;
 // Launch shape: waves per block (4 or 8), 64-k steps in flight per wave (1,
 // 2 or 4), k-splits across blocks (0: chosen by w8f_shape).
 struct W8fShape {

@@ -175,11 +175,10 @@ hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, i
 //   kW8SwiGLU:   the rows are gate/up interleaved in groups of 8 (tile rows
 //                0..7 gate channels 8t..8t+7, rows 8..15 the up channels),
 //                out16[m][c] = fp16(silu(gate) * up) (Qwen3_5MLP,
-//                modeling_qwen3_5.py:704-717);
-//   kW8AddNorm:  y into a residual branch, then the grid's last block adds
-//                it to the residual stream and applies the next RMSNorm
-//                (Qwen3_5RMSNorm, weight 1 + w) into fp16 -- the decoder
-//                layer's "h = h + branch; x = norm(h)" without a launch.
+//                modeling_qwen3_5.py:704-717).
+// With W8Out::nin_h set, the input is formed in each block instead of read:
+// the decoder layer's "h = h + branch; x = norm(h)" (Qwen3_5RMSNorm, weight
+// 1 + w) ahead of the matrix that reads x, without a launch of its own.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -201,59 +200,60 @@ __global__ __launch_bounds__(256) void w8f_tile_kernel(const int8_t *__restrict_
     *reinterpret_cast<uint4 *>(dst + q * 16) = *reinterpret_cast<const uint4 *>(src + n * K + k);
 }
 
-// kW8AddNorm's last block, 256 threads: row b of d (written in this launch
-// by other blocks, so read through sc1), h and x16 as W8Out describes.
-__device__ void w8f_addnorm_rows(const W8Out &out, int M, int N, float *s_ss) {
-    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(out.seg[0].dst, 0, 0x7FFFFFFF, kBufFlags);
-    const int n4 = N / 4, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// The normalised input of a block (W8Out::nin_*), threads 0..255 with the
+// arithmetic of the hybrid model's addnorm kernel (the same per-thread
+// chunks and wave-sum pairing, so the rows are bit-identical): xs[b][k] = fp16(h'[b][k] * inv * (1 + w[k])), h' = h + add;
+// `writer` stores h'.  Every thread of the block calls it (barriers).
+__device__ void w8f_norm_input(const W8Out &out, int M, int K, uint16_t *xs, float *s_ss, bool writer) {
+    const int n4 = K / 4, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int b = 0; b < M; ++b) {
-        f32x4_t x[4], dv[4];
-        float4 *hr = reinterpret_cast<float4 *>(out.h + (size_t)b * N);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            if (i < n4) {
-                dv[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, (b * N + 4 * i) * 4,
-                                                                                          0, kSc1));
-                const float4 hv = hr[i];
-                x[j] = f32x4_t{hv.x, hv.y, hv.z, hv.w};
-            }
-        }
+        f32x4_t x[4];
         float ss = 0.f;
+        if (tid < 256) {
+            const float4 *hr = reinterpret_cast<const float4 *>(out.nin_h + (size_t)b * K);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            if (i < n4) {
-                x[j] += dv[j];
-                hr[i] = make_float4(x[j][0], x[j][1], x[j][2], x[j][3]);
-                ss += x[j][0] * x[j][0] + x[j][1] * x[j][1] + x[j][2] * x[j][2] + x[j][3] * x[j][3];
+            for (int j = 0; j < 4; ++j) {
+                const int i = tid + 256 * j;
+                if (i < n4) {
+                    const float4 hv = hr[i];
+                    x[j] = f32x4_t{hv.x, hv.y, hv.z, hv.w};
+                    if (out.nin_add) {
+                        const float4 dv = reinterpret_cast<const float4 *>(out.nin_add + (size_t)b * K)[i];
+                        x[j] += f32x4_t{dv.x, dv.y, dv.z, dv.w};
+                        if (writer)
+                            reinterpret_cast<float4 *>(out.nin_hout + (size_t)b * K)[i] =
+                                make_float4(x[j][0], x[j][1], x[j][2], x[j][3]);
+                    }
+                    ss += x[j][0] * x[j][0] + x[j][1] * x[j][1] + x[j][2] * x[j][2] + x[j][3] * x[j][3];
+                }
             }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            if (lane == 0) s_ss[wave] = ss;
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) s_ss[wave] = ss;
         __syncthreads();
-        // the wave sums in the pairing of the hybrid model's addnorm kernel,
-        // so both paths give bit-identical rows
-        const float inv = 1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)N + out.eps);
+        const float inv = 1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)K + out.nin_eps);
         __syncthreads();  // s_ss is rewritten by the next row
+        if (tid < 256) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            if (i < n4) {
-                const float4 wv = reinterpret_cast<const float4 *>(out.norm_w)[i];
-                uint2 o;
-                o.x = (uint32_t)f32_to_f16_rne(x[j][0] * inv * (1.0f + wv.x)) |
-                      ((uint32_t)f32_to_f16_rne(x[j][1] * inv * (1.0f + wv.y)) << 16);
-                o.y = (uint32_t)f32_to_f16_rne(x[j][2] * inv * (1.0f + wv.z)) |
-                      ((uint32_t)f32_to_f16_rne(x[j][3] * inv * (1.0f + wv.w)) << 16);
-                reinterpret_cast<uint2 *>(out.x16 + (size_t)b * N)[i] = o;
+            for (int j = 0; j < 4; ++j) {
+                const int i = tid + 256 * j;
+                if (i < n4) {
+                    const float4 wv = reinterpret_cast<const float4 *>(out.nin_w)[i];
+                    uint2 o;
+                    o.x = (uint32_t)f32_to_f16_rne(x[j][0] * inv * (1.0f + wv.x)) |
+                          ((uint32_t)f32_to_f16_rne(x[j][1] * inv * (1.0f + wv.y)) << 16);
+                    o.y = (uint32_t)f32_to_f16_rne(x[j][2] * inv * (1.0f + wv.z)) |
+                          ((uint32_t)f32_to_f16_rne(x[j][3] * inv * (1.0f + wv.w)) << 16);
+                    *reinterpret_cast<uint2 *>(&xs[(size_t)b * K + 4 * i]) = o;
+                }
             }
         }
     }
+    __syncthreads();
 }
 
-template <int WAVES, int DEPTH>
+template <int WAVES, int DEPTH, bool NORM_IN = false>
 __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restrict__ x,
                                                          const int8_t *__restrict__ W,
                                                          const float *__restrict__ scale, int M, int N, int K,
@@ -262,6 +262,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
     __shared__ f32x4_t red[WAVES][4][64];
     __shared__ float s_ss[4];
     __shared__ bool last;
+    extern __shared__ __align__(16) uint16_t xs[];  // NORM_IN: the normalised rows [M][K] (dynamic)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, r = lane & 15;
     const int c = blockIdx.x;
@@ -272,7 +273,8 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
     const int8_t *wp = W + ((size_t)c * (K / kKStep) + kb / kKStep) * 4096 + lane * 16;
     const bool row_ok = r < M;
     // rows past M read row 0 (in bounds, one cache line per wave) and are zeroed
-    const uint16_t *xp = x + (size_t)(row_ok ? r : 0) * K + kb + 16 * g;
+    const uint16_t *xp = NORM_IN ? &xs[(size_t)(row_ok ? r : 0) * K + kb + 16 * g]
+                                 : x + (size_t)(row_ok ? r : 0) * K + kb + 16 * g;
     f32x4_t acc[4] = {zero4(), zero4(), zero4(), zero4()};
     u32x4_t buf[DEPTH][4];
     auto load_w = [&](u32x4_t (&w)[4], int st) {
@@ -296,6 +298,8 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
     // DEPTH steps in flight: step st + DEPTH is requested as step st is used
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i) load_w(buf[i], i);
+    // the normalised input forms while the first weight steps are in flight
+    if constexpr (NORM_IN) w8f_norm_input(out, M, K, xs, s_ss, blockIdx.x == 0 && blockIdx.y == 0);
     int base = 0;
     for (; base + DEPTH < nsteps; base += DEPTH) {
 #pragma unroll
@@ -361,14 +365,6 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
             const int cc = (n0 + 16 * j) / 2 + 4 * g;
             *reinterpret_cast<uint2 *>(out.x16 + (size_t)r * (N / 2) + cc) = make_uint2(h[0], h[1]);
         }
-    } else if (out.mode == kW8AddNorm) {
-        const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(out.seg[0].dst, 0, 0x7FFFFFFF, kBufFlags);
-        if (row_ok) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), rd, (r * N + n) * 4, 0, kSc1);
-        stores_done();
-        __syncthreads();
-        if (threadIdx.x == 0) last = arrive_last(out.norm_cnt, gridDim.x);
-        __syncthreads();
-        if (last) w8f_addnorm_rows(out, M, N, s_ss);
     } else if (row_ok && n < out.seg[out.nseg - 1].n_end) {  // channels past the last segment: padding
         int sgi = 0, nb = 0;
 #pragma unroll
@@ -426,14 +422,17 @@ hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, in
     const int S = sh.splits;
     if (M > 16 || N % kW8fGroup != 0 || K % (S * sh.waves * sh.depth * kKStep) != 0) return hipErrorInvalidValue;
     if (S > 1 && (!part || !cnt || (size_t)S * M * N * 4 > 0x7FFFFFFFull)) return hipErrorInvalidValue;
-    if (out.mode == kW8AddNorm &&
-        (N > 4096 || out.nseg != 1 || out.seg[0].ld != N || !out.seg[0].dst || !out.h || !out.norm_w ||
-         !out.x16 || !out.norm_cnt))
+    if (out.nin_h && (M > kW8NormInRows || K > kW8NormInMaxK || K % 4 || !out.nin_w ||
+                      (out.nin_add && !out.nin_hout)))
         return hipErrorInvalidValue;
     const dim3 grid(N / kW8fGroup, S);
 #define W8F_CASE(WV, DP)                                                                                  \
     if (sh.waves == WV && sh.depth == DP) {                                                                \
-        w8f_kernel<WV, DP><<<grid, 64 * WV, 0, st>>>(x, W, scale, M, N, K, K / S, S, part, cnt, out);     \
+        if (out.nin_h)                                                                                     \
+            w8f_kernel<WV, DP, true><<<grid, 64 * WV, (size_t)M * K * 2, st>>>(x, W, scale, M, N, K, K / S, S, \
+                                                                               part, cnt, out);             \
+        else                                                                                               \
+            w8f_kernel<WV, DP><<<grid, 64 * WV, 0, st>>>(x, W, scale, M, N, K, K / S, S, part, cnt, out); \
         return hipGetLastError();                                                                          \
     }
     W8F_CASE(4, 1)

@@ -360,11 +360,11 @@ def test_hybrid_long_context_span_sizes_vs_oracle(hb, fixture):
 
 
 def test_hybrid_fused_and_separate_norms_agree(hb, fixture):
-    """Up to batch 2 the residual add and RMSNorm run in the last block of
-    the out and down matrices; from batch 3 in a kernel of their own, with
-    the same arithmetic in the same order.  The same two sequences stepped
-    at batch 2 and (with a third) at batch 3 give bit-identical logits and
-    greedy tokens."""
+    """Up to batch 2 the residual add and RMSNorm run in every block of the
+    matrices that read the norm (in-projections, gate|up, lm_head); from
+    batch 3 in a kernel of their own, with the same arithmetic in the same
+    order.  The same two sequences stepped at batch 2 and (with a third) at
+    batch 3 give bit-identical logits and greedy tokens."""
     d, fields = fixture
     gm, _ = models(hb, fields, int(d["seed"]), max_batch=3)
     tokens = d["tokens"]
