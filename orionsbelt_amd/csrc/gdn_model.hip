@@ -385,6 +385,57 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
     }
 }
 
+// The narrow branch matrices at small M (out_proj, down: N = 2560): one
+// 16-channel tile per block and no k-split.  Wave w takes NS consecutive
+// 64-k steps, all its weight fragments requested up front; the waves' tiles
+// are summed in LDS in wave order and wave 0 stores.  Against the k-split
+// form (whose last block sums the splits), at N = 2560: K = 4096 5.3
+// against 7.3 us (M = 1) and 7.2 against 8.0 us (M = 16); K = 9216 7.6
+// against 8.9 us (M <= 3), but 12.8 against 9.8 us at M = 16 (its 18 steps
+// per wave spill), where the k-split form stays.
+template <int WAVES, int NS>
+__global__ __launch_bounds__(64 * WAVES) void w8n_kernel(const uint16_t *__restrict__ x, const int8_t *__restrict__ W,
+                                                         const float *__restrict__ scale, int M, int N, int K,
+                                                         W8Out out) {
+    __shared__ f32x4_t red[WAVES][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int t = blockIdx.x;         // 16-channel tile
+    const int c = t >> 2, j = t & 3;  // its 64-channel group and place in the group
+    const int steps = K / kKStep;
+    const int s0 = wave * NS;         // this wave's first 64-k step
+    const int8_t *wp = W + ((size_t)c * steps + s0) * 4096 + j * 1024 + lane * 16;
+    const bool row_ok = r < M;
+    // rows past M read row 0 (in bounds) and are zeroed
+    const uint16_t *xp = x + (size_t)(row_ok ? r : 0) * K + s0 * kKStep + 16 * g;
+    u32x4_t wv[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+        wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(wp + (size_t)i * 4096));
+    f32x4_t acc = zero4();
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        u32x4_t xa = *reinterpret_cast<const u32x4_t *>(xp + i * kKStep);
+        u32x4_t xb = *reinterpret_cast<const u32x4_t *>(xp + i * kKStep + 8);
+        if (!row_ok) xa = xb = u32x4_t{0u, 0u, 0u, 0u};
+        f16x8_t w0, w1;
+        i8x16_to_f16(wv[i], w0, w1);
+        acc = mfma_f16(w0, __builtin_bit_cast(f16x8_t, xa), acc);
+        acc = mfma_f16(w1, __builtin_bit_cast(f16x8_t, xb), acc);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4_t y = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) y += red[w][lane];
+    const int n = 16 * t + 4 * g;  // C lane (g, r): channels n .. n+3 of batch row r
+    if (row_ok && n < out.seg[0].n_end) {
+        y = y * *reinterpret_cast<const f32x4_t *>(scale + n);
+        *reinterpret_cast<f32x4_t *>(out.seg[0].dst + (size_t)r * out.seg[0].ld + n) = y;
+    }
+}
+
 }  // namespace
 
 // Launch shape from a sweep over the Qwen3.5-4B matrices at M = 1 and 16
@@ -418,6 +469,14 @@ hipError_t launch_w8f_tile(const int8_t *src, int8_t *dst, int N, int K, hipStre
 hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, int M, int N, int K,
                       const W8Out &out, float *part, uint32_t *cnt, hipStream_t st, W8fShape sh) {
     if (M == 0 || N == 0) return hipSuccess;
+    // the narrow single-output matrices: one tile per block, no k-split
+    // (w8n_kernel), when no launch shape is asked for
+    if (sh.splits == 0 && out.mode == kW8Segments && out.nseg == 1 && !out.nin_h && N % kW8fGroup == 0 &&
+        ((K == 8 * 8 * kKStep && M <= 16) || (K == 8 * 18 * kKStep && M <= 3))) {
+        if (K == 8 * 8 * kKStep) w8n_kernel<8, 8><<<N / 16, 512, 0, st>>>(x, W, scale, M, N, K, out);
+        else w8n_kernel<8, 18><<<N / 16, 512, 0, st>>>(x, W, scale, M, N, K, out);
+        return hipGetLastError();
+    }
     if (sh.splits == 0) sh = w8f_shape(N, K);
     const int S = sh.splits;
     if (M > 16 || N % kW8fGroup != 0 || K % (S * sh.waves * sh.depth * kKStep) != 0) return hipErrorInvalidValue;
