@@ -35,6 +35,7 @@ import ctypes
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -364,7 +365,7 @@ def bench_prefill(L, ob, torch, timer, reps=5):
     return {"workload": "chunked WY prefill, B=1 T=16384 Hv=32 Hk=16 d=128 bf16 in, fp32 state",
             "tokens_per_s": round(PF_T / (ms * 1e-3), 1), "ms": round(ms, 4),
             "achieved_tflops": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-            "ms_20_warmups": round(ms_ref, 4),
+            "flop_per_launch": flop, "ms_20_warmups": round(ms_ref, 4),
             "timing_note": f"ms: p50 of 30 calls after {PF_WARMUP_S:g} s of warm-up calls (steady clocks); "
                            "ms_20_warmups: the reference's 20 warm-ups alone, right after the input "
                            "set-up left the GPU idle (clocks still rising)"}
@@ -851,6 +852,69 @@ def run_profile(which, L, ob, torch, timer, steps, warmup):
     log("calibration copy: 3 x 268435456 bytes")
 
 
+def compact_cpu(c):
+    """A cpu_baseline entry without its long strings (they stay on the
+    detail line)."""
+    if not c:
+        return c
+    out = {k: c[k] for k in ("value", "unit", "cores", "kind") if k in c}
+    if "sample" in c:  # its first clause, without parentheses
+        out["sample"] = re.sub(r"\s*\([^)]*\)", "", c["sample"]).split(",")[0]
+    if "single_thread" in c:
+        out["single_thread"] = c["single_thread"]["value"]
+    if "port_all_cores" in c:
+        out["port_all_cores"] = c["port_all_cores"]["value"]
+    return out
+
+
+def compact_secondary(sec):
+    """The secondary lines, figures only, in a fixed order with the T=16K
+    prefill (the second half of the metric) last."""
+    out = {}
+
+    def stream_line(d):
+        e = {"us": d.get("us"), "frac": d.get("hbm_frac")}
+        c = d.get("cpu_baseline")
+        if c:  # GB/s of the reference's scalar build (1 core) and of the port (all cores)
+            if c.get("kind") == "reference":
+                e["cpu_ref_gbs"] = c["value"]
+                e["cpu_port_gbs"] = c["port_all_cores"]["value"]
+            else:
+                e["cpu_port_gbs"] = c["value"]
+        return e
+
+    for key in ("conv", "cumdecay"):
+        if key in sec:
+            out[key] = stream_line(sec[key])
+    for key, d in sec.get("scans", {}).items():
+        out[key] = stream_line(d)
+    if "decode_f16_state" in sec:
+        d = sec["decode_f16_state"]
+        out["decode_f16_state"] = {"ms_per_step": d["ms_per_step"], "tok_s": d["tokens_per_s"],
+                                   "launch_us": d["launch_us"], "frac": d["hbm_frac"]}
+    for key in ("gating_prologue", "gated_rmsnorm"):
+        if key in sec:
+            out[key] = stream_line(sec[key])
+    if "prefill_f16_state" in sec:
+        out["prefill_f16_state"] = [{"T": r["T"], "ms": r["ms"], "tok_s": r["tokens_per_s"],
+                                     "state_bytes": r["state_bytes_per_layer"]}
+                                    for r in sec["prefill_f16_state"]["lengths"]]
+    if "hybrid_decode" in sec:
+        out["hybrid_decode"] = [{k: r[k] for k in ("batch", "ms_per_step", "tokens_per_s", "hbm_frac", "ttft_ms")
+                                 if k in r} for r in sec["hybrid_decode"]["runs"]]
+    if "prefill" in sec:
+        d = sec["prefill"]
+        e = {"T": PF_T, "ms": d["ms"], "ms_20_warmups": d["ms_20_warmups"], "tok_s": d["tokens_per_s"],
+             "mfma_frac": d["mfma_frac"],
+             "roofline": {"bound": "mfma", "kernel": "prefill_pass1_kernel+prefill_pass2_kernel",
+                          "flop_per_launch": d["flop_per_launch"], "achieved": d["achieved_tflops"],
+                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": d["mfma_frac"]}}
+        if "cpu_baseline" in d:
+            e["cpu_baseline"] = compact_cpu(d["cpu_baseline"])
+        out["prefill"] = e
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -935,6 +999,20 @@ def main():
                 line_["cpu_baseline"] = entry
             log(f"cpu stream: {stream_cpu}")
 
+    rl = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profile_traffic("delta_decode_kernel"),
+          "kernel": "delta_decode_kernel<128,128,f32>", "bytes_per_launch": DEC_BYTES,
+          "launch_us": round(kern_ms * 1e3, 2), "launch_us_event_pairs": round(kern_pairs * 1e3, 2),
+          "frac_measured": round(achieved / peaks["hbm_copy_gbs"], 4)}
+    # launch_us: the timed region (decode launches only, back to back) / launch
+    # count; launch_us_event_pairs: events recorded between every two launches,
+    # which adds each event's own cost.
+    for key, val in secondary.items():
+        add_measured_fracs(val, peaks, read_bound=(key == "hybrid_decode"))
+    # The whole result tree (workload strings, samples, notes) on stderr; the
+    # JSON line on stdout keeps the figures only, with the T=16K prefill last.
+    log("detail: " + json.dumps({"roofline": rl, "cpu_baseline": cpu, "measured_peaks": peaks,
+                                 "secondary": secondary}))
     line = {
         "metric": "GDN decode tok/s (B=64, 24 layers, 1 GPU) + % of HBM roofline",
         "value": round(B_DEC / (ms_step * 1e-3), 1),
@@ -949,26 +1027,15 @@ def main():
         "dtype": "f32",
         "data": "synthetic (BASELINE distributions, random state)",
         "config": {"workload": "gated delta-rule decode step: 24 GDN layers, batch 64, "
-                               "Hv=32 Hk=16 d_k=d_v=128, fp32 state (BASELINE configs[1])",
-                   "batch": B_DEC, "layers": LAYERS, "num_v_heads": HV, "num_k_heads": HK,
-                   "head_dim": DK},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": profile_traffic("delta_decode_kernel"),
-                     "kernel": "delta_decode_kernel<128,128,f32>",
-                     "bytes_per_launch": DEC_BYTES, "launch_us": round(kern_ms * 1e3, 2),
-                     "launch_us_event_pairs": round(kern_pairs * 1e3, 2),
-                     "launch_note": "launch_us: the timed region (decode launches only, back to back) / "
-                                    "launch count; launch_us_event_pairs: events recorded between every "
-                                    "two launches, which adds each event's own cost"},
-        "cpu_baseline": cpu,
-        "measured_peaks": peaks,
-        "secondary": secondary,
+                               "Hv=32 Hk=16 d_k=d_v=128, fp32 state (BASELINE configs[1])"},
+        "roofline": rl,
+        "cpu_baseline": compact_cpu(cpu),
+        "peaks": {"copy_gbs": peaks["hbm_copy_gbs"], "read_gbs": peaks["hbm_read_gbs"],
+                  "mfma_tflops": peaks["mfma_bf16_tflops"],
+                  "mfma16_tflops": peaks["mfma_bf16_16x16x32_tflops"]},
+        "secondary": compact_secondary(secondary),
     }
-    line["roofline"]["frac_measured"] = round(achieved / peaks["hbm_copy_gbs"], 4)
-    for key, val in secondary.items():
-        add_measured_fracs(val, peaks, read_bound=(key == "hybrid_decode"))
-    print(json.dumps(line), flush=True)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

@@ -74,6 +74,13 @@ int kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip(const float *in, const float *w,
 int kai_run_gdn_gemv_f32_f32_f32_hip(const float *a, const float *b, float *c,
                                      size_t k, size_t n, void *stream);
 
+/* Replaces gdn_delta_rule_matmul
+ * (src/orionsbelt/engines/cpu/kernels/gdn_delta_matmul.h:15-16) on the
+ * caller's stream: C[M][N] = A[M][K] . B[K][N], row-major fp32, each element
+ * the k-ordered sum of rounded products.  K == 0 writes zeros. */
+int kai_run_gdn_delta_rule_matmul_f32_hip(const float *A, const float *B, float *C, size_t M,
+                                          size_t K, size_t N, void *stream);
+
 /* ---- mixed-precision diagonal kernels (gdn_sve.h:56-72) ------------------
  * fp16 values are IEEE binary16 bit patterns, bf16 values the upper half of a
  * binary32 (round to nearest even), both passed as uint16_t.  fp32

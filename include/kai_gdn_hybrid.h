@@ -83,6 +83,31 @@ int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next,
  * (gdn_e2e_decode.c:2644-2700, with the M > 1 GEMM of :606-612). */
 int kai_gdn_hybrid_prefill(kai_gdn_hybrid *m, const int32_t *tokens, int batch, int length,
                            int32_t *next, float *logits, void *stream);
+/* Per-layer-type timing, the GPU counterpart of the e2e program's phase
+ * timers (gdn_e2e_decode.c:1365-1371, reported at :2708-2710,2820-2857).
+ * With timing on, kai_gdn_hybrid_step and kai_gdn_hybrid_prefill record a
+ * HIP event on their stream at every phase boundary (about 130 per step,
+ * which adds their own cost to the call); kai_gdn_hybrid_phase_times waits
+ * for the last one, adds each interval to its phase and writes the sums in
+ * microseconds since the previous read (or since timing was switched on)
+ * to us[0 .. n-1] in KAI_GDN_PHASE_* order, then starts new sums.  Phases:
+ * the GDN layers' input projection (in_proj_qkvz|b|a), their conv update,
+ * gating, delta rule and gated RMSNorm (one fused kernel in a decode step;
+ * conv, gating prologue, chunked delta rule and norm in a prefill), their
+ * out_proj with the residual add; the attention layers whole; the MLPs
+ * (with the norm that feeds them in a prefill); and the rest (embedding,
+ * first norm, LM head, argmax).  Returns 0, or hipErrorInvalidValue. */
+enum {
+    KAI_GDN_PHASE_GDN_PROJ = 0,
+    KAI_GDN_PHASE_GDN_CORE = 1,
+    KAI_GDN_PHASE_GDN_OPROJ = 2,
+    KAI_GDN_PHASE_ATTN = 3,
+    KAI_GDN_PHASE_FFN = 4,
+    KAI_GDN_PHASE_OTHER = 5,
+    KAI_GDN_PHASE_COUNT = 6
+};
+int kai_gdn_hybrid_set_timing(kai_gdn_hybrid *m, int on);
+int kai_gdn_hybrid_phase_times(kai_gdn_hybrid *m, double *us, int n);
 /* Current position (context + steps taken) and device bytes held. */
 int kai_gdn_hybrid_position(const kai_gdn_hybrid *m);
 size_t kai_gdn_hybrid_device_bytes(const kai_gdn_hybrid *m);

@@ -76,6 +76,7 @@ struct orc_hybrid {
     float *final_norm;
     mat lm;
     int batch, pos;
+    int gdn_bf16_io;  /* orc_hybrid_set_gdn_bf16_io */
 };
 
 static void make_mat(mat *w, int N, int K, uint64_t seed, uint64_t stream) {
@@ -231,7 +232,16 @@ static void gdn_mixer(orc_hybrid *m, layer *L, const uint16_t *x16, float *out) 
     gemm(x16, &L->ap, a, B);
     orc_causal_conv1d_update_f32(qkv, L->conv_state, L->conv_w, cv, B, 1, (size_t)C, 1);
     orc_gating_prologue_f32(cv, a, bb, L->A_log, L->dt_bias, q, k, v, g, beta, (size_t)B, Hk, Hv);
+    if (m->gdn_bf16_io) {  /* the recurrence's operands in the device prefill's format */
+        for (size_t i = 0; i < (size_t)B * Hk * 128; ++i) {
+            q[i] = orc_bf16_to_f32(orc_f32_to_bf16(q[i]));
+            k[i] = orc_bf16_to_f32(orc_f32_to_bf16(k[i]));
+        }
+        for (size_t i = 0; i < (size_t)B * V; ++i) v[i] = orc_bf16_to_f32(orc_f32_to_bf16(v[i]));
+    }
     orc_delta_rule_decode_f32(L->S, q, k, v, g, beta, o, B, Hv, Hk, 128, 128, 1.0f / sqrtf(128.0f));
+    if (m->gdn_bf16_io)
+        for (size_t i = 0; i < (size_t)B * V; ++i) o[i] = orc_bf16_to_f32(orc_f32_to_bf16(o[i]));
     orc_gated_rmsnorm_f32(o, z, L->norm_w, y, (size_t)B * Hv, 128, c->rms_eps);
     for (size_t i = 0; i < (size_t)B * V; ++i) y16[i] = orc_f32_to_f16(y[i]);
     gemm(y16, &L->out, out, B);
@@ -333,6 +343,8 @@ void orc_hybrid_step(orc_hybrid *m, const int32_t *tokens, int32_t *next, float 
 }
 
 int orc_hybrid_position(const orc_hybrid *m) { return m->pos; }
+
+void orc_hybrid_set_gdn_bf16_io(orc_hybrid *m, int on) { m->gdn_bf16_io = on != 0; }
 
 /* Export one drawn tensor as fp32 (matrices dequantised: q * scale, [N][K]).
  * layer < 0 selects the model-level tensors (G_*).  Returns the element

@@ -164,6 +164,18 @@ void orc_gemv_f32(const float *a, const float *b, float *c, size_t k, size_t n) 
     }
 }
 
+/* C = A.B, A [m][k], B [k][n], C [m][n] row-major: the portable branch of
+ * the reference's delta-rule matmul (gdn_delta_matmul.c:111-118, the same
+ * loop as its test's naive_matmul, test_gdn_delta_matmul.c:32-41). */
+void orc_delta_rule_matmul_f32(const float *A, const float *B, float *C, size_t m, size_t k, size_t n) {
+    for (size_t i = 0; i < m; ++i)
+        for (size_t j = 0; j < n; ++j) {
+            float acc = 0.0f;
+            for (size_t kk = 0; kk < k; ++kk) acc = acc + A[i * k + kk] * B[kk * n + j];
+            C[i * n + j] = acc;
+        }
+}
+
 /* ======================================================================== */
 /* Narrow formats                                                            */
 /* ======================================================================== */

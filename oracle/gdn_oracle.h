@@ -16,6 +16,11 @@
  *   orc_cumdecay_f32, orc_gated_scan_f32, orc_causal_dwconv1d_f32_k4,
  *   orc_gemv_f32            -- bit-identical to the reference kai sources
  *                              compiled in oracle/_ref, plus closed forms.
+ *   orc_delta_rule_matmul_f32 -- bit-identical to the reference's
+ *                              gdn_delta_matmul.c (portable branch) compiled
+ *                              in oracle/_ref and to its golden vectors;
+ *                              within the fp32 error bound of a float64
+ *                              product; K = 0 gives zeros.
  *   orc_*_f16 / orc_*_bf16  -- bit-identical to the reference gdn_sve.c
  *                              compiled in oracle/_ref (clang), plus numpy
  *                              float16 / RNE-bfloat16 conversion checks.
@@ -82,6 +87,10 @@ void orc_causal_dwconv1d_silu_f32_k4(const float *in, const float *w, float *out
 /* c[j] = sum_k a[k]*b[k][j], k-loop inner, acc from 0.0f.
  * kleidiai_submission/kai/ukernels/gdn/kai_gdn_gemv_f32_f32_f32_1x4_neon.c:78-86 */
 void orc_gemv_f32(const float *a, const float *b, float *c, size_t k, size_t n);
+
+/* C[i][j] = sum_k A[i][k]*B[k][j], k-loop inner, acc from 0.0f.
+ * src/orionsbelt/engines/cpu/kernels/gdn_delta_matmul.c:111-118 */
+void orc_delta_rule_matmul_f32(const float *A, const float *B, float *C, size_t m, size_t k, size_t n);
 
 /* ---- mixed precision (gdn_sve.c scalar branches) ------------------------ */
 /* fp16 values are passed as IEEE binary16 bit patterns (uint16_t), bf16 as the
@@ -231,6 +240,12 @@ orc_hybrid *orc_hybrid_create(const orc_hybrid_config *cfg, uint64_t seed);
 void orc_hybrid_reset(orc_hybrid *m, int batch, int context, uint64_t seed);
 void orc_hybrid_step(orc_hybrid *m, const int32_t *tokens, int32_t *next, float *logits);
 int orc_hybrid_position(const orc_hybrid *m);
+/* With on != 0, each GDN layer rounds the recurrence's q, k, v (after the
+ * gating prologue) and its output o (before the gated RMSNorm) to bf16 by
+ * round-to-nearest-even: the formats the device prefill hands between its
+ * kernels (bf16 gating prologue, bf16 chunked delta rule), so that a device
+ * prefill compares with this model up to the kernels' own arithmetic. */
+void orc_hybrid_set_gdn_bf16_io(orc_hybrid *m, int on);
 long orc_hybrid_tensor(const orc_hybrid *m, int layer, int id, float *dst);
 void orc_hybrid_destroy(orc_hybrid *m);
 

@@ -14,7 +14,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liborb_oracle.so")
+# ORB_ORACLE_LIB selects another build of the same sources (the sanitizer
+# build of `make asan`).
+LIB_PATH = os.environ.get("ORB_ORACLE_LIB") or os.path.join(HERE, "liborb_oracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -126,6 +128,23 @@ def gemv_f32(a, b, k, n, L=None):
     fn = getattr(L, "orc_gemv_f32", None) or L.kai_run_gdn_gemv_f32_f32_f32_1x4_neon
     fn(P(a), P(b), P(c), _sz(k), _sz(n))
     return c[:n]
+
+
+def delta_rule_matmul(A, B, m, k, n, L=None):
+    """C = A.B (orc_delta_rule_matmul_f32, or the reference's own
+    gdn_delta_rule_matmul when L is ref_matmul())."""
+    L = L or lib()
+    c = np.empty(max(m * n, 1), np.float32)
+    fn = getattr(L, "orc_delta_rule_matmul_f32", None) or L.gdn_delta_rule_matmul
+    fn(P(A), P(B), P(c), _sz(m), _sz(k), _sz(n))
+    return c[:m * n].reshape(m, n)
+
+
+def ref_matmul() -> ctypes.CDLL | None:
+    """The reference's gdn_delta_matmul.c (portable branch, no KleidiAI)
+    compiled from its source into oracle/_ref, or None when not built."""
+    p = os.path.join(REF_DIR, "libdelta_matmul_ref.so")
+    return ctypes.CDLL(p) if os.path.exists(p) else None
 
 
 def cumdecay_narrow(a, seq, ch, fmt, L=None, prefix="orc_"):
@@ -347,6 +366,7 @@ class HybridModel:
         L.orc_hybrid_tensor.restype = ctypes.c_long
         L.orc_hybrid_tensor.argtypes = [ctypes.c_void_p, _int, _int, _f32p]
         L.orc_hybrid_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_hybrid_set_gdn_bf16_io.argtypes = [ctypes.c_void_p, _int]
         self.cfg = cfg
         self._h = L.orc_hybrid_create(ctypes.byref(cfg), ctypes.c_uint64(seed))
         self.batch = cfg.max_batch
@@ -354,6 +374,11 @@ class HybridModel:
     def reset(self, batch: int, context: int, seed: int) -> None:
         lib().orc_hybrid_reset(self._h, batch, context, ctypes.c_uint64(seed))
         self.batch = batch
+
+    def set_gdn_bf16_io(self, on: bool) -> None:
+        """Round the delta rule's q, k, v and output to bf16 (the device
+        prefill's formats) from now on."""
+        lib().orc_hybrid_set_gdn_bf16_io(self._h, int(bool(on)))
 
     def step(self, tokens):
         """-> (next tokens [batch] int32, logits [batch][vocab] fp32)."""

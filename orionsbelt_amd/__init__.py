@@ -29,6 +29,7 @@ HIP_SYMBOLS = (
     "kai_run_gdn_causal_dwconv1d_f32_k4_hip",
     "kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip",
     "kai_run_gdn_gemv_f32_f32_f32_hip",
+    "kai_run_gdn_delta_rule_matmul_f32_hip",
     "kai_run_gdn_cumdecay_f16_hip",
     "kai_run_gdn_cumdecay_bf16_hip",
     "kai_run_gdn_gated_scan_f16_hip",
@@ -60,6 +61,8 @@ HIP_SYMBOLS = (
     "kai_gdn_hybrid_reset",
     "kai_gdn_hybrid_step",
     "kai_gdn_hybrid_prefill",
+    "kai_gdn_hybrid_set_timing",
+    "kai_gdn_hybrid_phase_times",
     "kai_gdn_hybrid_position",
     "kai_gdn_hybrid_device_bytes",
     "kai_gdn_hybrid_weight_bytes",
@@ -84,7 +87,9 @@ SVE_SYMBOLS = (
     "gdn_gated_scan_bf16",
     "gdn2_gated_scan_f32",
 )
-ALL_SYMBOLS = KAI_SYMBOLS + HIP_SYMBOLS + SVE_SYMBOLS
+# The reference's delta-rule matmul (include/gdn_delta_matmul.h).
+MATMUL_SYMBOLS = ("gdn_delta_rule_matmul",)
+ALL_SYMBOLS = KAI_SYMBOLS + HIP_SYMBOLS + SVE_SYMBOLS + MATMUL_SYMBOLS
 
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
@@ -120,6 +125,8 @@ _SIGS = {
     "kai_run_gdn_causal_dwconv1d_f32_k4_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "kai_run_gdn_gemv_f32_f32_f32_hip": (_i, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "kai_run_gdn_delta_rule_matmul_f32_hip": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "gdn_delta_rule_matmul": (None, [_vp, _vp, _vp, _sz, _sz, _sz]),
     "kai_run_gdn_delta_rule_decode_f32_hip":
         (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "kai_run_gdn_delta_rule_decode_f16state_hip":
@@ -154,6 +161,8 @@ _SIGS = {
     "kai_gdn_hybrid_reset": (_i, [_vp, _i, _i, ctypes.c_ulonglong]),
     "kai_gdn_hybrid_step": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "kai_gdn_hybrid_prefill": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "kai_gdn_hybrid_set_timing": (_i, [_vp, _i]),
+    "kai_gdn_hybrid_phase_times": (_i, [_vp, ctypes.POINTER(ctypes.c_double), _i]),
     "kai_gdn_hybrid_position": (_i, [_vp]),
     "kai_gdn_hybrid_device_bytes": (_sz, [_vp]),
     "kai_gdn_hybrid_weight_bytes": (_sz, [_vp]),

@@ -167,7 +167,8 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     float eps, uint16_t *vT, int Tv) {
     __shared__ float red[4];
     __shared__ float rot[64];
-    const int slot = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+    // rows on grid x (a prefill's T can exceed grid y's 65535), heads on y
+    const int slot = blockIdx.y, row = blockIdx.x, d = threadIdx.x;
     const int b = seq < 0 ? row : seq;
     const int p = seq < 0 ? pos : row;
     if (slot >= Hq + Hkv) {  // value head: copy into the cache
@@ -386,6 +387,15 @@ struct kai_gdn_hybrid {
     int batch = 0, pos = 0;
     int parity = 0;  // which conv cache of each GDN layer is current
     int tmax = 0;    // KV cache positions: max_context rounded up to 16 (K is tiled by 16)
+    // phase timing (kai_gdn_hybrid_set_timing): events recorded so far in
+    // this round of sums, the phase each interval (event i-1 .. i) closes
+    struct Timing {
+        bool on = false;
+        std::vector<hipEvent_t> pool;
+        std::vector<int> phase;
+        size_t used = 0;
+        double sum_us[KAI_GDN_PHASE_COUNT] = {};
+    } timing;
 };
 
 namespace gdn {
@@ -415,6 +425,36 @@ hipError_t fill(float *dst, size_t n, uint64_t seed, uint64_t stream, float amp,
     } while (0)
 
 int pad64(int n) { return (n + 63) / 64 * 64; }
+
+// Timing mode: an event on `st` that closes an interval of phase `ph` (the
+// first event of a call opens one, ph < 0).  No-op when timing is off.
+hipError_t mark(kai_gdn_hybrid *m, int ph, hipStream_t st) {
+    auto &t = m->timing;
+    if (!t.on) return hipSuccess;
+    if (t.used == t.pool.size()) {
+        hipEvent_t e;
+        TRY(hipEventCreate(&e));
+        t.pool.push_back(e);
+        t.phase.push_back(-1);
+    }
+    t.phase[t.used] = ph;
+    return hipEventRecord(t.pool[t.used++], st);
+}
+
+// Adds the recorded intervals to the sums and empties the event list.
+hipError_t collect(kai_gdn_hybrid *m) {
+    auto &t = m->timing;
+    if (t.used == 0) return hipSuccess;
+    TRY(hipEventSynchronize(t.pool[t.used - 1]));
+    for (size_t i = 1; i < t.used; ++i) {
+        if (t.phase[i] < 0) continue;
+        float ms = 0.f;
+        TRY(hipEventElapsedTime(&ms, t.pool[i - 1], t.pool[i]));
+        t.sum_us[t.phase[i]] += (double)ms * 1e3;
+    }
+    t.used = 0;
+    return hipSuccess;
+}
 
 struct Part {
     int rows;
@@ -642,11 +682,14 @@ hipError_t gdn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     const int B = m->batch, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads, C = m->conv_dim, V = m->value_dim;
     TRY(gemm_in(m, L.in, segments({{m->qkv, C, C}, {m->zb, V, C + V}, {m->bb, Hv, C + V + Hv},
                                         {m->ab, Hv, C + V + 2 * Hv}}), st));
+    TRY(mark(m, KAI_GDN_PHASE_GDN_PROJ, st));
     // conv update, gating prologue, delta rule, gated RMSNorm -> fp16: one kernel
     TRY(launch_gdn_step_fused(m->qkv, L.conv_state[m->parity], L.conv_state[m->parity ^ 1], L.conv_w, m->ab,
                               m->bb, L.A_log, L.dt_bias, L.S, m->zb, L.norm_w, m->o16, B, Hk, Hv,
                               1.0f / sqrtf(128.0f), c.rms_eps, st));
-    return gemm_addnorm(m, m->o16, L.out, m->mix, L.ln_post, st);
+    TRY(mark(m, KAI_GDN_PHASE_GDN_CORE, st));
+    TRY(gemm_addnorm(m, m->o16, L.out, m->mix, L.ln_post, st));
+    return mark(m, KAI_GDN_PHASE_GDN_OPROJ, st);
 }
 
 hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
@@ -655,19 +698,21 @@ hipError_t attn_mixer(kai_gdn_hybrid *m, Layer &L, hipStream_t st) {
     const int nq = Hq * 512, nkv = Hkv * 256;
     TRY(gemm_in(m, L.in, segments({{m->qg, nq, nq}, {m->kx, nkv, nq + nkv}, {m->vx, nkv, nq + 2 * nkv}}),
              st));
-    attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, B), 256, 0, st>>>(m->qg, m->kx, m->vx, L.q_norm, L.k_norm, m->q16,
+    attn_prologue_kernel<<<dim3(B, Hq + 2 * Hkv), 256, 0, st>>>(m->qg, m->kx, m->vx, L.q_norm, L.k_norm, m->q16,
                                                                  L.Kc, L.Vc, Hq, Hkv, m->tmax, -1, m->pos,
                                                                  c.rope_theta, c.rms_eps, nullptr, 0);
     TRY(hipGetLastError());
     // o * sigmoid(gate) -> fp16 in the span combine; gate = dims 256..511 of each qg head
     TRY(launch_attn_decode(m->q16, L.Kc, L.Vc, nullptr, B, Hq, Hkv, m->tmax, m->pos + 1, 1.0f / 16.0f,
                            m->attn_ws, st, m->qg + 256, 512, m->o16, /*k_tiled=*/true));
-    return gemm_addnorm(m, m->o16, L.out, m->mix, L.ln_post, st);
+    TRY(gemm_addnorm(m, m->o16, L.out, m->mix, L.ln_post, st));
+    return mark(m, KAI_GDN_PHASE_ATTN, st);
 }
 
 hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *logits, hipStream_t st) {
     const kai_gdn_hybrid_config &c = m->cfg;
     const int B = m->batch, H = c.hidden;
+    TRY(mark(m, -1, st));
     embed_kernel<<<B, 256, 0, st>>>(tokens, m->embed, m->h, H, c.vocab);
     TRY(hipGetLastError());
     W8Out swiglu{};
@@ -684,18 +729,21 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
         addnorm_kernel<<<B, 256, 0, st>>>(m->h, nullptr, m->layers[0].ln_in, m->x16, H, c.rms_eps);
         TRY(hipGetLastError());
     }
+    TRY(mark(m, KAI_GDN_PHASE_OTHER, st));
     for (size_t l = 0; l < m->layers.size(); ++l) {
         Layer &L = m->layers[l];
         TRY(L.attn ? attn_mixer(m, L, st) : gdn_mixer(m, L, st));
         TRY(gemm_in(m, L.gate_up, swiglu, st));
         const float *next_norm = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : m->final_norm;
         TRY(gemm_addnorm(m, m->act16, L.down, m->mlp, next_norm, st));
+        TRY(mark(m, KAI_GDN_PHASE_FFN, st));
     }
     float *lg = logits ? logits : m->logits;
     TRY(gemm_in(m, m->lm, segments({{lg, c.vocab, c.vocab}}), st));
     argmax_kernel<<<dim3(kArgBlocks, B), 256, 0, st>>>(lg, next ? next : m->next, c.vocab, m->arg_part,
                                                        m->arg_cnt);
     TRY(hipGetLastError());
+    TRY(mark(m, KAI_GDN_PHASE_OTHER, st));
     ++m->pos;
     m->parity ^= 1;
     return hipSuccess;
@@ -750,10 +798,12 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
     const int H = c.hidden, C = m->conv_dim, V = m->value_dim, Hk = c.gdn_k_heads, Hv = c.gdn_v_heads,
               Hq = c.attn_q_heads, Hkv = c.attn_kv_heads, I = c.inter;
     kai_gdn_hybrid::Prefill &p = m->pf;
+    TRY(mark(m, -1, st));
     embed_kernel<<<T, 256, 0, st>>>(tokens, m->embed, p.h, H, c.vocab);
     TRY(hipGetLastError());
     addnorm_kernel<<<T, 256, 0, st>>>(p.h, nullptr, m->layers[0].ln_in, p.x16, H, c.rms_eps);
     TRY(hipGetLastError());
+    TRY(mark(m, KAI_GDN_PHASE_OTHER, st));
     W8Out swiglu{};
     swiglu.mode = kW8SwiGLU;
     swiglu.x16 = p.act16;
@@ -762,6 +812,7 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
         if (!L.attn) {
             TRY(w8p(p.x16, H, L.in, T, segments({{p.qkv, C, C}, {p.z, V, C + V}, {p.b, Hv, C + V + Hv},
                                                   {p.a, Hv, C + V + 2 * Hv}}), st));
+            TRY(mark(m, KAI_GDN_PHASE_GDN_PROJ, st));
             // the decode step's conv cache: the last four conv inputs
             TRY(launch_conv_state_from_inputs(p.qkv, L.conv_state[0] + (size_t)b * C * 4, 1, T, C, st));
             TRY(hipMemsetAsync(p.hist, 0, (size_t)3 * C * sizeof(float), st));
@@ -777,12 +828,14 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
             prefill_gated_norm_kernel<<<(unsigned)((rows + 7) / 8), 256, 0, st>>>(p.o, p.z, L.norm_w, p.x16, rows,
                                                                                   c.rms_eps);
             TRY(hipGetLastError());
+            TRY(mark(m, KAI_GDN_PHASE_GDN_CORE, st));
             TRY(w8p(p.x16, V, L.out, T, segments({{p.mix, H, H}}), st));
+            TRY(mark(m, KAI_GDN_PHASE_GDN_OPROJ, st));
         } else {
             const int nq = Hq * 512, nkv = Hkv * 256;
             TRY(w8p(p.x16, H, L.in, T, segments({{p.qkv, nq, nq}, {p.kx, nkv, nq + nkv}, {p.vx, nkv, nq + 2 * nkv}}),
                     st));
-            attn_prologue_kernel<<<dim3(Hq + 2 * Hkv, T), 256, 0, st>>>(p.qkv, p.kx, p.vx, L.q_norm, L.k_norm, p.q16,
+            attn_prologue_kernel<<<dim3(T, Hq + 2 * Hkv), 256, 0, st>>>(p.qkv, p.kx, p.vx, L.q_norm, L.k_norm, p.q16,
                                                                         L.Kc, L.Vc, Hq, Hkv, m->tmax, b, 0,
                                                                         c.rope_theta, c.rms_eps, p.vT, p.tv);
             TRY(hipGetLastError());
@@ -790,6 +843,7 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
             TRY(launch_attn_prefill(p.q16, L.Kc + kvrow, p.vT, p.qkv + 256, nq, p.x16, T, Hq, Hkv, m->tmax, p.tv,
                                     1.0f / 16.0f, st));
             TRY(w8p(p.x16, Hq * 256, L.out, T, segments({{p.mix, H, H}}), st));
+            TRY(mark(m, KAI_GDN_PHASE_ATTN, st));
         }
         addnorm_kernel<<<T, 256, 0, st>>>(p.h, p.mix, L.ln_post, p.x16, H, c.rms_eps);
         TRY(hipGetLastError());
@@ -798,6 +852,7 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
         const float *next_norm = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : m->final_norm;
         addnorm_kernel<<<T, 256, 0, st>>>(p.h, p.mix, next_norm, p.x16, H, c.rms_eps);
         TRY(hipGetLastError());
+        TRY(mark(m, KAI_GDN_PHASE_FFN, st));
     }
     return hipMemcpyAsync(m->x16 + (size_t)b * H, p.x16 + (size_t)(T - 1) * H, (size_t)H * sizeof(uint16_t),
                           hipMemcpyDeviceToDevice, st);
@@ -814,10 +869,12 @@ hipError_t prefill(kai_gdn_hybrid *m, const int32_t *tokens, int batch, int T, i
     m->parity = 0;
     for (int b = 0; b < batch; ++b) TRY(prefill_seq(m, tokens + (size_t)b * T, b, T, st));
     float *lg = logits ? logits : m->logits;
+    TRY(mark(m, -1, st));
     TRY(gemm(m, m->x16, m->lm, segments({{lg, c.vocab, c.vocab}}), st));
     argmax_kernel<<<dim3(kArgBlocks, batch), 256, 0, st>>>(lg, next ? next : m->next, c.vocab, m->arg_part,
                                                            m->arg_cnt);
     TRY(hipGetLastError());
+    TRY(mark(m, KAI_GDN_PHASE_OTHER, st));
     m->pos = T;
     return hipSuccess;
 }
@@ -879,6 +936,7 @@ extern "C" kai_gdn_hybrid_config kai_gdn_hybrid_qwen35_4b(int max_batch, int max
 extern "C" void kai_gdn_hybrid_destroy(kai_gdn_hybrid *m) {
     if (!m) return;
     for (void *p : m->allocs) (void)hipFree(p);
+    for (hipEvent_t e : m->timing.pool) (void)hipEventDestroy(e);
     delete m;
 }
 
@@ -942,10 +1000,31 @@ extern "C" int kai_gdn_hybrid_step(kai_gdn_hybrid *m, const int32_t *tokens, int
 
 extern "C" int kai_gdn_hybrid_prefill(kai_gdn_hybrid *m, const int32_t *tokens, int batch, int length,
                                       int32_t *next, float *logits, void *stream) {
+    // every launch of the prefill accepts `length` rows (checked here, so a
+    // refused call leaves the model's states untouched)
     if (!m || !tokens || batch < 1 || batch > m->cfg.max_batch || length < 1 || length >= m->cfg.max_context ||
-        !device_ptr(tokens) || (next && !device_ptr(next)) || (logits && !device_ptr(logits)))
+        length > gdn::w8p_max_rows() || !device_ptr(tokens) || (next && !device_ptr(next)) ||
+        (logits && !device_ptr(logits)))
         return (int)hipErrorInvalidValue;
     return (int)gdn::prefill(m, tokens, batch, length, next, logits, (hipStream_t)stream);
+}
+
+extern "C" int kai_gdn_hybrid_set_timing(kai_gdn_hybrid *m, int on) {
+    if (!m) return (int)hipErrorInvalidValue;
+    auto &t = m->timing;
+    t.on = on != 0;
+    t.used = 0;
+    for (double &v : t.sum_us) v = 0.0;
+    return 0;
+}
+
+extern "C" int kai_gdn_hybrid_phase_times(kai_gdn_hybrid *m, double *us, int n) {
+    if (!m || !us || n < 0 || n > KAI_GDN_PHASE_COUNT) return (int)hipErrorInvalidValue;
+    const hipError_t e = gdn::collect(m);
+    if (e != hipSuccess) return (int)e;
+    for (int i = 0; i < n; ++i) us[i] = m->timing.sum_us[i];
+    for (double &v : m->timing.sum_us) v = 0.0;
+    return 0;
 }
 
 extern "C" int kai_gdn_hybrid_position(const kai_gdn_hybrid *m) { return m ? m->pos : -1; }

@@ -16,6 +16,7 @@ enum Narrow : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
 hipError_t launch_conv_k4(const float *in, const float *w, float *out, float *hist,
                           size_t seq, size_t ch, bool silu, hipStream_t st);
 
+hipError_t launch_matmul(const float *A, const float *B, float *Cm, size_t m, size_t k, size_t n, hipStream_t st);
 hipError_t launch_gemv(const float *a, const float *b, float *c, size_t k, size_t n,
                        hipStream_t st);
 
@@ -178,6 +179,8 @@ hipError_t launch_w8_quantize(const float *W, int8_t *Wq, float *scale, int N, i
 // The model's int8 GEMM for many rows: x [M][ldx] fp16 (16-byte aligned
 // rows), weights tiled by launch_w8f_tile (N % 64 == 0, K % 64 == 0); `out`
 // as for launch_w8f in kW8Segments or kW8SwiGLU mode.
+// The largest M launch_w8p accepts (its grid's y limit).
+long long w8p_max_rows();
 hipError_t launch_w8p(const uint16_t *x, int ldx, const int8_t *W, const float *scale, int M, int N, int K,
                       const W8Out &out, hipStream_t st);
 // Causal attention of one sequence's T positions: q16 [T][Hq][256] fp16,

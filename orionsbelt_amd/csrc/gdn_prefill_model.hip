@@ -499,6 +499,8 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
 
 }  // namespace
 
+long long w8p_max_rows() { return 65535LL * kPBM2; }
+
 hipError_t launch_w8p(const uint16_t *x, int ldx, const int8_t *W, const float *scale, int M, int N, int K,
                       const W8Out &out, hipStream_t st) {
     if (M <= 0) return hipSuccess;

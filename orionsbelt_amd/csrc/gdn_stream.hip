@@ -454,6 +454,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float *__restrict__ a,
     c[j] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Delta-rule matmul: C[i][j] = sum_k A[i][k] * B[k][j]
+// ---------------------------------------------------------------------------
+// One thread per output element, row i = blockIdx.y (+ multiples of gridDim.y),
+// k-loop in order with contraction off: the naive fp32 loop of the reference's
+// test (test_gdn_delta_matmul.c:32-41) bit for bit.  Rows of B are read
+// coalesced across the wavefront; A[i][k] is the same for every lane.
+__global__ __launch_bounds__(256) void matmul_kernel(const float *__restrict__ A, const float *__restrict__ B,
+                                                     float *__restrict__ Cm, int64_t m, int64_t k, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    for (int64_t i = blockIdx.y; i < m; i += gridDim.y) {
+        const float *a = A + i * k;
+        float acc = 0.0f;
+        int64_t kk = 0;
+        for (; kk + 8 <= k; kk += 8) {
+            float bv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) bv[u] = B[(kk + u) * n + j];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = acc + a[kk + u] * bv[u];
+        }
+        for (; kk < k; ++kk) acc = acc + a[kk] * B[kk * n + j];
+        Cm[i * n + j] = acc;
+    }
+}
+
 }  // namespace
 
 // Production configuration of the streaming kernels, measured on MI355X at
@@ -545,6 +573,14 @@ hipError_t launch_gemv(const float *a, const float *b, float *c, size_t k, size_
     if (n == 0) return hipSuccess;
     dim3 grid((unsigned)((n + 255) / 256)), block(256);
     gemv_kernel<<<grid, block, 0, st>>>(a, b, c, (int64_t)k, (int64_t)n);
+    return hipGetLastError();
+}
+
+hipError_t launch_matmul(const float *A, const float *B, float *Cm, size_t m, size_t k, size_t n, hipStream_t st) {
+    if (m == 0 || n == 0) return hipSuccess;
+    if (n > (size_t)0x7FFFFFFF * 256) return hipErrorInvalidValue;
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)std::min<size_t>(m, 65535)), block(256);
+    matmul_kernel<<<grid, block, 0, st>>>(A, B, Cm, (int64_t)m, (int64_t)k, (int64_t)n);
     return hipGetLastError();
 }
 

@@ -35,6 +35,7 @@
 #include "../../include/kai/ukernels/gdn/kai_gdn_cumdecay_f32_sve.h"
 #include "../../include/kai/ukernels/gdn/kai_gdn_gated_scan_f32_sve.h"
 #include "../../include/kai/ukernels/gdn/kai_gdn_gemv_f32_f32_f32_1x4_neon.h"
+#include "../../include/gdn_delta_matmul.h"
 
 namespace {
 
@@ -533,6 +534,13 @@ extern "C" int kai_run_gdn_causal_dwconv1d_silu_f32_k4_hip(const float *in, cons
     return (int)gdn::launch_conv_k4(in, w, out, hist, seq, channels, true, (hipStream_t)stream);
 }
 
+extern "C" int kai_run_gdn_delta_rule_matmul_f32_hip(const float *A, const float *B, float *C, size_t M,
+                                                     size_t K, size_t N, void *stream) {
+    if (M == 0 || N == 0) return 0;
+    if (!C || (K > 0 && (!A || !B))) return (int)hipErrorInvalidValue;
+    return (int)gdn::launch_matmul(A, B, C, M, K, N, (hipStream_t)stream);
+}
+
 extern "C" int kai_run_gdn_gemv_f32_f32_f32_hip(const float *a, const float *b, float *c,
                                                 size_t k, size_t n, void *stream) {
     return (int)gdn::launch_gemv(a, b, c, k, n, (hipStream_t)stream);
@@ -926,6 +934,21 @@ extern "C" void kai_run_gdn_gemv_f32_f32_f32_1x4_neon(const float *a, const floa
     check(gdn::launch_gemv((const float *)args[0].dev, (const float *)args[1].dev,
                            (float *)args[2].dev, k, n, c->stream),
           "gemv launch");
+    finish(c, args, 3);
+}
+
+// gdn_delta_rule_matmul (gdn_delta_matmul.h:15-16): the same staging as the
+// kai symbols.
+extern "C" void gdn_delta_rule_matmul(const float *A, const float *B, float *C_, size_t M, size_t K, size_t N) {
+    if (M == 0 || N == 0) return;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    DeviceCtx *c = sync_ctx();
+    Arg args[3] = {stage_arg(c, 0, A, (K ? M * K : 1) * sizeof(float), K > 0, false),
+                   stage_arg(c, 1, B, (K ? K * N : 1) * sizeof(float), K > 0, false),
+                   stage_arg(c, 2, C_, M * N * sizeof(float), false, true)};
+    check(gdn::launch_matmul((const float *)args[0].dev, (const float *)args[1].dev, (float *)args[2].dev, M, K, N,
+                             c->stream),
+          "delta_rule_matmul launch");
     finish(c, args, 3);
 }
 

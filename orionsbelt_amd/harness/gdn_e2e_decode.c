@@ -10,14 +10,19 @@
  *   --ctx-sweep L1,L2..  decode cost at growing context lengths
  *   --help
  * with the reference's CSV headers, so its parser (bench/convert_e2e_decode.py)
- * reads these rows.  The reference's per-phase CPU timers have no counterpart
- * in one GPU step: those columns print nan.  Added:
+ * reads these rows.  The reference's per-phase timers (:1365-1371) are filled
+ * from a separate timing pass after the measured one (the library's timing
+ * mode, kai_gdn_hybrid_set_timing: HIP events between the kernel groups,
+ * whose own cost would perturb the measured pass): GDN input projection,
+ * GDN out projection, full attention and FFN as in the reference.  The
+ * reference's conv1d, cumdecay and gated-scan phases are one fused kernel in
+ * a GPU decode step; its time is reported as gdn_scan and the conv and decay
+ * columns as 0.  Added:
  *   --prefill M          process M prompt tokens in one pass
  *                        (kai_gdn_hybrid_prefill) and report TTFT and prefill
  *                        throughput (:2644-2730: 2 warm-up passes, then one
- *                        measured; its CSV header; the per-layer-type split
- *                        prints nan, the GPU runs the pass as one stream of
- *                        kernels)
+ *                        measured; its CSV header with the GDN / full
+ *                        attention / FFN split of a timing pass)
  *   --batch B            sequences decoded together (default 1, at most 16)
  *   --ctx L              a drawn context of L positions before the timed
  *                        tokens (KV caches, recurrent and conv states)
@@ -82,6 +87,20 @@ static void first_tokens(runner *r, uint32_t seed) {
     r->which = 0;
 }
 
+/* `n` untimed steps with the library's timing mode on, from a fresh drawn
+ * context; ph[] gets each phase's sum over them (microseconds). */
+static void phase_pass(runner *r, int ctx, int n, double *ph) {
+    KAI_OK(kai_gdn_hybrid_reset(r->m, r->batch, ctx, 7));
+    first_tokens(r, 42u);
+    KAI_OK(kai_gdn_hybrid_set_timing(r->m, 1));
+    for (int t = 0; t < n; ++t) {
+        KAI_OK(kai_gdn_hybrid_step(r->m, r->tok[r->which], r->tok[r->which ^ 1], NULL, r->st));
+        r->which ^= 1;
+    }
+    KAI_OK(kai_gdn_hybrid_phase_times(r->m, ph, KAI_GDN_PHASE_COUNT));
+    KAI_OK(kai_gdn_hybrid_set_timing(r->m, 0));
+}
+
 /* One step, timed on its own; returns microseconds. */
 static double timed_step(runner *r) {
     HIP_OK(hipEventRecord(r->e0, r->st));
@@ -135,13 +154,23 @@ static int run_prefill(int M, int batch, int csv) {
     float ms = 0.f;
     HIP_OK(hipEventElapsedTime(&ms, e0, e1));
     const double total_us = ms * 1e3, ttft_ms = ms, tps = (double)n * 1e6 / total_us;
+    /* the per-layer-type split, from a timing pass */
+    double ph[KAI_GDN_PHASE_COUNT];
+    KAI_OK(kai_gdn_hybrid_set_timing(m, 1));
+    KAI_OK(kai_gdn_hybrid_prefill(m, tok, batch, M, next, NULL, st));
+    KAI_OK(kai_gdn_hybrid_phase_times(m, ph, KAI_GDN_PHASE_COUNT));
+    KAI_OK(kai_gdn_hybrid_set_timing(m, 0));
+    const double gdn_us = ph[KAI_GDN_PHASE_GDN_PROJ] + ph[KAI_GDN_PHASE_GDN_CORE] + ph[KAI_GDN_PHASE_GDN_OPROJ];
     if (csv) {
         printf("model,prefill_M,ttft_ms,tok_per_sec_prefill,gdn_us,full_us,ffn_us\n");
-        printf(MODEL_NAME ",%d,%.2f,%.2f,nan,nan,nan\n", M, ttft_ms, tps);
+        printf(MODEL_NAME ",%d,%.2f,%.2f,%.0f,%.0f,%.0f\n", M, ttft_ms, tps, gdn_us, ph[KAI_GDN_PHASE_ATTN],
+               ph[KAI_GDN_PHASE_FFN]);
     } else {
         printf("Results (prefill M=%d, %d sequences):\n", M, batch);
         printf("  TTFT (prefill total):  %.2f ms  (%.0f us)\n", ttft_ms, total_us);
         printf("  Prefill throughput:    %.2f tok/s  (%.4f ms/tok)\n", tps, ttft_ms / (double)n);
+        printf("  Layer types (timing pass): GDN %.0f us, full attention %.0f us, FFN %.0f us, other %.0f us\n",
+               gdn_us, ph[KAI_GDN_PHASE_ATTN], ph[KAI_GDN_PHASE_FFN], ph[KAI_GDN_PHASE_OTHER]);
     }
     free(host);
     HIP_OK(hipFree(tok));
@@ -181,7 +210,13 @@ int main(int argc, char **argv) {
                    strncmp(argv[i], "--verify-", 9) == 0) {
             fprintf(stderr, "Warning: '%s' selects a CPU code path of the reference; ignored\n", argv[i]);
         } else if (strcmp(argv[i], "--prefill") == 0 && i + 1 < argc) {
-            prefill_m = atoi(argv[++i]);
+            char *end = NULL;
+            const long v = strtol(argv[++i], &end, 10);
+            if (end == argv[i] || *end != '\0' || v < 1 || v > 16777215) {
+                fprintf(stderr, "Error: --prefill must be an integer in 1..16777215 (got '%s')\n", argv[i]);
+                return 1;
+            }
+            prefill_m = (int)v;
         } else {
             fprintf(stderr, "Warning: unrecognized argument '%s' (ignored)\n", argv[i]);
         }
@@ -192,10 +227,6 @@ int main(int argc, char **argv) {
     }
     if (batch < 1 || batch > 16 || ctx < 0) {
         fprintf(stderr, "Error: --batch must be in 1..16 and --ctx >= 0\n");
-        return 1;
-    }
-    if (prefill_m < 0) {
-        fprintf(stderr, "Error: --prefill must be >= 1 (got %d)\n", prefill_m);
         return 1;
     }
     if (prefill_m > 0) return run_prefill(prefill_m, batch, csv);
@@ -239,10 +270,16 @@ int main(int argc, char **argv) {
             const double tps = batch * 1e6 / total;
             const double kv_mb = (double)(cfg.layers / cfg.attn_every) * batch * cfg.attn_kv_heads * lens[i] *
                                  256 * 2 * 2 / (1024.0 * 1024.0);
+            double ph[KAI_GDN_PHASE_COUNT];
+            phase_pass(&r, lens[i], reps, ph);
+            const double gdn = (ph[KAI_GDN_PHASE_GDN_PROJ] + ph[KAI_GDN_PHASE_GDN_CORE] +
+                                ph[KAI_GDN_PHASE_GDN_OPROJ]) / reps;
+            const double full = ph[KAI_GDN_PHASE_ATTN] / reps, ffn = ph[KAI_GDN_PHASE_FFN] / reps;
             if (csv)
-                printf(MODEL_NAME ",%d,nan,nan,nan,%.0f,%.2f,%.1f\n", lens[i], total, tps, kv_mb);
+                printf(MODEL_NAME ",%d,%.0f,%.0f,%.0f,%.0f,%.2f,%.1f\n", lens[i], gdn, full, ffn, total, tps, kv_mb);
             else
-                printf("  ctx=%5d  total=%7.0f us  %.2f tok/s  KV=%7.1f MB\n", lens[i], total, tps, kv_mb);
+                printf("  ctx=%5d  GDN=%7.0f us  full_attn=%7.0f us  FFN=%7.0f us  total=%7.0f us  %.2f tok/s"
+                       "  KV=%7.1f MB\n", lens[i], gdn, full, ffn, total, tps, kv_mb);
         }
     } else {
         if (!csv) {
@@ -267,11 +304,22 @@ int main(int argc, char **argv) {
         const double p50 = tok_times[num_tokens / 2], p95 = tok_times[(int)(num_tokens * 0.95)],
                      p99 = tok_times[(int)(num_tokens * 0.99)];
         const double tok_per_sec = batch * 1e6 / mean_us;
+        /* the reference's bottleneck breakdown (:2820-2857), from a timing
+         * pass: conv1d, cumdecay and the scan are one fused kernel here
+         * (reported as the scan; conv and decay 0) */
+        double ph[KAI_GDN_PHASE_COUNT];
+        phase_pass(&r, ctx, num_tokens, ph);
+        const double t_proj = ph[KAI_GDN_PHASE_GDN_PROJ], t_scan = ph[KAI_GDN_PHASE_GDN_CORE],
+                     t_oproj = ph[KAI_GDN_PHASE_GDN_OPROJ], t_full = ph[KAI_GDN_PHASE_ATTN],
+                     t_ffn = ph[KAI_GDN_PHASE_FFN];
+        const double phase_sum = t_proj + t_scan + t_oproj + t_full + t_ffn;
         if (csv) {
             printf("model,tokens,ttft_ms,tok_per_sec_mean,p50_us,p95_us,p99_us,mean_us,"
                    "gdn_proj_pct,gdn_conv_pct,gdn_decay_pct,gdn_scan_pct,gdn_oproj_pct,full_pct,ffn_pct\n");
-            printf(MODEL_NAME ",%d,%.2f,%.2f,%.0f,%.0f,%.0f,%.0f,nan,nan,nan,nan,nan,nan,nan\n", num_tokens,
-                   ttft_ms, tok_per_sec, p50, p95, p99, mean_us);
+            printf(MODEL_NAME ",%d,%.2f,%.2f,%.0f,%.0f,%.0f,%.0f,%.1f,%.1f,%.1f,%.1f,%.1f,%.1f,%.1f\n", num_tokens,
+                   ttft_ms, tok_per_sec, p50, p95, p99, mean_us, 100.0 * t_proj / phase_sum, 0.0, 0.0,
+                   100.0 * t_scan / phase_sum, 100.0 * t_oproj / phase_sum, 100.0 * t_full / phase_sum,
+                   100.0 * t_ffn / phase_sum);
         } else {
             printf("Results (%d tokens x %d sequences):\n", num_tokens, batch);
             printf("  TTFT (first token):  %.2f ms\n", ttft_ms);
@@ -282,6 +330,14 @@ int main(int argc, char **argv) {
             printf("    p99:  %.0f us  (%.2f ms)\n", p99, p99 / 1e3);
             printf("    mean: %.0f us  (%.2f ms)\n", mean_us, mean_us / 1e3);
             printf("  Total decode time:   %.2f s\n", total_us / 1e6);
+            printf("  Bottleneck breakdown (timing pass, share of the summed phases):\n");
+            printf("    GDN q/k/v proj:  %5.1f%%  (%.0f us/tok)\n", 100.0 * t_proj / phase_sum, t_proj / num_tokens);
+            printf("    GDN conv1d + cumdecay + gated_scan (one fused kernel): %5.1f%%  (%.0f us/tok)\n",
+                   100.0 * t_scan / phase_sum, t_scan / num_tokens);
+            printf("    GDN out proj:    %5.1f%%  (%.0f us/tok)\n", 100.0 * t_oproj / phase_sum,
+                   t_oproj / num_tokens);
+            printf("    Full-attention:  %5.1f%%  (%.0f us/tok)\n", 100.0 * t_full / phase_sum, t_full / num_tokens);
+            printf("    FFN:             %5.1f%%  (%.0f us/tok)\n", 100.0 * t_ffn / phase_sum, t_ffn / num_tokens);
         }
         free(tok_times);
     }

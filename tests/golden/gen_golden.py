@@ -4,8 +4,14 @@ installed HuggingFace transformers for the delta-rule vectors):
 
     python tests/golden/gen_golden.py
 
-Five fixture files, each a numpy .npz (no pickles):
+Seven fixture files, each a numpy .npz (no pickles):
 
+delta_matmul.npz  the reference's gdn_delta_rule_matmul
+                (src/orionsbelt/engines/cpu/kernels/gdn_delta_matmul.c,
+                portable branch) from oracle/_ref/libdelta_matmul_ref.so on
+                the inputs of its test (test_gdn_delta_matmul.c:50-52: rand_r
+                seed 42, values in [-1, 1) in steps of 1e-3), at M=3 and 64,
+                K=128, N=130 and 17.
 kai_ref.npz     inputs and outputs of the reference kai ukernels
                 (kleidiai_submission/kai/ukernels/gdn/*.c, scalar branch),
                 compiled from the reference sources by oracle/Makefile into
@@ -98,6 +104,38 @@ def gen_kai():
         d.update({f"{name}_a": a, f"{name}_b": b, f"{name}_c": orc.gemv_f32(a, b, k, n, L=L),
                   f"{name}_shape": np.array([k, n], np.int64)})
     np.savez_compressed(os.path.join(HERE, "kai_ref.npz"), **d)
+
+
+def _rand_r(seed):
+    """glibc rand_r (the generator of test_gdn_delta_matmul.c:50-52)."""
+    state = [seed & 0xFFFFFFFF]
+
+    def step():
+        nxt = state[0]
+        nxt = (nxt * 1103515245 + 12345) & 0xFFFFFFFF
+        result = (nxt // 65536) % 2048
+        nxt = (nxt * 1103515245 + 12345) & 0xFFFFFFFF
+        result = (result << 10) ^ ((nxt // 65536) % 1024)
+        nxt = (nxt * 1103515245 + 12345) & 0xFFFFFFFF
+        result = (result << 10) ^ ((nxt // 65536) % 1024)
+        state[0] = nxt
+        return result
+
+    return step
+
+
+def gen_matmul():
+    L = orc.ref_matmul()
+    assert L is not None, "oracle/_ref/libdelta_matmul_ref.so missing: run make -C oracle ref"
+    d = {}
+    for name, m, k, n in [("mm1", 3, 128, 130), ("mm2", 64, 128, 17)]:
+        r = _rand_r(42)
+        A = np.array([((r() % 2000) - 1000) / 1000.0 for _ in range(m * k)], np.float32)
+        B = np.array([((r() % 2000) - 1000) / 1000.0 for _ in range(k * n)], np.float32)
+        d[f"{name}_A"], d[f"{name}_B"] = A, B
+        d[f"{name}_C"] = orc.delta_rule_matmul(A, B, m, k, n, L=L).ravel()
+        d[f"{name}_shape"] = np.array([m, k, n], np.int64)
+    np.savez_compressed(os.path.join(HERE, "delta_matmul.npz"), **d)
 
 
 def gen_sve():
@@ -342,12 +380,16 @@ if __name__ == "__main__":
     if len(sys.argv) > 1 and sys.argv[1] == "hybrid":
         gen_hybrid()
         sys.exit(0)
+    if len(sys.argv) > 1 and sys.argv[1] == "matmul":
+        gen_matmul()
+        sys.exit(0)
     gen_kai()
+    gen_matmul()
     gen_sve()
     gen_hf()
     gen_layer()
     gen_state()
     gen_hybrid()
-    for f in ("kai_ref.npz", "sve_mixed.npz", "hf_gdr.npz", "hf_layer.npz", "hf_state.npz",
+    for f in ("kai_ref.npz", "delta_matmul.npz", "sve_mixed.npz", "hf_gdr.npz", "hf_layer.npz", "hf_state.npz",
               "hf_hybrid.npz"):
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

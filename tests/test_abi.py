@@ -96,6 +96,41 @@ def test_e2e_driver_cli():
         assert flag in r.stdout
     r = subprocess.run([exe, "--tokens", "0"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "--tokens must be >= 1" in r.stderr
+    for bad in ("0", "-3", "abc", "12x"):
+        r = subprocess.run([exe, "--prefill", bad], capture_output=True, text=True, timeout=60)
+        assert r.returncode == 1 and "--prefill must be an integer" in r.stderr, bad
+
+
+def test_bench_line_is_compact_with_prefill_last():
+    """bench.py's JSON line keeps the figures only and ends with the T=16K
+    prefill entry (its own roofline and cpu_baseline), so a reader of the
+    output's tail sees the prefill half of the metric."""
+    import json
+    import sys
+    sys.path.insert(0, REPO)
+    import bench
+    sec = {
+        "conv": {"us": 47.0, "hbm_frac": 0.71, "cpu_baseline": {"value": 0.4, "kind": "reference",
+                                                                  "port_all_cores": {"value": 10.0}}},
+        "cumdecay": {"us": 46.0, "hbm_frac": 0.72},
+        "scans": {"gated_scan_f32": {"us": 71.0, "hbm_frac": 0.7}},
+        "decode_f16_state": {"ms_per_step": 0.6, "tokens_per_s": 1.0e5, "launch_us": 24.0, "hbm_frac": 0.7},
+        "prefill_f16_state": {"lengths": [{"T": 1024, "ms": 0.05, "tokens_per_s": 2e7,
+                                           "state_bytes_per_layer": 1 << 20}]},
+        "hybrid_decode": {"runs": [{"batch": 1, "ms_per_step": 1.7, "tokens_per_s": 576.0, "hbm_frac": 0.37,
+                                    "ttft_ms": 372.0, "device_bytes": 1}]},
+        "prefill": {"ms": 0.2309, "ms_20_warmups": 0.277, "tokens_per_s": 7.1e7, "mfma_frac": 0.1637,
+                    "achieved_tflops": 409.3, "flop_per_launch": 94489280512,
+                    "cpu_baseline": {"value": 15302.8, "unit": "tokens/s", "cores": 16, "kind": "port",
+                                     "sample": "598 x T=256 (32 heads, OpenMP over heads), 10.0 s"}},
+    }
+    c = bench.compact_secondary(sec)
+    assert list(c)[-1] == "prefill"
+    p = c["prefill"]
+    assert p["roofline"]["bound"] == "mfma" and p["roofline"]["frac"] == 0.1637
+    assert p["cpu_baseline"]["kind"] == "port" and p["cpu_baseline"]["sample"] == "598 x T=256"
+    text = json.dumps({"secondary": c}, separators=(",", ":"))
+    assert text.index('"prefill":{') > text.index('"hybrid_decode"') and len(text) < 1500
 
 
 def test_bench_refuses_multi_gpu():

@@ -13,7 +13,9 @@ Programs:
   (oracle/Makefile), when that build exists;
 - orionsbelt_amd/bin/bench_kai_gdn: the bench harness, CSV mode;
 - oracle/_ref/test_gdn_{mixed,2_scan,sve}_on_hip: the reference's tests of
-  its gdn_sve.h kernels, compiled unchanged against this library."""
+  its gdn_sve.h kernels, compiled unchanged against this library;
+- oracle/_ref/test_gdn_delta_matmul_on_hip: the reference's test of its
+  delta-rule matmul, compiled unchanged against this library."""
 import os
 import subprocess
 
@@ -75,6 +77,22 @@ def test_reference_gdn_sve_tests_on_hip_library(prog):
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
     assert "ALL TESTS PASSED" in r.stdout
     print(r.stdout.strip().splitlines()[-1])
+
+
+def test_reference_delta_matmul_test_on_hip_library():
+    """test_gdn_delta_matmul.c (naive fp32 loop against gdn_delta_rule_matmul
+    at M in {1, 64}, K = 128, N in {128, 2048, 130}, rel < 1e-4 each,
+    test_gdn_delta_matmul.c:70,87-96) with host pointers, through the
+    library's staging path."""
+    exe = os.path.join(REPO, "oracle", "_ref", "test_gdn_delta_matmul_on_hip")
+    if not os.access(exe, os.X_OK):
+        pytest.skip("oracle/_ref/test_gdn_delta_matmul_on_hip not built (needs the reference tree at build time)")
+    r = run(exe)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
+    lines = [ln for ln in r.stdout.splitlines() if "max_rel" in ln]
+    assert len(lines) == 6 and all(ln.rstrip().endswith("PASS") for ln in lines), r.stdout
+    assert "ALL PASS" in r.stdout
+    print("\n".join(lines))
 
 
 def test_reference_gdn_sve_report_on_hip_library():

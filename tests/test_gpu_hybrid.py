@@ -289,7 +289,11 @@ def test_hybrid_config5_batch16_ctx32k(hb):
 def test_e2e_driver_runs(hb):
     """The C driver (orionsbelt_amd/bin/gdn_e2e_decode, the reference e2e
     program's interface) decodes at the 4B shape and prints the reference's
-    CSV rows: the decode report, a context sweep and the prefill report."""
+    CSV rows: the decode report, a context sweep and the prefill report,
+    with the per-layer-type columns (gdn_e2e_decode.c:2708-2710,2820-2857)
+    filled by the library's timing mode: positive numbers, except the conv
+    and decay shares of a decode step, which run inside the fused scan kernel
+    (0); the decode shares add up to 100%."""
     import os
     import subprocess
     exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "orionsbelt_amd", "bin",
@@ -301,12 +305,19 @@ def test_e2e_driver_runs(hb):
     assert head.startswith("model,tokens,ttft_ms,tok_per_sec_mean,p50_us")
     f = row.split(",")
     assert f[0] == "Qwen3.5-4B" and f[1] == "4" and float(f[3]) > 0 and float(f[7]) > 0
+    pct = [float(x) for x in f[8:15]]
+    print("decode shares (proj, conv, decay, scan, oproj, full, ffn):", pct)
+    assert pct[1] == 0.0 and pct[2] == 0.0
+    assert all(pct[i] > 0 for i in (0, 3, 4, 5, 6)) and abs(sum(pct) - 100.0) < 0.5
     r = subprocess.run([exe, "--csv", "--ctx-sweep", "1,300"], capture_output=True, text=True, timeout=240)
     assert r.returncode == 0, r.stderr
     lines = r.stdout.strip().splitlines()
     assert lines[0].startswith("model,ctx_len,gdn_layer_us,full_attn_us,ffn_us,total_us")
     assert [ln.split(",")[1] for ln in lines[1:]] == ["1", "300"]
-    assert all(float(ln.split(",")[5]) > 0 for ln in lines[1:])
+    for ln in lines[1:]:
+        v = [float(x) for x in ln.split(",")[2:6]]
+        print("sweep (gdn, full, ffn, total us):", v)
+        assert all(x > 0 for x in v) and v[0] + v[1] + v[2] < 1.5 * v[3]
     # --prefill M: the reference's prefill report (gdn_e2e_decode.c:2708-2710)
     r = subprocess.run([exe, "--csv", "--prefill", "1000", "--batch", "2"], capture_output=True, text=True,
                        timeout=240)
@@ -315,6 +326,9 @@ def test_e2e_driver_runs(hb):
     assert head == "model,prefill_M,ttft_ms,tok_per_sec_prefill,gdn_us,full_us,ffn_us"
     f = row.split(",")
     assert f[0] == "Qwen3.5-4B" and f[1] == "1000" and float(f[2]) > 0 and float(f[3]) > 0
+    gdn, full, ffn = (float(x) for x in f[4:7])
+    print("prefill split (gdn, full, ffn us):", gdn, full, ffn, "ttft ms", f[2])
+    assert gdn > 0 and full > 0 and ffn > 0 and (gdn + full + ffn) < 1.5 * float(f[2]) * 1e3
 
 
 def test_hybrid_real_head_counts_vs_oracle(hb, fixture):

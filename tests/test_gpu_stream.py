@@ -282,6 +282,40 @@ def test_gemv_bit_exact(L):
 
 
 # ---------------------------------------------------------------------------
+# Delta-rule matmul (gdn_delta_matmul.h:15-16)
+# ---------------------------------------------------------------------------
+
+def test_delta_rule_matmul_bit_exact(L, golden):
+    """kai_run_gdn_delta_rule_matmul_f32_hip against the oracle at the
+    reference test's shapes (test_gdn_delta_matmul.c:87-96: M in {1, 64},
+    K = 128, N in {128, 2048, 130}) and ragged ones, and against the
+    reference's golden vectors; bit-identical (the naive k-ordered loop).
+    K = 0 writes zeros; M = 0 writes nothing."""
+    import orionsbelt_amd as ob
+    torch = torch_mod()
+    rs = np.random.RandomState(11)
+    for m, k, n in [(1, 128, 128), (64, 128, 128), (1, 128, 2048), (64, 128, 2048), (1, 128, 130),
+                    (64, 128, 130), (3, 5, 1), (70000, 3, 2), (2, 0, 5)]:
+        A = rs.uniform(-1, 1, max(m * k, 1)).astype(np.float32)
+        B = rs.uniform(-1, 1, max(k * n, 1)).astype(np.float32)
+        dA, dB = dev(A), dev(B)
+        dC = torch.full((m * n,), float("nan"), dtype=torch.float32, device="cuda")
+        ob.check(L.kai_run_gdn_delta_rule_matmul_f32_hip(P(dA), P(dB), P(dC), m, k, n, stream()))
+        want = orc.delta_rule_matmul(A, B, m, k, n).ravel()
+        assert np.array_equal(bits(host(dC)), bits(want)), (m, k, n)
+    dC = torch.full((4,), 7.0, device="cuda")
+    ob.check(L.kai_run_gdn_delta_rule_matmul_f32_hip(P(dC), P(dC), P(dC), 0, 4, 4, stream()))
+    assert np.all(host(dC) == 7.0)
+    d = golden("delta_matmul.npz")
+    for name in ("mm1", "mm2"):
+        m, k, n = (int(x) for x in d[f"{name}_shape"])
+        A, B = d[f"{name}_A"], d[f"{name}_B"]  # held: each NpzFile access makes a new array
+        C = np.empty(m * n, np.float32)
+        L.gdn_delta_rule_matmul(np_ptr(A), np_ptr(B), np_ptr(C), m, k, n)
+        assert np.array_equal(bits(C), bits(d[f"{name}_C"])), name
+
+
+# ---------------------------------------------------------------------------
 # Drop-in kai symbols with HOST pointers (the reference harness's usage)
 # ---------------------------------------------------------------------------
 

@@ -8,11 +8,14 @@ HuggingFace delta-rule vectors), and (c) closed forms and brute force chosen
 so that a dropped term, a wrong index or a transposed operand fails.
 """
 import math
+import os
 
 import numpy as np
 import pytest
 
 from oracle import oracle as orc
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -60,6 +63,57 @@ def test_kai_golden_gemv(golden):
     for n in ("gv1", "gv2"):
         k, nn = d[f"{n}_shape"]
         assert bits_equal(orc.gemv_f32(d[f"{n}_a"], d[f"{n}_b"], k, nn), d[f"{n}_c"])
+
+
+def test_delta_matmul_golden(golden):
+    """orc_delta_rule_matmul_f32 against the reference gdn_delta_matmul.c's
+    outputs on its test's inputs (tests/golden/delta_matmul.npz)."""
+    d = golden("delta_matmul.npz")
+    for n in ("mm1", "mm2"):
+        m, k, nn = (int(x) for x in d[f"{n}_shape"])
+        got = orc.delta_rule_matmul(d[f"{n}_A"], d[f"{n}_B"], m, k, nn)
+        assert bits_equal(got.ravel(), d[f"{n}_C"])
+
+
+def test_delta_matmul_bounds_and_live_reference():
+    """Against a float64 product: each element within the fp32 sum's error
+    bound (k * 2^-24 * sum |a b|, with slack 2); K = 0 gives zeros; a
+    transposed operand or a dropped k term fails the bound.  Bit-identical to
+    the live reference build when oracle/_ref holds it, at the reference
+    test's shapes (test_gdn_delta_matmul.c:87-96)."""
+    rs = np.random.RandomState(3)
+    ref = orc.ref_matmul()
+    for m, k, n in [(1, 128, 128), (64, 128, 128), (1, 128, 2048), (64, 128, 2048), (1, 128, 130),
+                    (64, 128, 130), (5, 7, 3)]:
+        A = rs.uniform(-1, 1, m * k).astype(np.float32)
+        B = rs.uniform(-1, 1, k * n).astype(np.float32)
+        C = orc.delta_rule_matmul(A, B, m, k, n)
+        A2, B2 = A.reshape(m, k).astype(np.float64), B.reshape(k, n).astype(np.float64)
+        exact = A2 @ B2
+        bound = 2 * k * 2.0 ** -24 * (np.abs(A2) @ np.abs(B2))
+        assert np.all(np.abs(C - exact) <= bound + 1e-30)
+        if k > 1:  # a dropped last term is far outside the bound somewhere
+            drop = A2[:, :-1] @ B2[:-1, :]
+            assert np.any(np.abs(drop - exact) > bound)
+        if k == n:  # so is a transposed operand
+            assert np.any(np.abs(A2 @ B2.T - exact) > bound)
+        if ref is not None:
+            assert bits_equal(C.ravel(), orc.delta_rule_matmul(A, B, m, k, n, L=ref).ravel())
+    z = orc.delta_rule_matmul(np.zeros(1, np.float32), np.zeros(1, np.float32), 2, 0, 3)
+    assert np.all(z == 0)
+
+
+def test_oracle_under_sanitizers():
+    """make -C oracle asan: the oracle rebuilt with AddressSanitizer and
+    UBSan runs this file's tests (and the reference kai test, when the
+    reference tree is present) without a report.  Skipped inside that run."""
+    if os.environ.get("ORB_ORACLE_LIB"):
+        pytest.skip("already running under the sanitizer build")
+    import subprocess
+    r = subprocess.run(["make", "-s", "-C", os.path.join(REPO, "oracle"), "asan"], capture_output=True,
+                       text=True, timeout=600)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    assert "passed" in r.stdout and "ERROR: AddressSanitizer" not in r.stderr + r.stdout
 
 
 # --------------------------------------------------------------------------
