@@ -146,10 +146,15 @@ class Timer:
 
 
 
-def bench_decode(L, ob, torch, steps, warmup, timer, f16_state=False):
+def bench_decode(L, ob, torch, steps, warmup, timer, f16_state=False, warmup_s=0.0):
     """The configs[1] step: 24 launches of the decode kernel, one per layer,
     each with its own state (fp32, or fp16 with f16_state: the narrow-state
-    variant of row a6, half the state bytes)."""
+    variant of row a6, half the state bytes).  `warmup` untimed steps, then,
+    with warmup_s, untimed steps until that much time has passed: the
+    inputs' host-side set-up leaves the GPU idle for seconds, and a 0.6 ms
+    step needs more than five steps to return to its steady clock (the first
+    20 timed fp16-state steps after 10 warm-ups read 25.2 us per launch
+    against a steady 24.2)."""
     from tests.gdn_inputs import decode_inputs
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     qs = 1.0 / math.sqrt(DK)
@@ -178,6 +183,10 @@ def bench_decode(L, ob, torch, steps, warmup, timer, f16_state=False):
 
     for _ in range(warmup):
         step()
+    t0 = time.perf_counter()
+    while warmup_s > 0 and time.perf_counter() - t0 < warmup_s:
+        step()
+        torch.cuda.synchronize()
     ms_step = timer.time_ms(step, steps)
     # The timed region holds only decode launches, back to back on the
     # stream the events are recorded on: its time / launch count is the mean
@@ -964,7 +973,8 @@ def main():
         secondary["conv"], secondary["cumdecay"] = bench_stream(L, ob, torch, timer)
         log(f"conv: {secondary['conv']}\ncumdecay: {secondary['cumdecay']}")
         log("decode with fp16 state ...")
-        ms16, kern16, pairs16 = bench_decode(L, ob, torch, args.steps, args.warmup, timer, f16_state=True)
+        ms16, kern16, pairs16 = bench_decode(L, ob, torch, args.steps, args.warmup, timer, f16_state=True,
+                                             warmup_s=0.15)
         b16 = DEC_BYTES - B_DEC * HV * DK * DV * 4  # the state read + written at 2 bytes
         gbs16 = b16 / (kern16 * 1e-3) / 1e9
         secondary["decode_f16_state"] = {
