@@ -72,6 +72,7 @@ HIP_SYMBOLS = (
     "kai_gdn_hip_check_device_error",
     "kai_gdn_hip_prefill_workspace_bytes",
     "kai_gdn_hip_device_bytes_held",
+    "kai_gdn_hip_prefill_windowed_heads",
     "kai_gdn_hip_probe_sink_bytes",
     "kai_gdn_hip_probe_stream",
     "kai_gdn_hip_probe_mfma_bf16",
@@ -172,6 +173,7 @@ _SIGS = {
     "kai_gdn_hip_check_device_error": (_i, []),
     "kai_gdn_hip_prefill_workspace_bytes": (_sz, [_i, _i, _i]),
     "kai_gdn_hip_device_bytes_held": (_sz, []),
+    "kai_gdn_hip_prefill_windowed_heads": (_i, []),
     "kai_gdn_hip_probe_sink_bytes": (_sz, []),
     "kai_gdn_hip_probe_stream": (_i, [_vp, _vp, _sz, _i, _vp, _vp]),
     "kai_gdn_hip_probe_mfma_bf16": (_i, [_i, _i, _vp, ctypes.POINTER(ctypes.c_ulonglong), _vp]),

@@ -86,6 +86,8 @@ constexpr int kHeadDim = 128;
 // prefill_carry_bytes(B, T, Hv) bytes of device memory (segment transitions
 // and start states); calls that share it must not overlap.
 size_t prefill_carry_bytes(int B, int T, int Hv);
+// (sequence, head) pairs of the last call that ran windowed (synchronises).
+int prefill_windowed_heads();
 hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_t *k,
                               const uint16_t *v, const float *g, const float *beta, uint16_t *o,
                               void *S, int B, int T, int Hv, int Hk, float q_scale, void *carry,

@@ -712,6 +712,11 @@ struct SegArgs {
     int T, Hv, Hk, NC, P;
     int bnd[kMaxSegs + 1];  // segment p covers chunks [bnd[p], bnd[p+1])
     float q_scale;
+    // Windowed segments (0 when the call has none): segment p outputs chunks
+    // [wbnd[p], wbnd[p+1]) and starts its recurrence at the chunk its head's
+    // window word names.
+    int Pw;
+    int wbnd[kMaxSegs + 1];
 };
 
 // Ring slots of chunk n in a segment starting at n0.
@@ -992,9 +997,10 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
 
 // State waves of an output segment: columns c0 .. c0 + 31 (two tiles).
 // o^T tiles: lane (g, r) of tile (ct, tt) holds o[t = 16 tt + r][c0 + 16 ct
-// + 4g .. +3], one 8-byte store.
+// + 4g .. +3], one 8-byte store.  Chunks before n_out (a windowed segment's
+// warm-up) run the same products but store no output.
 GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h, int n0,
-                            int n1, int c0, int lane) {
+                            int n1, int n_out, int c0, int lane) {
     const int g = lane >> 4, r = lane & 15;
     const TileOffs to = tile_offs(g, r);
     const int voff[2] = {acc_off(c0 / 16, g, r), acc_off(c0 / 16 + 1, g, r)};
@@ -1092,7 +1098,7 @@ GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int 
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct) O[ct][tt] = mfma_16x16x32_bf16(vf[kb][ct], af, O[ct][tt]);
                 }
-            const int valid = min(C, a.T - n * C);
+            const int valid = n < n_out ? 0 : min(C, a.T - n * C);
             uint16_t *ob = a.o + (((size_t)b * a.T + (size_t)n * C) * a.Hv + h) * D + c0 + 4 * g;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
@@ -1223,24 +1229,161 @@ GDN_DEV void combine_prefix(CombSmem &sm, f32x4_t (&S)[8][1], const float *carry
 // heads of one key head (and their shared k and q rows) in one L2.
 GDN_DEV int head_of(int x, int Hv) { return (Hv % 8 == 0) ? (Hv / 8) * (x % 8) + x / 8 : x; }
 
-// Output segment over chunks [n0, n1) from S (state waves' registers).
-GDN_DEV void run_output(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h, int n0, int n1) {
+// Output segment over chunks [n0, n1) from S (state waves' registers),
+// outputs stored from chunk n_out on.
+GDN_DEV void run_output(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h, int n0, int n1,
+                        int n_out) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     zero_upper_halves(sm, tid);
-    if (wave < NSW) state_loop_out(sm, S, a, b, h, n0, n1, 32 * wave, lane);
+    if (wave < NSW) state_loop_out(sm, S, a, b, h, n0, n1, n_out, 32 * wave, lane);
     else {
         f32x4_t none[8][1];
         helper_loop<true>(sm, a, b, h, n0, n1, wave - NSW, lane, none);
     }
 }
 
+// ---------------------------------------------------------------------------
+// Windowed segments
+// ---------------------------------------------------------------------------
+//
+// One token maps the state as S -> A_t S + beta_t k_t v_t^T with
+// A_t = gamma_t (I - beta_t k_t k_t^T), gamma_t = e^{g_t}; I - b k k^T has the
+// eigenvalues 1 and 1 - b |k|^2, so ||A_t||_2 = gamma_t max(1, |1 - beta_t
+// |k_t|^2|).  Over a window of chunks the state that entered it is carried
+// by a map of norm at most the product of these.  When that product is at
+// most 2^-24 (one fp32 rounding of the state it multiplies), a segment can
+// start its recurrence from S = 0 at the window's first chunk instead of
+// from the true state: what it drops is below that state's own fp32
+// resolution.  A head whose every segment boundary has such a window of at
+// most kWinMaxChunks chunks (checked on the device for each call) runs its
+// segments independently in one pass: segment p runs chunks [start_p,
+// wbnd[p+1]) and stores the outputs of [wbnd[p], wbnd[p+1]).  Other heads run
+// the two-pass algorithm, which is exact for any gates.
+//
+// Per (sequence, head), slot 0 of the carry (which the two-pass path does not
+// use) holds the window words in its Phi area (word p >= 1: start_p, or -1
+// when boundary p has no window; the head runs windowed when none is -1)
+// and, in its S area, the final state as fp32: the last segment writes it
+// there and pass 2 moves it to the caller's state, so that no segment that
+// reads the initial state races the one that ends the sequence.
+constexpr int kWinMaxChunks = 4;
+constexpr float kWinLog2Bound = -24.f;
+
+GDN_DEV int *win_words(float *carry, int b, int h, int Hv, int P) {
+    return reinterpret_cast<int *>(carry_slot(carry, b, h, Hv, P, 0, kPhi));
+}
+
+// One workgroup per (head, boundary p >= 1, sequence): the bound's log2 over
+// the kWinMaxChunks chunks before wbnd[p] (wave j: chunk wbnd[p] - 1 - j,
+// read as 16 coalesced 1 KiB row groups; a row's |k|^2 sums over its 16
+// lanes), then the shortest window that meets the bound: word p = its first
+// chunk, or -1 when none does.  A window that reaches chunk 0 starts from the
+// initial state and is exact.
+__global__ __launch_bounds__(256) void prefill_window_check_kernel(SegArgs a) {
+    static_assert(kWinMaxChunks == 4, "one wave per window chunk");
+    const int h = blockIdx.x, p = blockIdx.y + 1, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kh = h / (a.Hv / a.Hk);
+    __shared__ float lam[kWinMaxChunks];
+    __shared__ float kkrow[kWinMaxChunks][C];  // |k_t|^2 of each wave's chunk
+    const int c = a.wbnd[p] - 1 - wave;
+    float x = 0.f;
+    if (c >= 0) {
+        // lane l: the gates of token l of the chunk; instruction i: rows
+        // 4i + lane/16 of the chunk, 16-byte piece lane % 16
+        const int tl = c * C + lane;
+        const size_t gl = ((size_t)b * a.T + min(tl, a.T - 1)) * a.Hv + h;
+        const float gv = a.g[gl], bv = a.beta[gl];
+        const int sub = lane >> 4, piece = lane & 15;
+        u32x4_t w[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int t = min(c * C + 4 * i + sub, a.T - 1);
+            w[i] = *reinterpret_cast<const u32x4_t *>(a.k + (((size_t)b * a.T + t) * a.Hk + kh) * D + 8 * piece);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float kk = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = __uint_as_float(w[i][e] << 16), hi = __uint_as_float(w[i][e] & 0xFFFF0000u);
+                kk += lo * lo + hi * hi;
+            }
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1) kk += __shfl_xor(kk, off);
+            if (piece == 0) kkrow[wave][4 * i + sub] = kk;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (tl < a.T) x = gv * kLog2e + __log2f(fmaxf(1.f, fabsf(1.f - bv * kkrow[wave][lane])));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    }
+    if (lane == 0) lam[wave] = x;
+    __syncthreads();
+    if (tid == 0) {
+        float cum = 0.f;
+        int start = -1;
+        for (int j = 0; j < kWinMaxChunks && start < 0; ++j) {
+            const int cj = a.wbnd[p] - 1 - j;
+            if (cj < 0) start = 0;
+            else if ((cum += lam[j]) <= kWinLog2Bound) start = cj;  // false for NaN
+        }
+        if (start < 0 && a.wbnd[p] <= kWinMaxChunks) start = 0;
+        win_words(a.carry, b, h, a.Hv, a.P)[p] = start;
+    }
+}
+
+// Segment p of a windowed head.
+template <int IN_FMT>
+GDN_DEV void run_window(Smem &sm, const SegArgs &a, int b, int h, int p, const int *w) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int g = lane >> 4, r = lane & 15;
+    const int n_out = a.wbnd[p], n1 = a.wbnd[p + 1];
+    const int n0 = p == 0 ? 0 : __builtin_amdgcn_readfirstlane(w[p]);
+    f32x4_t S[8][2];
+    if (wave < NSW) {
+        if (n0 == 0) {
+            const void *Sg = static_cast<const char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (IN_FMT == kF16 ? 2 : 4);
+            tiles_load<IN_FMT, 2>(S, Sg, 32 * wave, g, r);
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) S[rt][ct] = zero4();
+        }
+    }
+    run_output(sm, S, a, b, h, n0, n1, n_out);
+    if (wave < NSW && p == a.Pw - 1)  // pass 2 moves it to the caller's state
+        tiles_store<kF32, 2>(S, carry_slot(a.carry, b, h, a.Hv, a.P, 0, kSst), 32 * wave, g, r);
+}
+
+// True when head h of sequence b runs windowed in this call: every
+// boundary has a window (words 1 .. Pw-1 >= 0), read by one lane each.
+GDN_DEV bool head_windowed(const SegArgs &a, int b, int h) {
+    if (a.Pw == 0) return false;
+    const int lane = threadIdx.x & 63;
+    const int *w = win_words(a.carry, b, h, a.Hv, a.P);
+    const int x = lane + 1 < a.Pw ? w[lane + 1] : 0;
+    return __builtin_amdgcn_ballot_w64(x < 0) == 0;
+}
+
 // Pass 1: slot p = blockIdx.y < P-1.  Segment 0 runs the output recurrence
-// from the initial state; segments 1 .. P-2 their transition.
+// from the initial state; segments 1 .. P-2 their transition.  A windowed
+// head's workgroups instead run its segments p < Pw (the grid covers the
+// longer of the two plans).
 template <int IN_FMT, int OUT_FMT>
 __global__ __launch_bounds__(NT) void prefill_pass1_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
     const int h = head_of(blockIdx.x, a.Hv), p = blockIdx.y, b = blockIdx.z;
+    if (a.Pw > 0) {
+        if (head_windowed(a, b, h)) {
+            if (p < a.Pw) run_window<IN_FMT>(sm, a, b, h, p, win_words(a.carry, b, h, a.Hv, a.P));
+            return;
+        }
+        if (p >= a.P - 1) return;
+    }
     const int n0 = a.bnd[p], n1 = a.bnd[p + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int g = lane >> 4, r = lane & 15;
@@ -1248,7 +1391,7 @@ __global__ __launch_bounds__(NT) void prefill_pass1_kernel(SegArgs a) {
         f32x4_t S[8][2];
         const void *Sg = static_cast<const char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (IN_FMT == kF16 ? 2 : 4);
         if (wave < NSW) tiles_load<IN_FMT, 2>(S, Sg, 32 * wave, g, r);
-        run_output(sm, S, a, b, h, n0, n1);
+        run_output(sm, S, a, b, h, n0, n1, n0);
         if (wave < NSW) {
             if (a.P == 1) {
                 void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
@@ -1291,6 +1434,18 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
     const int h = head_of(blockIdx.x, a.Hv), p = blockIdx.y + 1, b = blockIdx.z;
+    if (head_windowed(a, b, h)) {  // pass 1 ran it: its final state into the caller's
+        if (blockIdx.y == 0) {
+            const float *src = carry_slot(a.carry, b, h, a.Hv, a.P, 0, kSst);
+            void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
+            float x[D * D / NT];
+#pragma unroll
+            for (int j = 0; j < D * D / NT; ++j) x[j] = src[threadIdx.x + NT * j];
+#pragma unroll
+            for (int j = 0; j < D * D / NT; ++j) state_st<OUT_FMT>(So, threadIdx.x + NT * j, x[j]);
+        }
+        return;
+    }
     const int n0 = a.bnd[p], n1 = a.bnd[p + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int g = lane >> 4, r = lane & 15;
@@ -1305,7 +1460,7 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
         if (wave < NSW) tiles_load<kF32, 2>(S, Sl, 32 * wave, g, r);
         lds_barrier();
     }
-    run_output(sm, S, a, b, h, n0, n1);
+    run_output(sm, S, a, b, h, n0, n1, n0);
     if (wave < NSW && p == a.P - 1) {
         void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
         tiles_store<OUT_FMT, 2>(S, So, 32 * wave, g, r);
@@ -1439,6 +1594,56 @@ const SegPlan &cached_plan(int B, int Hv, int NC) {
     return plan;
 }
 
+// Windowed plan: P segments whose longest fills the device in the fewest
+// rounds of kTargetWgs workgroups.  Segments p >= 1 also run a warm-up
+// window (kWinTyp chunks assumed for planning; the device picks 1 ..
+// kWinMaxChunks), so segment 0, which has none, takes kWinTyp more output
+// chunks.  Modelled time: rounds x the longest segment's chunks.
+constexpr int kWinTyp = 2;
+
+void plan_window(int B, int Hv, int NC, SegPlan &pl) {
+    const int bh = B * Hv;
+    int best_p = 1;
+    long best_cost = NC;
+    for (int P = 2; P <= kMaxSegs && P <= NC - kWinTyp; ++P) {
+        const long rounds = ((long)bh * P + kTargetWgs - 1) / kTargetWgs;
+        const long len = (NC + (long)(P - 1) * kWinTyp + P - 1) / P;
+        if (rounds * len < best_cost) {
+            best_cost = rounds * len;
+            best_p = P;
+        }
+    }
+    pl.P = best_p;
+    pl.bnd[0] = 0;
+    if (best_p == 1) {
+        pl.bnd[1] = NC;
+        return;
+    }
+    // segment 0: L + kWinTyp chunks; the remainder goes to the last segments
+    const int L = (NC - kWinTyp) / best_p, rem = (NC - kWinTyp) - L * best_p;
+    pl.bnd[1] = L + kWinTyp;
+    for (int q = 1; q < best_p; ++q) pl.bnd[q + 1] = pl.bnd[q] + L + (q >= best_p - rem ? 1 : 0);
+}
+
+const SegPlan &cached_window_plan(int B, int Hv, int NC) {
+    thread_local int key_bh = -1, key_nc = -1;
+    thread_local SegPlan plan;
+    if (key_bh != B * Hv || key_nc != NC) {
+        plan_window(B, Hv, NC, plan);
+        key_bh = B * Hv;
+        key_nc = NC;
+    }
+    return plan;
+}
+
+// The shape and plan of the last call that could run windowed, for
+// prefill_windowed_heads.
+struct LastWindowCall {
+    const float *carry = nullptr;
+    int B = 0, Hv = 0, P = 0, Pw = 0;
+};
+LastWindowCall g_last_window;
+
 }  // namespace
 
 size_t prefill_carry_bytes(int B, int T, int Hv) {
@@ -1492,12 +1697,48 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
                 return e;
         attr_set = true;
     }
+    // windowed segments: only where the two-pass path would segment (it
+    // provides the carry); the device decides per head which path runs
+    if (a.P > 1) {
+        const SegPlan &wp = cached_window_plan(B, Hv, NC);
+        if (wp.P > 1) {
+            a.Pw = wp.P;
+            for (int p = 0; p <= wp.P; ++p) a.wbnd[p] = wp.bnd[p];
+        }
+    }
+    hipError_t e;
+    if (a.Pw > 0) {
+        prefill_window_check_kernel<<<dim3(Hv, a.Pw - 1, B), 256, 0, st>>>(a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        g_last_window = LastWindowCall{a.carry, B, Hv, a.P, a.Pw};
+    } else {
+        g_last_window = LastWindowCall{};
+    }
     const int slots = a.P > 1 ? a.P - 1 : 1;
-    pass1<<<dim3(Hv, slots, B), NT, smem, st>>>(a);
-    hipError_t e = hipGetLastError();
+    pass1<<<dim3(Hv, a.Pw > slots ? a.Pw : slots, B), NT, smem, st>>>(a);
+    e = hipGetLastError();
     if (e != hipSuccess || a.P == 1) return e;
     pass2<<<dim3(Hv, a.P - 1, B), NT, smem, st>>>(a);
     return hipGetLastError();
+}
+
+int prefill_windowed_heads() {
+    const LastWindowCall w = g_last_window;
+    if (!w.carry) return 0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    int n = 0;
+    for (int b = 0; b < w.B; ++b)
+        for (int h = 0; h < w.Hv; ++h) {
+            const size_t slot = (((size_t)b * w.Hv + h) * w.P + 0) * 3 + kPhi;
+            int words[kMaxSegs];
+            if (hipMemcpy(words, w.carry + slot * (size_t)(D * D), sizeof(int) * w.Pw, hipMemcpyDeviceToHost) !=
+                hipSuccess)
+                return -1;
+            bool ok = true;
+            for (int p = 1; p < w.Pw; ++p) ok = ok && words[p] >= 0;
+            n += ok;
+        }
+    return n;
 }
 
 }  // namespace gdn

@@ -408,6 +408,13 @@ extern "C" size_t kai_gdn_hip_prefill_workspace_bytes(int batch, int seq_len, in
     return gdn::prefill_carry_bytes(batch, seq_len, num_v_heads);
 }
 
+extern "C" int kai_gdn_hip_prefill_windowed_heads(void) {
+    DeviceCtx *c;
+    if (get_ctx(&c) != hipSuccess) return -1;
+    std::lock_guard<std::mutex> lk(c->mu);
+    return gdn::prefill_windowed_heads();
+}
+
 extern "C" size_t kai_gdn_hip_device_bytes_held(void) {
     DeviceCtx *c;
     if (get_ctx(&c) != hipSuccess) return 0;

@@ -28,7 +28,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from tests.gdn_inputs import bf16_bits, bf16_to_f32, prefill_inputs, rel_errors
+from tests.gdn_inputs import bf16_bits, bf16_to_f32, prefill_inputs, rel_errors, round_bf16
 from tests.gpu_util import P, dev, empty, host, host_u16, stream, torch_mod
 
 pytestmark = pytest.mark.gpu
@@ -148,6 +148,9 @@ def test_prefill_decay_regimes(L, gate):
             chunk = np.arange(T) // 64
             g[:] = np.where(chunk % 2 == 0, -0.6, -0.05)[None, :, None]
         o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+        # weak gates keep the state for thousands of tokens: the exact
+        # two-pass path; the others forget it within a window
+        assert L.kai_gdn_hip_prefill_windowed_heads() == (0 if gate == "weak" else Hv), gate
         o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, T, Hv, Hk, 128, 128, 64)
         check(o, o_ref, T, f"{gate} T={T} output")
         check(Sg, S_ref, T, f"{gate} T={T} state")
@@ -237,6 +240,9 @@ def test_prefill_config3_all_heads(L):
     B, T, Hv, Hk = 1, 16384, 32, 16
     q, k, v, g, beta, S = prefill_inputs(3, B, T, Hv, Hk)
     o1, S1 = gpu_prefill(L, q, k, v, g, beta, S)
+    # the config-3 gates decay the state by about e^-22 per chunk: every
+    # head runs windowed
+    assert L.kai_gdn_hip_prefill_windowed_heads() == B * Hv
     assert np.isfinite(o1).all() and np.isfinite(S1).all()
     o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, B, T, Hv, Hk, 128, 128, 64)
     check(o1, o_ref, T, "output, all 32 heads")
@@ -328,3 +334,63 @@ def test_prefill_config4_long_sequences(L, T):
     o_ref, S_ref = orc.chunk_gdr(*sub, 1, T, 2, 1, 128, 128, 64)
     check(f32(o1[:, :, hv]), o_ref, T, f"output T={T}, heads 30-31")
     check(f32(S1[:, hv]), S_ref, T, f"state (fp16) T={T}, heads 30-31")
+
+
+def test_prefill_windowed_and_exact_heads_in_one_call(L):
+    """Per head, the call picks its path: heads with weak gates (-0.01) run
+    the exact two-pass segments, heads with config-3 gates run windowed
+    segments, in the same launches; both against the oracle."""
+    T, Hv, Hk = 2048 + 37, 8, 4
+    q, k, v, g, beta, S = prefill_inputs(T + 11, 1, T, Hv, Hk)
+    g[:, :, ::2] = -0.01
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    assert L.kai_gdn_hip_prefill_windowed_heads() == Hv // 2
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, "mixed paths output")
+    check(Sg, S_ref, T, "mixed paths state")
+
+
+@pytest.mark.parametrize("g_val,windowed", [(-1.0, False), (-2.0, True)])
+def test_prefill_window_bound_counts_key_norms(L, g_val, windowed):
+    """Keys of norm 3 with beta = 0.5: one token's state map has norm
+    e^g |1 - 4.5| = 3.5 e^g, so g = -1 (3.5 e^-1 > 1: no window bounds the
+    state) must take the exact path and g = -2 (0.47 per token) may run
+    windowed.  Both against the oracle."""
+    T, Hv, Hk = 1600, 4, 2
+    q, k, v, g, beta, S = prefill_inputs(91, 1, T, Hv, Hk)
+    k = round_bf16(3.0 * k)
+    beta[:] = 0.5
+    g[:] = g_val
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    assert L.kai_gdn_hip_prefill_windowed_heads() == (Hv if windowed else 0)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, f"|k| = 3, g = {g_val} output")
+    check(Sg, S_ref, T, f"|k| = 3, g = {g_val} state")
+
+
+@pytest.mark.parametrize("chunk_log2", [-20.0, -70.0, -120.0])
+def test_prefill_window_lengths(L, chunk_log2):
+    """Gates whose chunk decays by 2^-20 (two chunks meet the 2^-24 bound),
+    2^-70 and 2^-120 (one chunk); the last chunk of the window is where a
+    mistake in the window's start would show.  Against the oracle."""
+    T, Hv, Hk = 4096 + 64 * 3, 4, 2
+    q, k, v, g, beta, S = prefill_inputs(5 + int(-chunk_log2), 1, T, Hv, Hk)
+    g[:] = chunk_log2 / 64 * math.log(2.0)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    assert L.kai_gdn_hip_prefill_windowed_heads() == Hv
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, f"chunk decay 2^{chunk_log2:.0f} output")
+    check(Sg, S_ref, T, f"chunk decay 2^{chunk_log2:.0f} state")
+
+
+def test_prefill_windowed_f16_state(L):
+    """The fp16-state variant runs windowed too (its initial state read once,
+    its final state narrowed once)."""
+    T, Hv, Hk = 4096, 8, 4
+    q, k, v, g, beta, S = prefill_inputs(123, 1, T, Hv, Hk)
+    S16 = S.astype(np.float16).astype(np.float32)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S16, f16=True)
+    assert L.kai_gdn_hip_prefill_windowed_heads() == Hv
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S16, 1, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, "windowed fp16 output")
+    check(Sg, S_ref, T, "windowed fp16 state (fp16)")
