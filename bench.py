@@ -928,7 +928,8 @@ def compact_secondary(sec):
              "roofline": {"bound": "mfma",
                           "kernel": "prefill_window_check_kernel+prefill_pass1_kernel+prefill_pass2_kernel",
                           "flop_per_launch": d["flop_per_launch"], "achieved": d["achieved_tflops"],
-                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": d["mfma_frac"]}}
+                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": d["mfma_frac"],
+                          "traffic": profile_traffic("prefill_windowed_call")}}
         if "cpu_baseline" in d:
             e["cpu_baseline"] = compact_cpu(d["cpu_baseline"])
         out["prefill"] = e
