@@ -19,15 +19,16 @@
 //
 // Prefill attention: Qwen3_5Attention's causal softmax(q k^T / 16) v with
 // the sigmoid output gate (modeling_qwen3_5.py:629-701), GQA, head dim 256,
-// on the model's fp16 KV cache.  Block (32 positions, kv head), 8 waves: wave
-// w takes query head kv * rep + (w % 4) at positions +16 (w / 4) .. +15 and
-// walks the keys in blocks of 64 shared through LDS.  Scores on fp16 MFMA
+// on the model's fp16 KV cache.  Block (64 positions, kv head), 8 waves: wave
+// w takes query head kv * rep + (w % 4) at positions +32 (w / 4) .. +31, as
+// two 16-query tiles, and walks the keys in blocks of 64 shared through LDS
+// (K and a transposed copy of V, both moved by DMA).  Scores on fp16 MFMA
 // 16x16x32 as S^T = K q^T (A = the 16-key x 32-dim fragment, which is one
-// contiguous 1 KB of the tiled K cache; B = the wave's queries), online
+// contiguous 1 KB of the tiled K cache; B = the tile's queries), online
 // softmax in exp2 per query column, then O^T = V^T P^T with P taken from the
 // score registers as the B operand (the 8 keys a lane holds, 4g .. 4g+3 and
-// 16 + 4g .. 16 + 4g+3, permute the k index of both operands alike) and
-// V^T read from a transposed copy of V written by the prologue.
+// 16 + 4g .. 16 + 4g+3, permute the k index of both operands alike).  Each K
+// and V fragment read from LDS feeds both query tiles.
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -347,153 +348,208 @@ __global__ __launch_bounds__(512, 1) void w8p2_kernel(const uint16_t *__restrict
 
 // ---- causal prefill attention ------------------------------------------------
 
-constexpr int kApQ = 32;       // positions per block
+constexpr int kApQ = 64;       // positions per block
 constexpr int kApK = 64;       // keys per step
 constexpr int kApD = 256;      // head dim
-constexpr int kApVPitch = 68;  // halves per V^T LDS row: 64 keys + 4 (8-byte reads of 16 rows hit 32 banks)
 
-__global__ __launch_bounds__(512) void attn_prefill_kernel(
+// V^T tile in LDS: [256 dims][64 keys], 128 bytes per dim row, the 16-byte
+// piece c of row d in slot c ^ (d % 8): a fragment read (16 rows x 32
+// bytes) then covers every bank twice, the minimum.
+GDN_DEV int vt_slot(int d, int c) { return d * kApK + ((c ^ (d & 7)) << 3); }
+
+// Block (64 positions, kv head), 8 waves: wave w takes query head
+// kv * rep + (w % 4) at positions +32 (w / 4) .. +31, as two 16-query tiles
+// that share every K and V fragment the wave reads from LDS (two MFMAs per
+// fragment read, against one with a tile per wave: the LDS reads bounded
+// that form).  K (the cache's tiled layout, 32 KB per step, contiguous) and
+// V^T (from the transposed copy) reach LDS by DMA, double buffered.
+constexpr int kApT = 2;  // query tiles per wave
+constexpr int kApThreads = 512;
+
+__global__ __launch_bounds__(kApThreads) void attn_prefill_kernel(
     const uint16_t *__restrict__ q16, const uint16_t *__restrict__ Kc, const uint16_t *__restrict__ vT,
     const float *__restrict__ gate, int gate_row, uint16_t *__restrict__ out16, int T, int Hq, int Hkv, int Tmax,
     int Tv, float sc_log2) {
-    __shared__ __align__(16) uint16_t ks[2][kApK * kApD];        // tiled as in the cache
-    __shared__ __align__(16) uint16_t vs[2][kApD * kApVPitch];  // [dim][key]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) uint16_t ks[2][kApK * kApD];  // tiled as in the cache
+    __shared__ __align__(16) uint16_t vs[2][kApD * kApK];  // [dim][key], swizzled pieces
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: the DMA addresses stay in SGPRs
     const int g = lane >> 4, r = lane & 15;
     const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
     const int kv = blockIdx.y;
     const int rep = Hq / Hkv;
     const bool live = (wave & 3) < rep;                   // wave-uniform
     const int h = kv * rep + min(wave & 3, rep - 1);
-    const int qpos = qb * kApQ + 16 * (wave >> 2) + r;    // this lane's query (B column r)
+    int qpos[kApT];
+#pragma unroll
+    for (int qt = 0; qt < kApT; ++qt) qpos[qt] = qb * kApQ + 32 * (wave >> 2) + 16 * qt + r;  // B column r
 
     // the wave's queries as B operands: dims 32 j + 8 g .. +7 of query r
-    f16x8_t qf[8];
-    {
-        const uint16_t *qp = q16 + ((size_t)min(qpos, T - 1) * Hq + h) * kApD + 8 * g;
+    f16x8_t qf[kApT][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qf[j] = *reinterpret_cast<const f16x8_t *>(qp + 32 * j);
+    for (int qt = 0; qt < kApT; ++qt) {
+        const uint16_t *qp = q16 + ((size_t)min(qpos[qt], T - 1) * Hq + h) * kApD + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qf[qt][j] = *reinterpret_cast<const f16x8_t *>(qp + 32 * j);
     }
-    f32x4_t o[16];  // O^T: dims 16 dt + 4 g + e of query r
+    f32x4_t o[kApT][16];  // O^T per tile: dims 16 dt + 4 g + e of query r
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) o[dt] = zero4();
-    float m = -INFINITY, l = 0.f;  // running max (log2 units, all lanes of column r agree); partial sum
+    for (int qt = 0; qt < kApT; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) o[qt][dt] = zero4();
+    // running max (log2 units, all lanes of column r agree) and partial sum, per tile
+    float m[kApT], l[kApT];
+#pragma unroll
+    for (int qt = 0; qt < kApT; ++qt) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
+    }
 
     const int kend = min(T, qb * kApQ + kApQ);
     const int nkb = (kend + kApK - 1) / kApK;
     const uint16_t *kbase = Kc + (size_t)kv * Tmax * kApD;
     const uint16_t *vbase = vT + (size_t)kv * kApD * Tv;
-    // staging: K 16-byte chunk tid + 512 i of the block's 32 KB (group i:
-    // 16 keys, 8 KB contiguous in the cache), consecutive lanes on
-    // consecutive chunks so the LDS stores do not collide; V^T row tid / 2,
-    // keys 32 (tid % 2) .. +31
-    u32x4_t kr[4], vr[4];
-    const int vrow = tid >> 1, vhalf = (tid & 1) * 32;
-    auto gload = [&](int kb) {
-        // a group past the cache rows reads the last group instead (its
-        // keys are masked: every key >= T lies after every query)
+    // DMA of step kb into buffer b: wave w moves K kilobytes 4w .. 4w+3 (of
+    // 16-key group w / 2: a group past the cache rows reads the last group
+    // instead, its keys are masked, every key >= T lies after every query)
+    // and V^T rows 32 w .. 32 w + 31 (8 per instruction)
+    // per-lane parts of the DMA addresses (loop-invariant): K chunk lane of a
+    // kilobyte; V^T row lane / 8 of an 8-row group (whose first row is a
+    // multiple of 8, so the row's swizzle is (lane / 8) % 8), piece lane % 8
+    const int koff = lane * 8;
+    const int voff = (lane >> 3) * Tv + 8 * ((lane & 7) ^ (lane >> 3));
+    auto dma = [&](int kb, int b) {
+        const int t0 = min(kb * kApK + 16 * (wave >> 1), Tmax - 16);
+        const uint16_t *kp = kbase + (size_t)t0 * kApD + (4 * (wave & 1)) * 512;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t0 = min(kb * kApK + 16 * i, Tmax - 16);
-            kr[i] = *reinterpret_cast<const u32x4_t *>(kbase + (size_t)t0 * kApD + tid * 8);
-        }
-        const uint16_t *vp = vbase + (size_t)vrow * Tv + kb * kApK + vhalf;
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(kp + i * 512 + koff, (lds_void_t *)&ks[b][(4 * wave + i) * 512], 16, 0,
+                                             0);
+        const uint16_t *vp = vbase + (size_t)(32 * wave) * Tv + kb * kApK;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vr[i] = *reinterpret_cast<const u32x4_t *>(vp + 8 * i);
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(vp + (size_t)(8 * i) * Tv + voff,
+                                             (lds_void_t *)&vs[b][(32 * wave + 8 * i) * kApK], 16, 0, 0);
     };
-    auto lstore = [&](int b) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t *>(&ks[b][i * 4096 + tid * 8]) = kr[i];
-        uint16_t *vd = &vs[b][vrow * kApVPitch + vhalf];  // 8-byte aligned rows
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<u32x2_t *>(vd + 8 * i) = u32x2_t{vr[i][0], vr[i][1]};
-            *reinterpret_cast<u32x2_t *>(vd + 8 * i + 4) = u32x2_t{vr[i][2], vr[i][3]};
-        }
-    };
+    // One step: the 64 keys of buffer b as two halves of 32, each an online
+    // softmax update (scores, P, then P V), so that one half's scores and P
+    // fragments are live at a time (registers).
     auto step = [&](int b, int kb) {
         if (!live) return;
-        // S^T tiles: keys kb * 64 + 16 kt + 4 g + e, query r
-        f32x4_t s[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            s[kt] = zero4();
+        for (int half = 0; half < 2; ++half) {
+            // S^T tiles: keys kb * 64 + 32 half + 16 kh + 4 g + e, query r of tile qt
+            f32x4_t s[kApT][2];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    *reinterpret_cast<const f16x8_t *>(&ks[b][kt * 4096 + j * 512 + lane * 8]), qf[j], s[kt], 0, 0,
-                    0);
-        }
-        float mx = m;
+            for (int kh = 0; kh < 2; ++kh) {
+                const int kt = 2 * half + kh;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+                for (int qt = 0; qt < kApT; ++qt) s[qt][kh] = zero4();
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int key = kb * kApK + 16 * kt + 4 * g + e;
-                const float v = key <= qpos ? s[kt][e] * sc_log2 : -INFINITY;
-                s[kt][e] = v;
-                mx = fmaxf(mx, v);
+                for (int j = 0; j < 8; ++j) {
+                    const f16x8_t kf = *reinterpret_cast<const f16x8_t *>(&ks[b][kt * 4096 + j * 512 + lane * 8]);
+#pragma unroll
+                    for (int qt = 0; qt < kApT; ++qt)
+                        s[qt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[qt][j], s[qt][kh], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one key tile's fragments in flight at a time
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // key 0 precedes every query, so the first step leaves mx finite
-        const float alpha = __builtin_amdgcn_exp2f(m - mx);
-        m = mx;
-        // once the running maxima settle, alpha is 1 in every lane: skip
-        // the 64 multiplies of O (x * 1 = x, so the result is the same)
-        if (__ballot(alpha != 1.0f)) {
-            l *= alpha;
+            f16x8_t pb[kApT];  // P^T fragments: keys 32 half + {4g .. 4g+3, 16 + 4g .. 16 + 4g+3}
 #pragma unroll
-            for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
-        }
-        f16x8_t pb[2];  // P^T fragments: keys 32 ks + {4g .. 4g+3, 16 + 4g .. 16 + 4g+3}
+            for (int qt = 0; qt < kApT; ++qt) {
+                float mx = m[qt];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+                for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float p = __builtin_amdgcn_exp2f(s[kt][e] - mx);
-                l += p;
-                pb[kt >> 1][(kt & 1) * 4 + e] = (_Float16)p;
+                    for (int e = 0; e < 4; ++e) {
+                        const int key = kb * kApK + 32 * half + 16 * kh + 4 * g + e;
+                        const float v = key <= qpos[qt] ? s[qt][kh][e] * sc_log2 : -INFINITY;
+                        s[qt][kh][e] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                // the first half of the first step holds key 0, which precedes
+                // every query: mx is finite from then on (a later fully
+                // masked half leaves m and alpha = 1 unchanged)
+                const float alpha = __builtin_amdgcn_exp2f(m[qt] - mx);
+                m[qt] = mx;
+                // once the running maxima settle, alpha is 1 in every lane: skip
+                // the 64 multiplies of O (x * 1 = x, so the result is the same)
+                if (__ballot(alpha != 1.0f)) {
+                    l[qt] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < 16; ++dt) o[qt][dt] *= alpha;
+                }
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float p = __builtin_amdgcn_exp2f(s[qt][kh][e] - mx);
+                        l[qt] += p;
+                        pb[qt][kh * 4 + e] = (_Float16)p;
+                    }
             }
-#pragma unroll
-        for (int ksn = 0; ksn < 2; ++ksn)
+            __builtin_amdgcn_sched_barrier(0);
+            // per-lane V^T offsets of this half, recomputed here (a few VALU
+            // operations) rather than kept live across the step: row r, keys
+            // 32 half + 4 g .. +3 (piece 4 half + g / 2, half g % 2) and 16
+            // keys further (piece + 2); row 16 dt + r adds 1024 dt
+            int vlo, vhi;
+            {
+                int ln = lane;
+                __asm__ volatile("" : "+v"(ln));
+                const int gg = ln >> 4, rr = ln & 15;
+                vlo = vt_slot(rr, 4 * half + (gg >> 1)) + 4 * (gg & 1);
+                vhi = vt_slot(rr, 4 * half + 2 + (gg >> 1)) + 4 * (gg & 1);
+            }
 #pragma unroll
             for (int dt = 0; dt < 16; ++dt) {
-                const uint16_t *vp = &vs[b][(16 * dt + r) * kApVPitch + 32 * ksn + 4 * g];
-                const u32x2_t lo = *reinterpret_cast<const u32x2_t *>(vp);
-                const u32x2_t hi = *reinterpret_cast<const u32x2_t *>(vp + 16);
-                const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), pb[ksn], o[dt], 0, 0, 0);
+                const uint16_t *vb = &vs[b][1024 * dt];  // rows 16 dt + r keep their swizzle (16 dt % 8 = 0)
+                const u32x2_t lo = *reinterpret_cast<const u32x2_t *>(vb + vlo);
+                const u32x2_t hi = *reinterpret_cast<const u32x2_t *>(vb + vhi);
+                const f16x8_t a = __builtin_bit_cast(f16x8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+                for (int qt = 0; qt < kApT; ++qt)
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[qt], o[qt][dt], 0, 0, 0);
+                if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // four V fragments in flight
             }
+        }
     };
 
-    gload(0);
-    lstore(0);
+    dma(0, 0);
+    wait_vm<0>();
     __syncthreads();
     for (int kb = 0; kb < nkb; ++kb) {
-        if (kb + 1 < nkb) gload(kb + 1);
+        if (kb + 1 < nkb) dma(kb + 1, (kb + 1) & 1);  // into the buffer step kb - 1 read
         step(kb & 1, kb);
-        if (kb + 1 < nkb) lstore((kb + 1) & 1);
+        wait_vm<0>();
         __syncthreads();
     }
-    if (!live || qpos >= T) return;
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.0f / l;
-    const float *gp = gate + (size_t)qpos * gate_row + (size_t)h * 512;
-    uint16_t *op = out16 + ((size_t)qpos * Hq + h) * kApD;
+    if (!live) return;
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-        const int d = 16 * dt + 4 * g;
-        const f32x4_t gt = *reinterpret_cast<const f32x4_t *>(gp + d);
-        uint32_t hv[2];
+    for (int qt = 0; qt < kApT; ++qt) {
+        // lanes of one query column agree on qpos, so the shuffles stay within active lanes
+        if (qpos[qt] >= T) continue;
+        float lt = l[qt];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const float inv = 1.0f / lt;
+        const float *gp = gate + (size_t)qpos[qt] * gate_row + (size_t)h * 512;
+        uint16_t *op = out16 + ((size_t)qpos[qt] * Hq + h) * kApD;
 #pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-            const float a = (o[dt][e] * inv) * (1.0f / (1.0f + expf(-gt[e])));
-            const float b = (o[dt][e + 1] * inv) * (1.0f / (1.0f + expf(-gt[e + 1])));
-            hv[e / 2] = (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+        for (int dt = 0; dt < 16; ++dt) {
+            const int d = 16 * dt + 4 * g;
+            const f32x4_t gt = *reinterpret_cast<const f32x4_t *>(gp + d);
+            uint32_t hv[2];
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const float a = (o[qt][dt][e] * inv) * (1.0f / (1.0f + expf(-gt[e])));
+                const float b = (o[qt][dt][e + 1] * inv) * (1.0f / (1.0f + expf(-gt[e + 1])));
+                hv[e / 2] = (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+            }
+            *reinterpret_cast<uint2 *>(op + d) = make_uint2(hv[0], hv[1]);
         }
-        *reinterpret_cast<uint2 *>(op + d) = make_uint2(hv[0], hv[1]);
     }
 }
 
@@ -527,7 +583,7 @@ hipError_t launch_attn_prefill(const uint16_t *q16, const uint16_t *Kc, const ui
     if (Hkv <= 0 || Hq % Hkv || Hq / Hkv > 4 || Tmax % 16 || Tmax < T || Tv % kApK || Tv < T)
         return hipErrorInvalidValue;
     const float sc_log2 = scaling * 1.4426950408889634f;
-    attn_prefill_kernel<<<dim3((unsigned)((T + kApQ - 1) / kApQ), (unsigned)Hkv), 512, 0, st>>>(
+    attn_prefill_kernel<<<dim3((unsigned)((T + kApQ - 1) / kApQ), (unsigned)Hkv), kApThreads, 0, st>>>(
         q16, Kc, vT, gate, gate_row, out16, T, Hq, Hkv, Tmax, Tv, sc_log2);
     return hipGetLastError();
 }
