@@ -394,3 +394,18 @@ def test_prefill_windowed_f16_state(L):
     o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S16, 1, T, Hv, Hk, 128, 128, 64)
     check(o, o_ref, T, "windowed fp16 output")
     check(Sg, S_ref, T, "windowed fp16 state (fp16)")
+
+
+def test_prefill_windowed_batch_of_two(L):
+    """Two sequences in one call, both windowed but for one head of the
+    second sequence, whose weak gates take the exact path: each (sequence,
+    head) decides on its own, and the final states land in their own slots.
+    Ragged T (not a multiple of 64)."""
+    B, T, Hv, Hk = 2, 3000, 4, 2
+    q, k, v, g, beta, S = prefill_inputs(202, B, T, Hv, Hk)
+    g[1, :, 3] = -0.01
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    assert L.kai_gdn_hip_prefill_windowed_heads() == B * Hv - 1
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, B, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, "B=2 output")
+    check(Sg, S_ref, T, "B=2 state")
