@@ -340,11 +340,12 @@ size_t kai_gdn_hip_prefill_workspace_bytes(int batch, int seq_len, int num_v_hea
  * with the largest call seen and are kept until the process ends. */
 size_t kai_gdn_hip_device_bytes_held(void);
 /* No reference counterpart.  How many (sequence, value head) pairs of the
- * last chunked-prefill call on this process ran as windowed segments (each
+ * last chunked-prefill call ran as windowed segments (each
  * segment restarted from a zero state a few chunks before its first output,
  * taken where the state map over that window has norm at most 2^-24) rather
  * than by the exact two-pass segment algorithm; 0 when that call ran as one
- * segment.  Synchronises the device.  Returns -1 on a device error. */
+ * segment.  Counts the last call on the current device.  Synchronises the
+ * device.  Returns -1 on a device error. */
 int kai_gdn_hip_prefill_windowed_heads(void);
 
 /* ---- measurement probes --------------------------------------------------

@@ -1636,13 +1636,20 @@ const SegPlan &cached_window_plan(int B, int Hv, int NC) {
     return plan;
 }
 
-// The shape and plan of the last call that could run windowed, for
-// prefill_windowed_heads.
+// The shape and plan of the last call on each device that could run
+// windowed, for prefill_windowed_heads (calls on one device are serialised
+// by the caller, which holds that device's lock).
 struct LastWindowCall {
     const float *carry = nullptr;
     int B = 0, Hv = 0, P = 0, Pw = 0;
 };
-LastWindowCall g_last_window;
+constexpr int kMaxDevices = 64;
+LastWindowCall g_last_window[kMaxDevices];
+LastWindowCall *last_window_slot() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    return &g_last_window[dev];
+}
 
 }  // namespace
 
@@ -1710,9 +1717,9 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
     if (a.Pw > 0) {
         prefill_window_check_kernel<<<dim3(Hv, a.Pw - 1, B), 256, 0, st>>>(a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        g_last_window = LastWindowCall{a.carry, B, Hv, a.P, a.Pw};
-    } else {
-        g_last_window = LastWindowCall{};
+        if (LastWindowCall *lw = last_window_slot()) *lw = LastWindowCall{a.carry, B, Hv, a.P, a.Pw};
+    } else if (LastWindowCall *lw = last_window_slot()) {
+        *lw = LastWindowCall{};
     }
     const int slots = a.P > 1 ? a.P - 1 : 1;
     pass1<<<dim3(Hv, a.Pw > slots ? a.Pw : slots, B), NT, smem, st>>>(a);
@@ -1723,7 +1730,9 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
 }
 
 int prefill_windowed_heads() {
-    const LastWindowCall w = g_last_window;
+    const LastWindowCall *lw = last_window_slot();
+    if (!lw) return -1;
+    const LastWindowCall w = *lw;
     if (!w.carry) return 0;
     if (hipDeviceSynchronize() != hipSuccess) return -1;
     int n = 0;
