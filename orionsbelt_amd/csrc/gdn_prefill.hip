@@ -238,7 +238,8 @@ struct Gates {
     float egl[C];   // e^{G_last - G}
     float seg[C];   // scale e^{G}
     float gam;      // e^{G_last}
-    float pad[3];
+    float mnorm;    // largest column sum of |M| (the matrix 1-norm), NaN if M is not finite
+    float pad[2];
 };
 
 // Fragments of the lower block triangle of a 64x64 matrix X for 16x16x32
@@ -554,7 +555,46 @@ GDN_DEV void row_subst(float (&x)[16], const f32x4_t (&mcol)[4], int j) {
     x[0] = -acc[0];
 }
 
-GDN_DEV void t_subst(Smem &sm, u32x4_t (&Tf)[6][64], TRegs &tr, int lane) {
+// The 1-norm of M (largest column sum of |M|) from the values t_subst holds:
+// lane (a, j) column j of M_aa, every lane (g, r) rows 4g .. 4g+3 of column
+// r of each off-diagonal block.  Sums of |x| propagate NaN; the max keeps it.
+GDN_DEV float m_one_norm(const f32x4_t (&mcol)[4], const f32x4_t (&MC)[6]) {
+    constexpr int off_b[6] = {0, 1, 2, 0, 1, 0};
+    // per lane: column r of each column block b < 3, over the rows it holds
+    u32x4_t cb;
+    float c[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c[off_b[i]] += fabsf(MC[i][e]);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) cb[b] = __builtin_bit_cast(uint32_t, c[b]);
+    // afterwards cb[q] row g holds c[g] of row group q: their sum is the
+    // off-diagonal part of column 16 g + r
+    row_transpose4(cb);
+    float col = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) col += __builtin_bit_cast(float, cb[q]);
+    // the diagonal block's part: lane (a, j) holds column j of block a,
+    // the same column
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) col += fabsf(mcol[q][e]);
+    // largest over the wave: rows by DPP, then the four rows' last lanes
+    auto mx = [](float x, float y) { return (x > y || x != x) ? x : y; };
+    col = mx(col, dpp_src<0x111, 0xF>(col));  // row_shr:1
+    col = mx(col, dpp_src<0x112, 0xF>(col));  // row_shr:2
+    col = mx(col, dpp_src<0x114, 0xF>(col));  // row_shr:4
+    col = mx(col, dpp_src<0x118, 0xF>(col));  // row_shr:8
+    const int ci = __builtin_bit_cast(int, col);
+    float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(ci, 15));
+    m = mx(m, __builtin_bit_cast(float, __builtin_amdgcn_readlane(ci, 31)));
+    m = mx(m, __builtin_bit_cast(float, __builtin_amdgcn_readlane(ci, 47)));
+    return mx(m, __builtin_bit_cast(float, __builtin_amdgcn_readlane(ci, 63)));
+}
+
+GDN_DEV void t_subst(Smem &sm, u32x4_t (&Tf)[6][64], TRegs &tr, float *mnorm, int lane) {
     const int g = lane >> 4, r = lane & 15;
     // one LDS round trip for every input: lane (a, j) reads column j of M_aa,
     // every lane the accumulator tiles of the six off-diagonal blocks
@@ -565,6 +605,10 @@ GDN_DEV void t_subst(Smem &sm, u32x4_t (&Tf)[6][64], TRegs &tr, int lane) {
     constexpr int off_a[6] = {1, 2, 3, 2, 3, 3}, off_b[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
     for (int i = 0; i < 6; ++i) tr.MC[i] = lds_f4(&sm.Mb[mbi(off_a[i], off_b[i])][kMbPitch * r + 4 * g]);
+    {
+        const float mn = m_one_norm(mcol, tr.MC);
+        if (lane == 0) *mnorm = mn;
+    }
     // lane (a, j) computes row j of T_aa
     {
         float x[16];
@@ -948,7 +992,7 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
     else if (WITH_Q && hw == 3) qk(n0, true);
     else if (WITH_Q && h0) qk(n0, false);
     lds_barrier();
-    if (h0) t_subst(sm, sm.Tf[pslot(n0, n0)], tr, lane);
+    if (h0) t_subst(sm, sm.Tf[pslot(n0, n0)], tr, &sm.gt[pslot(n0, n0)].mnorm, lane);
     lds_barrier();
     for (int n = n0; n < n1; ++n) {
         const bool more = n + 1 < n1;
@@ -974,7 +1018,7 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
         if (h2) wait_vmem0();  // q rows of chunk n+1
         lds_barrier();              // X
         if (h0) {
-            if (more) t_subst(sm, sm.Tf[pslot(n + 1, n0)], tr, lane);
+            if (more) t_subst(sm, sm.Tf[pslot(n + 1, n0)], tr, &sm.gt[pslot(n + 1, n0)].mnorm, lane);
         } else if (WITH_Q && h2) {
             // into the slot chunk n's q leaves (read in phase 1 only)
             load_rows_n<16>(sm.Qb[pslot(n + 2, n0)], a.q, a.Hk, kh, b, c2, a.T, 0, lane);
@@ -1054,28 +1098,51 @@ GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int 
                 for (int e = 0; e < 4; ++e) P[rt][ct][e] = bt[e] * (vv[e] - eg[e] * P[rt][ct][e]);
             }
         }
-        // v = R + (T - I) R, with R as a hi + lo pair: consecutive rows of R
-        // can nearly cancel in T R (repeated keys), so R keeps 16 bits here
+        // v = R + (T - I) R.  Consecutive rows of R can nearly cancel in T R
+        // (repeated keys), so R goes in as a hi + lo pair of bf16 fragments,
+        // unless the chunk's M has 1-norm s < 1/2: then |T - I|_1 <= s/(1-s)
+        // and |R|_1 <= (1+s)|v|_1 bound the error of one bf16 rounding of R
+        // by 1.5 bf16 roundings of v, which the products below apply to v
+        // anyway.
         {
-            bf16x8_t rh[2][2], rl[2][2];
+            const float mn = __builtin_bit_cast(
+                float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, gt.mnorm)));
+            if (mn < 0.5f) {
+                bf16x8_t rh[2][2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) frag_acc_split(P[2 * kb][ct], P[2 * kb + 1][ct], rh[kb][ct], rl[kb][ct]);
+                    for (int ct = 0; ct < 2; ++ct) rh[kb][ct] = frag_acc(P[2 * kb][ct], P[2 * kb + 1][ct]);
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt)
+                for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-                for (int kb = 0; kb <= (rt >> 1); ++kb) {
-                    const bf16x8_t tf = frag_ld(sm.Tf[pslot(n, n0)][fidx(rt, kb)][lane]);
+                    for (int kb = 0; kb <= (rt >> 1); ++kb) {
+                        const bf16x8_t tf = frag_ld(sm.Tf[pslot(n, n0)][fidx(rt, kb)][lane]);
 #pragma unroll
-                    for (int ct = 0; ct < 2; ++ct) {
-                        P[rt][ct] = mfma_16x16x32_bf16(tf, rh[kb][ct], P[rt][ct]);
-                        P[rt][ct] = mfma_16x16x32_bf16(tf, rl[kb][ct], P[rt][ct]);
+                        for (int ct = 0; ct < 2; ++ct) P[rt][ct] = mfma_16x16x32_bf16(tf, rh[kb][ct], P[rt][ct]);
                     }
-                }
+            } else {
+                bf16x8_t rh[2][2], rl[2][2];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        frag_acc_split(P[2 * kb][ct], P[2 * kb + 1][ct], rh[kb][ct], rl[kb][ct]);
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                    for (int kb = 0; kb <= (rt >> 1); ++kb) {
+                        const bf16x8_t tf = frag_ld(sm.Tf[pslot(n, n0)][fidx(rt, kb)][lane]);
+#pragma unroll
+                        for (int ct = 0; ct < 2; ++ct) {
+                            P[rt][ct] = mfma_16x16x32_bf16(tf, rh[kb][ct], P[rt][ct]);
+                            P[rt][ct] = mfma_16x16x32_bf16(tf, rl[kb][ct], P[rt][ct]);
+                        }
+                    }
+            }
         }
-        // o^T = scale e^G O^T + v^T A^T
-        {
+        // o^T = scale e^G O^T + v^T A^T (a warm-up chunk stores no outputs)
+        if (n >= n_out) {
             const int ps = pslot(n, n0);
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
@@ -1098,7 +1165,7 @@ GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int 
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct) O[ct][tt] = mfma_16x16x32_bf16(vf[kb][ct], af, O[ct][tt]);
                 }
-            const int valid = n < n_out ? 0 : min(C, a.T - n * C);
+            const int valid = min(C, a.T - n * C);
             uint16_t *ob = a.o + (((size_t)b * a.T + (size_t)n * C) * a.Hv + h) * D + c0 + 4 * g;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {

@@ -3,7 +3,8 @@ of HF torch_chunk_gated_delta_rule (fp32), through the C-ABI.
 
 The kernel feeds bf16 operands to MFMA (q/k/v are bf16 inputs; T - I, the
 bf16 copy of S, v_new and A are rounded to bf16 once each; R enters as a
-bf16 hi + lo pair) and accumulates in fp32; the state stays fp32 and the
+bf16 hi + lo pair, or as one bf16 fragment in chunks whose M has 1-norm
+below 1/2) and accumulates in fp32; the state stays fp32 and the
 output is stored in bf16.  Bounds, relative to the largest reference
 magnitude (max) and as a relative 2-norm (l2):
     output  max <= 1.0e-2   l2 <= 5.0e-3
@@ -190,6 +191,26 @@ def test_prefill_repeated_keys(L):
             mx, l2 = rel_errors(got, ref)
             print(f"repeated keys beta={beta_v} {what}: max_rel {mx:.3e} l2_rel {l2:.3e}", flush=True)
             assert mx <= 4e-2 and l2 <= 3.5e-2, f"beta={beta_v} {what}: max_rel {mx:.3e} l2_rel {l2:.3e}"
+
+
+@pytest.mark.parametrize("beta_v", [0.0075, 0.0085])
+def test_prefill_repeated_keys_at_the_norm_bound(L, beta_v):
+    """The one-fragment T R product is taken when the chunk's M has 1-norm
+    below 1/2.  Identical keys with no decay make column 0 of M sum to
+    63 beta |k|^2: 0.47 at beta = 0.0075 (one bf16 fragment of R) and 0.54 at
+    0.0085 (the hi + lo pair).  A zero start state leaves the outputs to the
+    v products alone; both sides of the bound meet the generic bounds."""
+    q, k, v, g, beta, S = prefill_inputs(43, 1, 256, 2, 1)
+    k[:, :] = k[:, :1]
+    beta[:] = beta_v
+    g[:] = 0.0
+    S[:] = 0.0
+    col0 = 63 * beta_v * float(np.sum(round_bf16(k[0, 0, 0]) ** 2))
+    assert (col0 < 0.5) == (beta_v < 0.008)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, 256, 2, 1, 128, 128, 64)
+    check(o, o_ref, 256, f"norm-bound beta={beta_v} output")
+    check(Sg, S_ref, 256, f"norm-bound beta={beta_v} state")
 
 
 def test_prefill_split_calls_bit_identical(L):
