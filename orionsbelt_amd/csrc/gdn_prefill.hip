@@ -1165,16 +1165,25 @@ GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int 
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct) O[ct][tt] = mfma_16x16x32_bf16(vf[kb][ct], af, O[ct][tt]);
                 }
+            // one 16-byte store per row tile: a swap between neighbouring
+            // 16-lane rows gives lane (g, r) the eight consecutive columns
+            // 16 (g & 1) + 8 (g >> 1) .. +7 (rows 0, 2 of tile 0 keep theirs
+            // and take rows 0, 2 of tile 1's; rows 1, 3 the reverse)
             const int valid = min(C, a.T - n * C);
-            uint16_t *ob = a.o + (((size_t)b * a.T + (size_t)n * C) * a.Hv + h) * D + c0 + 4 * g;
+            uint16_t *ob = a.o + (((size_t)b * a.T + (size_t)n * C) * a.Hv + h) * D + c0 + 16 * (g & 1) +
+                           8 * (g >> 1);
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
+                const u32x2_t w0 = bf4u(O[0][tt]), w1 = bf4u(O[1][tt]);
+                const auto s0 = __builtin_amdgcn_permlane16_swap(w0[0], w1[0], false, false);
+                const auto s1 = __builtin_amdgcn_permlane16_swap(w0[1], w1[1], false, false);
+                u32x4_t w;
+                w[0] = s0[0];
+                w[1] = s1[0];
+                w[2] = s0[1];
+                w[3] = s1[1];
                 const int t = 16 * tt + r;
-                if (t < valid) {
-#pragma unroll
-                    for (int ct = 0; ct < 2; ++ct)
-                        *reinterpret_cast<u32x2_t *>(ob + (size_t)t * a.Hv * D + 16 * ct) = bf4u(O[ct][tt]);
-                }
+                if (t < valid) *reinterpret_cast<u32x4_t *>(ob + (size_t)t * a.Hv * D) = w;
             }
         }
         // S = e^{G_last} S + K^T diag(e^{G_last - G}) v
