@@ -1350,26 +1350,47 @@ GDN_DEV int *win_words(float *carry, int b, int h, int Hv, int P) {
 }
 
 // One workgroup per (head, boundary p >= 1, sequence): the bound's log2 over
-// the kWinMaxChunks chunks before wbnd[p] (wave j: chunk wbnd[p] - 1 - j,
-// read as 16 coalesced 1 KiB row groups; a row's |k|^2 sums over its 16
-// lanes), then the shortest window that meets the bound: word p = its first
-// chunk, or -1 when none does.  A window that reaches chunk 0 starts from the
-// initial state and is exact.
+// the kWinMaxChunks chunks before wbnd[p] (wave j: chunk wbnd[p] - 1 - j),
+// then the shortest window that meets the bound: word p = its first chunk,
+// or -1 when none does.  A window that reaches chunk 0 starts from the
+// initial state and is exact.  The key factors are at least 1 (log2 >= 0),
+// so no window shorter than the first whose gates alone meet the bound can
+// meet it: the k rows (16 coalesced 1 KiB row groups per chunk; a row's |k|^2
+// sums over its 16 lanes) are read only for that window's chunks, and for
+// the longer windows only when it fails.  A head whose gates never reach the
+// bound reads no k rows at all.
 __global__ __launch_bounds__(256) void prefill_window_check_kernel(SegArgs a) {
     static_assert(kWinMaxChunks == 4, "one wave per window chunk");
     const int h = blockIdx.x, p = blockIdx.y + 1, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kh = h / (a.Hv / a.Hk);
-    __shared__ float lam[kWinMaxChunks];
+    __shared__ float gsum[kWinMaxChunks], lam[kWinMaxChunks];
     __shared__ float kkrow[kWinMaxChunks][C];  // |k_t|^2 of each wave's chunk
+    __shared__ int first_pass;                 // start found in the first round, or -2
     const int c = a.wbnd[p] - 1 - wave;
-    float x = 0.f;
+    const int tl = c * C + lane;
+    float gv = 0.f, bv = 0.f;
     if (c >= 0) {
-        // lane l: the gates of token l of the chunk; instruction i: rows
-        // 4i + lane/16 of the chunk, 16-byte piece lane % 16
-        const int tl = c * C + lane;
+        // lane l: the gates of token l of the chunk
         const size_t gl = ((size_t)b * a.T + min(tl, a.T - 1)) * a.Hv + h;
-        const float gv = a.g[gl], bv = a.beta[gl];
+        gv = a.g[gl];
+        bv = a.beta[gl];
+        float x = tl < a.T ? gv * kLog2e : 0.f;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+        if (lane == 0) gsum[wave] = x;
+    }
+    __syncthreads();
+    // the window length whose gates alone first meet the bound (or that
+    // reaches chunk 0), 0 for none; the same in every thread
+    int L1 = 0;
+    {
+        float cum = 0.f;
+        for (int j = 0; j < kWinMaxChunks && L1 == 0; ++j)
+            if (a.wbnd[p] - 1 - j < 0 || (cum += gsum[j]) <= kWinLog2Bound) L1 = j + 1;  // false for NaN
+    }
+    // lam[wave] = log2 of the bound over this wave's chunk
+    auto chunk_bound = [&] {
         const int sub = lane >> 4, piece = lane & 15;
         u32x4_t w[16];
 #pragma unroll
@@ -1391,20 +1412,34 @@ __global__ __launch_bounds__(256) void prefill_window_check_kernel(SegArgs a) {
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float x = 0.f;
         if (tl < a.T) x = gv * kLog2e + __log2f(fmaxf(1.f, fabsf(1.f - bv * kkrow[wave][lane])));
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-    }
-    if (lane == 0) lam[wave] = x;
-    __syncthreads();
-    if (tid == 0) {
+        if (lane == 0) lam[wave] = x;
+    };
+    // the shortest window among the first n chunks' bounds, or -1
+    auto shortest = [&](int n) {
         float cum = 0.f;
         int start = -1;
-        for (int j = 0; j < kWinMaxChunks && start < 0; ++j) {
+        for (int j = 0; j < n && start < 0; ++j) {
             const int cj = a.wbnd[p] - 1 - j;
             if (cj < 0) start = 0;
             else if ((cum += lam[j]) <= kWinLog2Bound) start = cj;  // false for NaN
         }
+        return start;
+    };
+    if (c >= 0 && wave < L1) chunk_bound();
+    __syncthreads();
+    if (tid == 0) first_pass = L1 == 0 ? -1 : (shortest(L1) >= 0 || L1 == kWinMaxChunks ? shortest(L1) : -2);
+    __syncthreads();
+    int start = first_pass;
+    if (start == -2) {  // the first window failed on its key factors: the longer ones
+        if (c >= 0 && wave >= L1) chunk_bound();
+        __syncthreads();
+        start = shortest(kWinMaxChunks);
+    }
+    if (tid == 0) {
         if (start < 0 && a.wbnd[p] <= kWinMaxChunks) start = 0;
         win_words(a.carry, b, h, a.Hv, a.P)[p] = start;
     }
@@ -1510,15 +1545,15 @@ __global__ __launch_bounds__(NT) void prefill_pass2_kernel(SegArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
     const int h = head_of(blockIdx.x, a.Hv), p = blockIdx.y + 1, b = blockIdx.z;
-    if (head_windowed(a, b, h)) {  // pass 1 ran it: its final state into the caller's
-        if (blockIdx.y == 0) {
-            const float *src = carry_slot(a.carry, b, h, a.Hv, a.P, 0, kSst);
-            void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
-            float x[D * D / NT];
+    if (head_windowed(a, b, h)) {
+        // pass 1 ran it: its final state into the caller's, in 16-byte
+        // pieces spread over all of this head's workgroups
+        const float *src = carry_slot(a.carry, b, h, a.Hv, a.P, 0, kSst);
+        void *So = static_cast<char *>(a.S) + ((size_t)b * a.Hv + h) * (D * D) * (OUT_FMT == kF16 ? 2 : 4);
+        for (int i = blockIdx.y * NT + threadIdx.x; i < D * D / 4; i += gridDim.y * NT) {
+            const f32x4_t x = *reinterpret_cast<const f32x4_t *>(src + 4 * i);
 #pragma unroll
-            for (int j = 0; j < D * D / NT; ++j) x[j] = src[threadIdx.x + NT * j];
-#pragma unroll
-            for (int j = 0; j < D * D / NT; ++j) state_st<OUT_FMT>(So, threadIdx.x + NT * j, x[j]);
+            for (int e = 0; e < 4; ++e) state_st<OUT_FMT>(So, 4 * i + e, x[e]);
         }
         return;
     }
