@@ -26,6 +26,10 @@
 //   pass 2: segment p = 1 .. P-1 first composes its start state,
 //           S_start(q+1) = Phi_q S_start(q) + C_q from S_start(1) = the end of
 //           segment 0, then reruns the recurrence from it, with o.
+// Where the gates let the state forget within a few chunks (checked on the
+// device per sequence and head, before pass 1), a head instead runs its
+// segments independently in pass 1, each from S = 0 a short window before
+// its first output chunk ("windowed segments", below).
 //
 // Workgroup: 8 waves in two roles, one of each role per SIMD.
 //  - State waves 0..3 own 32 state columns each (48 of the 256 in a
@@ -37,10 +41,10 @@
 //    and stream the chunk tiles.  While the state waves are in phase 1 of
 //    chunk n, helper 0 finishes T of chunk n (the off-diagonal 16x16 blocks
 //    on MFMA), helpers 1 and 2 form K K^T of chunk n+1 and write M, and
-//    helper 3 forms half of K Q^T of chunk n+1 (the A fragments).  In
-//    phase 2, helper 0 starts T of chunk n+1 (forward substitution of the
-//    diagonal blocks of M on the VALU), helper 1 forms the other half of
-//    K Q^T, and helpers 2 and 3 load tiles.
+//    helper 3 issues tile loads.  In phase 2, helper 0 starts T of chunk
+//    n+1 (forward substitution of the diagonal blocks of M on the VALU),
+//    helpers 1 and 3 form K Q^T of chunk n+1 (the A fragments), and helper 2
+//    issues tile loads.
 //  Two LDS barriers per chunk separate the phases, so the MFMA-heavy state
 //  work of one role overlaps the latency-bound work of the other.
 //
@@ -1041,7 +1045,7 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
 
 // State waves of an output segment: columns c0 .. c0 + 31 (two tiles).
 // o^T tiles: lane (g, r) of tile (ct, tt) holds o[t = 16 tt + r][c0 + 16 ct
-// + 4g .. +3], one 8-byte store.  Chunks before n_out (a windowed segment's
+// + 4g .. +3].  Chunks before n_out (a windowed segment's
 // warm-up) run the same products but store no output.
 GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h, int n0,
                             int n1, int n_out, int c0, int lane) {
