@@ -370,9 +370,14 @@ def bench_prefill(L, ob, torch, timer, reps=5):
     ms_ref = timer.p50_ms(run, warmup=20, reps=max(reps, 30))
     ms = timer.p50_ms(run, warmup=20, reps=max(reps, 30), warmup_s=PF_WARMUP_S)
     windowed = int(L.kai_gdn_hip_prefill_windowed_heads())
-    # the same shapes with long-memory gates (g = -0.01: the state decays by
-    # e^-0.64 per chunk), which no window bounds: the exact two-pass path
+    # the same shapes with long-memory gates: g = -0.01 (the state decays by
+    # e^-0.64 per chunk, 2^-24 in 26 chunks: windows that long), and
+    # g = -0.001 (no window within a segment bounds it: the exact two-pass
+    # path)
     dg.fill_(-0.01)
+    ms_long = timer.p50_ms(run, warmup=20, reps=max(reps, 30), warmup_s=PF_WARMUP_S)
+    long_windowed = int(L.kai_gdn_hip_prefill_windowed_heads())
+    dg.fill_(-0.001)
     ms_exact = timer.p50_ms(run, warmup=20, reps=max(reps, 30), warmup_s=PF_WARMUP_S)
     exact_windowed = int(L.kai_gdn_hip_prefill_windowed_heads())
     flop = PF_FLOP_PER_CHUNK_HEAD * (PF_T // 64) * HV
@@ -382,6 +387,7 @@ def bench_prefill(L, ob, torch, timer, reps=5):
             "achieved_tflops": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
             "flop_per_launch": flop, "ms_20_warmups": round(ms_ref, 4),
             "windowed_heads": windowed,
+            "ms_long_memory": round(ms_long, 4), "long_memory_windowed_heads": long_windowed,
             "ms_exact_path": round(ms_exact, 4), "exact_path_windowed_heads": exact_windowed,
             "mfma_frac_exact_path": round(flop / (ms_exact * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
             "timing_note": f"ms: p50 of 30 calls after {PF_WARMUP_S:g} s of warm-up calls (steady clocks); "
@@ -924,7 +930,8 @@ def compact_secondary(sec):
         d = sec["prefill"]
         e = {"T": PF_T, "ms": d["ms"], "ms_20_warmups": d["ms_20_warmups"], "tok_s": d["tokens_per_s"],
              "mfma_frac": d["mfma_frac"], "windowed_heads": d["windowed_heads"],
-             "ms_exact_path": d["ms_exact_path"], "mfma_frac_exact_path": d["mfma_frac_exact_path"],
+             "ms_long_memory": d.get("ms_long_memory"), "ms_exact_path": d["ms_exact_path"],
+             "mfma_frac_exact_path": d["mfma_frac_exact_path"],
              "roofline": {"bound": "mfma",
                           "kernel": "prefill_window_check_kernel+prefill_pass1_kernel+prefill_pass2_kernel",
                           "flop_per_launch": d["flop_per_launch"], "achieved": d["achieved_tflops"],

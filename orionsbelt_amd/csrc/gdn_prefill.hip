@@ -70,6 +70,8 @@
 //    the tiles (srow below), which the products that write the state follow
 //    by reading their A operand rows in the same order.
 
+#include <algorithm>
+
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -765,6 +767,7 @@ struct SegArgs {
     // window word names.
     int Pw;
     int wbnd[kMaxSegs + 1];
+    int Wmax;  // longest window checked, in chunks (kWinMin .. kWinCap)
 };
 
 // Ring slots of chunk n in a segment starting at n0.
@@ -1045,8 +1048,8 @@ GDN_DEV void helper_loop(Smem &sm, const SegArgs &a, int b, int h, int n0, int n
 
 // State waves of an output segment: columns c0 .. c0 + 31 (two tiles).
 // o^T tiles: lane (g, r) of tile (ct, tt) holds o[t = 16 tt + r][c0 + 16 ct
-// + 4g .. +3].  Chunks before n_out (a windowed segment's
-// warm-up) run the same products but store no output.
+// + 4g .. +3].  Chunks before n_out (a windowed segment's warm-up) update
+// the state only: no o products, no stores.
 GDN_DEV void state_loop_out(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, int h, int n0,
                             int n1, int n_out, int c0, int lane) {
     const int g = lane >> 4, r = lane & 15;
@@ -1335,7 +1338,7 @@ GDN_DEV void run_output(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, i
 // start its recurrence from S = 0 at the window's first chunk instead of
 // from the true state: what it drops is below that state's own fp32
 // resolution.  A head whose every segment boundary has such a window of at
-// most kWinMaxChunks chunks (checked on the device for each call) runs its
+// most Wmax chunks (checked on the device for each call) runs its
 // segments independently in one pass: segment p runs chunks [start_p,
 // wbnd[p+1]) and stores the outputs of [wbnd[p], wbnd[p+1]).  Other heads run
 // the two-pass algorithm, which is exact for any gates.
@@ -1346,7 +1349,11 @@ GDN_DEV void run_output(Smem &sm, f32x4_t (&S)[8][2], const SegArgs &a, int b, i
 // and, in its S area, the final state as fp32: the last segment writes it
 // there and pass 2 moves it to the caller's state, so that no segment that
 // reads the initial state races the one that ends the sequence.
-constexpr int kWinMaxChunks = 4;
+// Wmax: the planned segment length, at least kWinMin and at most kWinCap
+// chunks.  A window as long as the segment doubles that segment's chunk
+// steps, about what the two-pass path costs.
+constexpr int kWinMin = 4, kWinCap = 32;
+constexpr int kCheckWaves = 16;
 constexpr float kWinLog2Bound = -24.f;
 
 GDN_DEV int *win_words(float *carry, int b, int h, int Hv, int P) {
@@ -1354,47 +1361,82 @@ GDN_DEV int *win_words(float *carry, int b, int h, int Hv, int P) {
 }
 
 // One workgroup per (head, boundary p >= 1, sequence): the bound's log2 over
-// the kWinMaxChunks chunks before wbnd[p] (wave j: chunk wbnd[p] - 1 - j),
-// then the shortest window that meets the bound: word p = its first chunk,
-// or -1 when none does.  A window that reaches chunk 0 starts from the
-// initial state and is exact.  The key factors are at least 1 (log2 >= 0),
-// so no window shorter than the first whose gates alone meet the bound can
-// meet it: the k rows (16 coalesced 1 KiB row groups per chunk; a row's |k|^2
-// sums over its 16 lanes) are read only for that window's chunks, and for
-// the longer windows only when it fails.  A head whose gates never reach the
-// bound reads no k rows at all.
-__global__ __launch_bounds__(256) void prefill_window_check_kernel(SegArgs a) {
-    static_assert(kWinMaxChunks == 4, "one wave per window chunk");
+// up to Wmax chunks before wbnd[p] (chunk j: wbnd[p] - 1 - j), then the
+// shortest window that meets the bound: word p = its first chunk, or -1 when
+// none does.  A window that reaches chunk 0 starts from the initial state
+// and is exact.  The key factors are at least 1 (log2 >= 0), so no window
+// shorter than the first whose gates alone meet the bound can meet it: the
+// k rows (16 coalesced 1 KiB row groups per chunk; a row's |k|^2 sums over
+// its 16 lanes) are read only for that window's chunks, and for the longer
+// windows only when it fails.  A head whose gates never reach the bound
+// reads no k rows.  The windows' sums are prefix sums over the chunks (one
+// wave, lane j = chunk j), and the shortest window is the first lane whose
+// sum meets the bound; the gates' and the key factors' sums take the same
+// order, so a chunk whose key factors are all 1 sums exactly as its gates.
+__global__ __launch_bounds__(64 * kCheckWaves) void prefill_window_check_kernel(SegArgs a) {
     const int h = blockIdx.x, p = blockIdx.y + 1, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kh = h / (a.Hv / a.Hk);
-    __shared__ float gsum[kWinMaxChunks], lam[kWinMaxChunks];
-    __shared__ float kkrow[kWinMaxChunks][C];  // |k_t|^2 of each wave's chunk
-    __shared__ int first_pass;                 // start found in the first round, or -2
-    const int c = a.wbnd[p] - 1 - wave;
-    const int tl = c * C + lane;
-    float gv = 0.f, bv = 0.f;
-    if (c >= 0) {
-        // lane l: the gates of token l of the chunk
-        const size_t gl = ((size_t)b * a.T + min(tl, a.T - 1)) * a.Hv + h;
-        gv = a.g[gl];
-        bv = a.beta[gl];
-        float x = tl < a.T ? gv * kLog2e : 0.f;
+    const int W = a.Wmax;
+    __shared__ float gsum[kWinCap], lam[kWinCap];
+    __shared__ float kkrow[kCheckWaves][C];  // |k_t|^2 of the chunk a wave is on
+    __shared__ int win[2];                   // L1, then the window's start (or -2: read more)
+    auto chunk_of = [&](int j) { return a.wbnd[p] - 1 - j; };
+    auto gate_at = [&](const float *x, int c) {
+        return x[((size_t)b * a.T + min(c * C + lane, a.T - 1)) * a.Hv + h];
+    };
+    // the first lane j < n whose prefix sum of v meets the bound or whose
+    // chunk is before chunk 0, as j + 1 (0: none); wave 0, every lane
+    auto first_window = [&](const float *v, int n) {
+        const bool in = lane < n;
+        const float x = in && chunk_of(lane) >= 0 ? v[lane] : 0.f;
+        const float pre = wave_incl_scan(x);
+        const bool hit = in && (chunk_of(lane) < 0 || pre <= kWinLog2Bound);  // false for NaN
+        const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+        return m ? (int)__builtin_ctzll(m) + 1 : 0;
+    };
+    // gsum[j] for chunks j in [j0, j1): log2 of the gates alone, chunk
+    // j0 + wave + 16 i to this wave, its loads issued together
+    auto gate_sums = [&](int j0, int j1) {
+        constexpr int kPer = kWinCap / kCheckWaves;
+        float x[kPer];
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-        if (lane == 0) gsum[wave] = x;
+        for (int i = 0; i < kPer; ++i) {
+            const int j = j0 + wave + kCheckWaves * i, c = chunk_of(j);
+            x[i] = j < j1 && c >= 0 && c * C + lane < a.T ? gate_at(a.g, c) * kLog2e : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int j = j0 + wave + kCheckWaves * i;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) x[i] += __shfl_xor(x[i], off);
+            if (lane == 0 && j < j1) gsum[j] = x[i];
+        }
+    };
+    // the gates in two rounds: the nearest four chunks, then the rest only
+    // when those do not meet the bound (a lane's gate shares its L2 line
+    // with the other heads', so each chunk costs 64 lines)
+    const int W1 = min(4, W);
+    gate_sums(0, W1);
+    __syncthreads();
+    if (wave == 0) {
+        const int L = first_window(gsum, W1);
+        if (lane == 0) win[0] = L;
     }
     __syncthreads();
-    // the window length whose gates alone first meet the bound (or that
-    // reaches chunk 0), 0 for none; the same in every thread
-    int L1 = 0;
-    {
-        float cum = 0.f;
-        for (int j = 0; j < kWinMaxChunks && L1 == 0; ++j)
-            if (a.wbnd[p] - 1 - j < 0 || (cum += gsum[j]) <= kWinLog2Bound) L1 = j + 1;  // false for NaN
+    if (win[0] == 0 && W1 < W) {
+        gate_sums(W1, W);
+        __syncthreads();
+        if (wave == 0) {
+            const int L = first_window(gsum, W);
+            if (lane == 0) win[0] = L;
+        }
+        __syncthreads();
     }
-    // lam[wave] = log2 of the bound over this wave's chunk
-    auto chunk_bound = [&] {
+    const int L1 = win[0];
+    // lam[j] = log2 of the bound over chunk j
+    auto chunk_bound = [&](int j) {
+        const int c = chunk_of(j);
         const int sub = lane >> 4, piece = lane & 15;
         u32x4_t w[16];
 #pragma unroll
@@ -1402,6 +1444,7 @@ __global__ __launch_bounds__(256) void prefill_window_check_kernel(SegArgs a) {
             const int t = min(c * C + 4 * i + sub, a.T - 1);
             w[i] = *reinterpret_cast<const u32x4_t *>(a.k + (((size_t)b * a.T + t) * a.Hk + kh) * D + 8 * piece);
         }
+        const float gv = gate_at(a.g, c), bv = gate_at(a.beta, c);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             float kk = 0.f;
@@ -1417,34 +1460,35 @@ __global__ __launch_bounds__(256) void prefill_window_check_kernel(SegArgs a) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float x = 0.f;
-        if (tl < a.T) x = gv * kLog2e + __log2f(fmaxf(1.f, fabsf(1.f - bv * kkrow[wave][lane])));
+        if (c * C + lane < a.T) x = gv * kLog2e + __log2f(fmaxf(1.f, fabsf(1.f - bv * kkrow[wave][lane])));
+        __builtin_amdgcn_wave_barrier();  // every lane has read kkrow before the next chunk writes it
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-        if (lane == 0) lam[wave] = x;
+        if (lane == 0) lam[j] = x;
     };
-    // the shortest window among the first n chunks' bounds, or -1
-    auto shortest = [&](int n) {
-        float cum = 0.f;
-        int start = -1;
-        for (int j = 0; j < n && start < 0; ++j) {
-            const int cj = a.wbnd[p] - 1 - j;
-            if (cj < 0) start = 0;
-            else if ((cum += lam[j]) <= kWinLog2Bound) start = cj;  // false for NaN
-        }
-        return start;
-    };
-    if (c >= 0 && wave < L1) chunk_bound();
-    __syncthreads();
-    if (tid == 0) first_pass = L1 == 0 ? -1 : (shortest(L1) >= 0 || L1 == kWinMaxChunks ? shortest(L1) : -2);
-    __syncthreads();
-    int start = first_pass;
-    if (start == -2) {  // the first window failed on its key factors: the longer ones
-        if (c >= 0 && wave >= L1) chunk_bound();
+    // the window's first chunk (0 when it reaches the start), -1 for none
+    auto start_of = [&](int L) { return L == 0 ? -1 : max(chunk_of(L - 1), 0); };
+    if (L1 > 0) {
+        for (int j = wave; j < L1 && chunk_of(j) >= 0; j += kCheckWaves) chunk_bound(j);
         __syncthreads();
-        start = shortest(kWinMaxChunks);
+        if (wave == 0) {
+            const int L = first_window(lam, L1);
+            if (lane == 0) win[1] = L > 0 ? start_of(L) : (L1 < W ? -2 : -1);
+        }
+        __syncthreads();
+        if (win[1] == -2) {  // the first window failed on its key factors: the longer ones
+            for (int j = L1 + wave; j < W && chunk_of(j) >= 0; j += kCheckWaves) chunk_bound(j);
+            __syncthreads();
+            if (wave == 0) {
+                const int L = first_window(lam, W);
+                if (lane == 0) win[1] = start_of(L);
+            }
+            __syncthreads();
+        }
     }
     if (tid == 0) {
-        if (start < 0 && a.wbnd[p] <= kWinMaxChunks) start = 0;
+        int start = L1 > 0 ? win[1] : -1;
+        if (start < 0 && a.wbnd[p] <= W) start = 0;
         win_words(a.carry, b, h, a.Hv, a.P)[p] = start;
     }
 }
@@ -1712,7 +1756,7 @@ const SegPlan &cached_plan(int B, int Hv, int NC) {
 // Windowed plan: P segments whose longest fills the device in the fewest
 // rounds of kTargetWgs workgroups.  Segments p >= 1 also run a warm-up
 // window (kWinTyp chunks assumed for planning; the device picks 1 ..
-// kWinMaxChunks), so segment 0, which has none, takes kWinTyp more output
+// Wmax), so segment 0, which has none, takes kWinTyp more output
 // chunks.  Modelled time: rounds x the longest segment's chunks.
 constexpr int kWinTyp = 2;
 
@@ -1826,11 +1870,12 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
         if (wp.P > 1) {
             a.Pw = wp.P;
             for (int p = 0; p <= wp.P; ++p) a.wbnd[p] = wp.bnd[p];
+            a.Wmax = std::min(kWinCap, std::max(kWinMin, NC / wp.P));
         }
     }
     hipError_t e;
     if (a.Pw > 0) {
-        prefill_window_check_kernel<<<dim3(Hv, a.Pw - 1, B), 256, 0, st>>>(a);
+        prefill_window_check_kernel<<<dim3(Hv, a.Pw - 1, B), 64 * kCheckWaves, 0, st>>>(a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (LastWindowCall *lw = last_window_slot()) *lw = LastWindowCall{a.carry, B, Hv, a.P, a.Pw};
     } else if (LastWindowCall *lw = last_window_slot()) {

@@ -121,6 +121,7 @@ def test_bench_line_is_compact_with_prefill_last():
                                     "ttft_ms": 372.0, "device_bytes": 1}]},
         "prefill": {"ms": 0.2309, "ms_20_warmups": 0.277, "tokens_per_s": 7.1e7, "mfma_frac": 0.1637,
                     "achieved_tflops": 409.3, "flop_per_launch": 94489280512, "windowed_heads": 32,
+                    "ms_long_memory": 0.19, "long_memory_windowed_heads": 32,
                     "ms_exact_path": 0.2433, "mfma_frac_exact_path": 0.1554,
                     "cpu_baseline": {"value": 15302.8, "unit": "tokens/s", "cores": 16, "kind": "port",
                                      "sample": "598 x T=256 (32 heads, OpenMP over heads), 10.0 s"}},
@@ -130,7 +131,7 @@ def test_bench_line_is_compact_with_prefill_last():
     p = c["prefill"]
     assert p["roofline"]["bound"] == "mfma" and p["roofline"]["frac"] == 0.1637
     assert p["cpu_baseline"]["kind"] == "port" and p["cpu_baseline"]["sample"] == "598 x T=256"
-    assert p["windowed_heads"] == 32 and p["ms_exact_path"] == 0.2433
+    assert p["windowed_heads"] == 32 and p["ms_exact_path"] == 0.2433 and p["ms_long_memory"] == 0.19
     text = json.dumps({"secondary": c}, separators=(",", ":"))
     assert text.index('"prefill":{') > text.index('"hybrid_decode"') and len(text) < 1500
 

@@ -404,6 +404,24 @@ def test_prefill_window_lengths(L, chunk_log2):
     check(Sg, S_ref, T, f"chunk decay 2^{chunk_log2:.0f} state")
 
 
+@pytest.mark.parametrize("g_val,windowed", [(-0.027, True), (-0.01, False)])
+def test_prefill_long_windows(L, g_val, windowed):
+    """Windows up to the planned segment length: at T = 8192 with 32 heads
+    the plan has 8 segments of 16 chunks, so windows of up to 16 chunks are
+    checked.  g = -0.027 decays a chunk by 2^-2.49, so ten chunks meet the
+    2^-24 bound (windowed, ten warm-up chunks per segment; the gates read in
+    a second round); g = -0.01 needs 26 (the exact two-pass path).  Against
+    the oracle, all heads."""
+    T, Hv, Hk = 8192, 32, 16
+    q, k, v, g, beta, S = prefill_inputs(61, 1, T, Hv, Hk)
+    g[:] = g_val
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
+    assert L.kai_gdn_hip_prefill_windowed_heads() == (Hv if windowed else 0)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, 1, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, f"g={g_val} output")
+    check(Sg, S_ref, T, f"g={g_val} state")
+
+
 def test_prefill_windowed_f16_state(L):
     """The fp16-state variant runs windowed too (its initial state read once,
     its final state narrowed once)."""
