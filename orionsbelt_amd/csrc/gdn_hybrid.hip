@@ -198,6 +198,96 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     else Kc[((size_t)b * Hkv + (slot - Hq)) * Tmax * 256 + kv_tiled_offset(p, d)] = o;  // K is tiled
 }
 
+// The attention prologue of a prefill, eight rows per wave: block (32 rows,
+// slot), 4 waves.  Lane l holds dims l + 64 c (c = 0..3) of a row, so each
+// norm sums as block_sum does (one butterfly per 64 dims, then (s0 + s1) +
+// (s2 + s3)) and the per-element arithmetic is attn_prologue_kernel's; a
+// wave keeps its rows' loads in flight together (one row per 256-thread
+// block left every block waiting on one load), and the transposed V copy
+// takes 8 positions of a dim per 16-byte store.  Row t is position t of
+// sequence seq; V^T positions past T in the last group are written as 0.
+constexpr int kApRows = 8;
+__global__ __launch_bounds__(256) void attn_prologue_rows_kernel(
+    const float *__restrict__ qg, const float *__restrict__ kx, const float *__restrict__ vx,
+    const float *__restrict__ q_norm, const float *__restrict__ k_norm, uint16_t *__restrict__ q16,
+    uint16_t *__restrict__ Kc, uint16_t *__restrict__ Vc, int Hq, int Hkv, int Tmax, int T, int seq, float theta,
+    float eps, uint16_t *__restrict__ vT, int Tv) {
+    const int slot = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = ((int)blockIdx.x * 4 + wave) * kApRows;
+    if (r0 >= T) return;  // the whole wave
+    const int nr = min(kApRows, T - r0);
+    if (slot >= Hq + Hkv) {  // value head: the cache, and the transposed copy
+        const int kv = slot - Hq - Hkv;
+        uint16_t v[kApRows][4];
+#pragma unroll
+        for (int j = 0; j < kApRows; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                v[j][c] = j < nr ? f32_to_f16_rne(vx[((size_t)(r0 + j) * Hkv + kv) * 256 + 64 * c + lane]) : 0;
+#pragma unroll
+        for (int j = 0; j < kApRows; ++j)
+            if (j < nr)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    Vc[(((size_t)seq * Hkv + kv) * Tmax + r0 + j) * 256 + 64 * c + lane] = v[j][c];
+        if (vT) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint4 w;
+                w.x = (uint32_t)v[0][c] | ((uint32_t)v[1][c] << 16);
+                w.y = (uint32_t)v[2][c] | ((uint32_t)v[3][c] << 16);
+                w.z = (uint32_t)v[4][c] | ((uint32_t)v[5][c] << 16);
+                w.w = (uint32_t)v[6][c] | ((uint32_t)v[7][c] << 16);
+                *reinterpret_cast<uint4 *>(vT + ((size_t)kv * 256 + 64 * c + lane) * Tv + r0) = w;
+            }
+        }
+        return;
+    }
+    const bool is_q = slot < Hq;
+    const float *wn = is_q ? q_norm : k_norm;
+    float w1[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w1[c] = 1.0f + wn[64 * c + lane];
+    float x[kApRows][4];
+#pragma unroll
+    for (int j = 0; j < kApRows; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            x[j][c] = j >= nr ? 0.f
+                      : is_q ? qg[((size_t)(r0 + j) * Hq + slot) * 512 + 64 * c + lane]
+                             : kx[((size_t)(r0 + j) * Hkv + (slot - Hq)) * 256 + 64 * c + lane];
+    // rotary frequency of dim lane (< 64): rotate_half pairs it with lane ^ 32
+    const float inv_freq = 1.0f / powf(theta, (float)(2 * (lane & 31)) / 64.0f);
+#pragma unroll
+    for (int j = 0; j < kApRows; ++j) {
+        if (j >= nr) break;
+        float r[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float xx = x[j][c] * x[j][c];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) xx += __shfl_xor(xx, o);
+            r[c] = xx;
+        }
+        const float inv = 1.0f / sqrtf(((r[0] + r[1]) + (r[2] + r[3])) / 256.0f + eps);
+        float y[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = f16_to_f32(f32_to_f16_rne(x[j][c] * inv * w1[c]));
+        const int p = r0 + j;
+        const float f = inv_freq * (float)p;
+        const float cs = cosf(f), sn = sinf(f);
+        const float other = __shfl_xor(y[0], 32);
+        y[0] = lane < 32 ? y[0] * cs - other * sn : y[0] * cs + other * sn;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint16_t o = f32_to_f16_rne(y[c]);
+            const int d = 64 * c + lane;
+            if (is_q) q16[((size_t)p * Hq + slot) * 256 + d] = o;
+            else Kc[((size_t)seq * Hkv + (slot - Hq)) * Tmax * 256 + kv_tiled_offset(p, d)] = o;
+        }
+    }
+}
+
 // The GDN output's gated RMSNorm for the prefill (the decode step's
 // step 4 in gdn_step_fused_kernel, on the prefill's bf16 output): rows of
 // 128, o bf16 [rows][128], z fp32 [rows][128] -> out16 fp16 =
@@ -835,9 +925,9 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
             const int nq = Hq * 512, nkv = Hkv * 256;
             TRY(w8p(p.x16, H, L.in, T, segments({{p.qkv, nq, nq}, {p.kx, nkv, nq + nkv}, {p.vx, nkv, nq + 2 * nkv}}),
                     st));
-            attn_prologue_kernel<<<dim3(T, Hq + 2 * Hkv), 256, 0, st>>>(p.qkv, p.kx, p.vx, L.q_norm, L.k_norm, p.q16,
-                                                                        L.Kc, L.Vc, Hq, Hkv, m->tmax, b, 0,
-                                                                        c.rope_theta, c.rms_eps, p.vT, p.tv);
+            attn_prologue_rows_kernel<<<dim3((T + 4 * kApRows - 1) / (4 * kApRows), Hq + 2 * Hkv), 256, 0, st>>>(
+                p.qkv, p.kx, p.vx, L.q_norm, L.k_norm, p.q16, L.Kc, L.Vc, Hq, Hkv, m->tmax, T, b, c.rope_theta,
+                c.rms_eps, p.vT, p.tv);
             TRY(hipGetLastError());
             const size_t kvrow = (size_t)b * Hkv * m->tmax * 256;
             TRY(launch_attn_prefill(p.q16, L.Kc + kvrow, p.vT, p.qkv + 256, nq, p.x16, T, Hq, Hkv, m->tmax, p.tv,
