@@ -404,15 +404,16 @@ def test_prefill_window_lengths(L, chunk_log2):
     check(Sg, S_ref, T, f"chunk decay 2^{chunk_log2:.0f} state")
 
 
-@pytest.mark.parametrize("g_val,windowed", [(-0.027, True), (-0.01, False)])
-def test_prefill_long_windows(L, g_val, windowed):
-    """Windows up to the planned segment length: at T = 8192 with 32 heads
-    the plan has 8 segments of 16 chunks, so windows of up to 16 chunks are
-    checked.  g = -0.027 decays a chunk by 2^-2.49, so ten chunks meet the
-    2^-24 bound (windowed, ten warm-up chunks per segment; the gates read in
-    a second round); g = -0.01 needs 26 (the exact two-pass path).  Against
-    the oracle, all heads."""
-    T, Hv, Hk = 8192, 32, 16
+@pytest.mark.parametrize("T,g_val,windowed", [(8192, -0.027, True), (8192, -0.01, False), (16384, -0.01, True)])
+def test_prefill_long_windows(L, T, g_val, windowed):
+    """Windows up to the planned segment length: with 32 heads the plan has
+    8 segments, of 16 chunks at T = 8192 and 32 at T = 16384, and windows
+    of up to that many chunks are checked.  g = -0.027 decays a chunk by
+    2^-2.49, so ten chunks meet the 2^-24 bound (windowed, ten warm-up
+    chunks per segment; the gates read in a second round); g = -0.01 needs
+    26: the exact two-pass path at T = 8192, 26-chunk windows at T = 16384
+    (the bench's long-memory line).  Against the oracle, all heads."""
+    Hv, Hk = 32, 16
     q, k, v, g, beta, S = prefill_inputs(61, 1, T, Hv, Hk)
     g[:] = g_val
     o, Sg = gpu_prefill(L, q, k, v, g, beta, S)
