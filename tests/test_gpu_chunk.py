@@ -213,6 +213,41 @@ def test_prefill_repeated_keys_at_the_norm_bound(L, beta_v):
     check(Sg, S_ref, 256, f"norm-bound beta={beta_v} state")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_random_shapes(L, seed):
+    """Seeded random shapes and gate regimes against the oracle: batch 1-3,
+    1-2 value heads per key head, ragged T, fp32 or fp16 state, and gates
+    that take the windowed path, the exact path, or both within one call
+    (every other head slow).  Each case prints its shape and how many heads
+    ran windowed."""
+    rng = np.random.default_rng(seed)
+    B = int(rng.choice([1, 1, 2, 3]))
+    Hk = int(rng.choice([1, 2, 4, 8, 16]))
+    Hv = Hk * int(rng.choice([1, 2]))
+    T = int(rng.integers(1, 6000 if B * Hv <= 8 else 2500))
+    regime = ["base", "weak", "slow", "strong", "mixed", "perhead"][seed % 6]
+    q, k, v, g, beta, S = prefill_inputs(2000 + seed, B, T, Hv, Hk)
+    if regime == "weak":
+        g[:] = -0.003
+    elif regime == "slow":
+        g[:] = -float(rng.uniform(0.008, 0.05))
+    elif regime == "strong":
+        g[:] = -1.0
+    elif regime == "mixed":
+        g[:] = np.where((np.arange(T) // 64) % 2 == 0, -0.6, -0.02)[None, :, None]
+    elif regime == "perhead":
+        g[:] = np.where(np.arange(Hv) % 2 == 0, -0.005, -0.4)[None, None, :]
+    f16 = seed % 4 == 3
+    if f16:
+        S = S.astype(np.float16).astype(np.float32)
+    o, Sg = gpu_prefill(L, q, k, v, g, beta, S, f16=f16)
+    windowed = L.kai_gdn_hip_prefill_windowed_heads()
+    print(f"B={B} T={T} Hv={Hv} Hk={Hk} {regime} f16={f16}: {windowed} windowed", flush=True)
+    o_ref, S_ref = orc.chunk_gdr(q, k, v, g, beta, S, B, T, Hv, Hk, 128, 128, 64)
+    check(o, o_ref, T, f"random {seed} output")
+    check(Sg, S_ref, T, f"random {seed} state")
+
+
 def test_prefill_split_calls_bit_identical(L):
     """Calls split at chunk boundaries carry the fp32 state exactly."""
     q, k, v, g, beta, S = prefill_inputs(13, 1, 640, 4, 2)
