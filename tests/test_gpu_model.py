@@ -102,7 +102,9 @@ def gpu_gemm_tiled(L, x16, q, s, reps=1):
                                    # their four 64-channel groups; 4, 8 and 12 k steps end its
                                    # three-step buffer ring after its first, second and third slot)
                                    (1000, 12352, 2560), (513, 2560, 9216), (600, 192, 512),
-                                   (2048, 10240, 2560), (520, 64, 256), (777, 320, 768)])
+                                   (2048, 10240, 2560), (520, 64, 256), (777, 320, 768),
+                                   # 16 and 32 row blocks
+                                   (4096, 320, 768), (8192, 192, 512)])
 def test_w8a16_gemm_tiled_vs_oracle(L, M, N, K):
     """The tiled-weight GEMM (the hybrid loop's): against the oracle at the
     row-major GEMM's bar, deterministic over calls that share one workspace
