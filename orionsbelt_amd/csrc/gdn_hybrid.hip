@@ -455,7 +455,7 @@ struct kai_gdn_hybrid {
     // small batches: the residual stream alternates between h and h2, and
     // the next matrix normalises its own input from the pending branch
     float *h2 = nullptr, *hcur = nullptr, *hnext = nullptr;
-    const float *pend_add = nullptr, *pend_w = nullptr;
+    const float *pend_w = nullptr;
     float *qkv = nullptr, *zb = nullptr, *ab = nullptr, *bb = nullptr;
     float *qg = nullptr, *kx = nullptr, *vx = nullptr, *logits = nullptr;
     int32_t *next = nullptr;
@@ -624,43 +624,44 @@ hipError_t gemm_to(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *y,
     return gemm(m, x, w, segments({{y, ld, w.N}}), st);
 }
 
-// Up to this many sequences, the matrices that read the residual stream's
-// norm (the in-projections, gate|up, lm_head) form it themselves: every
-// block adds the pending branch and normalises the row into LDS while its
-// first weights are in flight (W8Out::nin_*).  That replaces the norm
-// kernel, and the residual add at the end of the branch matrices, at no
-// cost to the reading matrix.  Above, one block per row in a kernel of its
-// own is faster than every block normalising every row.
+// At batch 1 the matrices that read the residual stream's norm (the
+// in-projections, gate|up, lm_head) form it themselves: every block
+// normalises the row into LDS while its weights are in flight
+// (W8Out::nin_*), and the branch matrix before them adds its branch to the
+// residual stream in its epilogue (W8Out::add_in).  That replaces the norm
+// kernel.  From batch 2, one block per row in a kernel of its own is faster
+// than every block normalising every row; both forms compute the same sums
+// in the same order, so a sequence's logits do not depend on the batch.
 bool norm_in(const kai_gdn_hybrid *m) { return m->batch <= kW8NormInRows && m->cfg.hidden <= kW8NormInMaxK; }
 
 // d = x W^T (the branch); h += d; x16 = fp16(rmsnorm(h) * (1 + norm_w)),
-// or, for small batches, the add and the norm left to the next matrix
+// or, at batch 1, h' = h + d from the matrix's epilogue and the norm left
+// to the next matrix
 hipError_t gemm_addnorm(kai_gdn_hybrid *m, const uint16_t *x, const Mat &w, float *d, const float *norm_w,
                         hipStream_t st) {
     const int B = m->batch, H = m->cfg.hidden;
-    TRY(gemm_to(m, x, w, d, H, st));
     if (norm_in(m)) {
-        m->pend_add = d;
+        W8Out o = segments({{m->hnext, H, w.N}});
+        o.add_in = m->hcur;
+        o.add_ld = H;
+        TRY(gemm(m, x, w, o, st));
+        std::swap(m->hcur, m->hnext);
         m->pend_w = norm_w;
         return hipSuccess;
     }
+    TRY(gemm_to(m, x, w, d, H, st));
     addnorm_kernel<<<B, 256, 0, st>>>(m->h, d, norm_w, m->x16, H, m->cfg.rms_eps);
     return hipGetLastError();
 }
 
-// o = norm(h) W^T: from x16, or, for small batches, normalising the
-// residual stream (plus the pending branch) in the matrix's own blocks
+// o = norm(h) W^T: from x16, or, at batch 1, normalising the residual
+// stream in the matrix's own blocks
 hipError_t gemm_in(kai_gdn_hybrid *m, const Mat &w, W8Out o, hipStream_t st) {
     if (!norm_in(m)) return gemm(m, m->x16, w, o, st);
     o.nin_h = m->hcur;
-    o.nin_add = m->pend_add;
-    o.nin_hout = m->pend_add ? m->hnext : nullptr;
     o.nin_w = m->pend_w;
     o.nin_eps = m->cfg.rms_eps;
-    TRY(gemm(m, nullptr, w, o, st));
-    if (m->pend_add) std::swap(m->hcur, m->hnext);
-    m->pend_add = nullptr;
-    return hipSuccess;
+    return gemm(m, nullptr, w, o, st);
 }
 
 hipError_t build(kai_gdn_hybrid *m, uint64_t seed) {
@@ -813,7 +814,6 @@ hipError_t step(kai_gdn_hybrid *m, const int32_t *tokens, int32_t *next, float *
     // final norm after the last layer
     m->hcur = m->h;
     m->hnext = m->h2;
-    m->pend_add = nullptr;
     m->pend_w = m->layers[0].ln_in;
     if (!norm_in(m)) {
         addnorm_kernel<<<B, 256, 0, st>>>(m->h, nullptr, m->layers[0].ln_in, m->x16, H, c.rms_eps);

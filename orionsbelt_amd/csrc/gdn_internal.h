@@ -159,8 +159,12 @@ struct W8Out {
     float *nin_hout;
     const float *nin_w;
     float nin_eps;
+    // Residual add in the epilogue (kW8Segments with one segment):
+    // seg[0].dst[m][n] = add_in[m * add_ld + n] + y[m][n].
+    const float *add_in;
+    int add_ld;
 };
-constexpr int kW8NormInRows = 2;
+constexpr int kW8NormInRows = 1;
 constexpr int kW8NormInMaxK = 4096;
 // Launch shape: waves per block (4 or 8), 64-k steps in flight per wave (1,
 // 2 or 4), k-splits across blocks (0: chosen by w8f_shape).

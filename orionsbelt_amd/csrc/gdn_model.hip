@@ -349,7 +349,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
         }
     }
     // epilogue (wave j, tile j)
-    const f32x4_t y = t * *reinterpret_cast<const f32x4_t *>(scale + n);
+    f32x4_t y = t * *reinterpret_cast<const f32x4_t *>(scale + n);
     if (out.mode == kW8SwiGLU) {
         f32x4_t up;
 #pragma unroll
@@ -381,6 +381,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8f_kernel(const uint16_t *__restr
                 dst = out.seg[q].dst;
                 ld = out.seg[q].ld;
             }
+        if (out.add_in) y = *reinterpret_cast<const f32x4_t *>(out.add_in + (size_t)r * out.add_ld + n) + y;
         *reinterpret_cast<f32x4_t *>(dst + (size_t)r * ld + (n - nb)) = y;
     }
 }
@@ -432,7 +433,213 @@ __global__ __launch_bounds__(64 * WAVES) void w8n_kernel(const uint16_t *__restr
     const int n = 16 * t + 4 * g;  // C lane (g, r): channels n .. n+3 of batch row r
     if (row_ok && n < out.seg[0].n_end) {
         y = y * *reinterpret_cast<const f32x4_t *>(scale + n);
+        if (out.add_in) y = *reinterpret_cast<const f32x4_t *>(out.add_in + (size_t)r * out.add_ld + n) + y;
         *reinterpret_cast<f32x4_t *>(out.seg[0].dst + (size_t)r * out.seg[0].ld + n) = y;
+    }
+}
+
+// The decode GEMM at batch <= kW8vRows: one 16-channel tile per block, WPT
+// waves over k, each wave NS consecutive 64-k steps (WPT * NS = K / 64).
+// The block's input reaches LDS before any weight is requested: the
+// activation rows (the block's threads copy x[M][K] in 16-byte pieces), or,
+// for NR = M <= kW8NormInRows rows with W8Out::nin_h, the loads of the
+// residual norm's inputs, whose arithmetic finishes after the weights are
+// requested.  Vector loads complete in issue order, so the input lands
+// first and the norm runs while the weights stream.  Every weight step of
+// a wave is requested up front, only the lanes of real rows read the input
+// from LDS, and the kernel stays near 64 VGPRs, so that several blocks
+// share a CU (the form that held 222 VGPRs ran at half the rate).  Each
+// wave sums its steps in order (two MFMAs per step) and the tile's waves
+// are added in wave order, the same for every M <= kW8vRows.  Epilogues as
+// in w8f_kernel (segments, SwiGLU on the interleaved rows).
+constexpr int kW8vRows = 3;
+constexpr int kW8vPieces = 4;  // 16-byte pieces of x per thread: M K <= 32 * threads
+constexpr int kW8vNormJ = 3;   // norm pieces per thread (of 256): K <= 3072
+
+// The first half of w8f_norm_input's work for NR rows: threads 0..255
+// request their pieces of h, add and w; w8v_norm_finish does the
+// arithmetic.  Pieces past K / 4 are not requested and not used.
+template <int NR> struct NormPieces {
+    f32x4_t h[NR][kW8vNormJ], a[NR][kW8vNormJ], w[kW8vNormJ];
+};
+template <int NR> GDN_DEV void w8v_norm_load(const W8Out &out, int K, NormPieces<NR> &p) {
+    const int n4 = K / 4, tid = threadIdx.x;
+    if (tid >= 256) return;
+#pragma unroll
+    for (int j = 0; j < kW8vNormJ; ++j) {
+        const int i = tid + 256 * j;
+        if (i < n4) {
+            const float4 wv = reinterpret_cast<const float4 *>(out.nin_w)[i];
+            p.w[j] = f32x4_t{wv.x, wv.y, wv.z, wv.w};
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NR; ++b)
+#pragma unroll
+        for (int j = 0; j < kW8vNormJ; ++j) {
+            const int i = tid + 256 * j;
+            if (i < n4) {
+                const float4 hv = reinterpret_cast<const float4 *>(out.nin_h + (size_t)b * K)[i];
+                p.h[b][j] = f32x4_t{hv.x, hv.y, hv.z, hv.w};
+                if (out.nin_add) {
+                    const float4 dv = reinterpret_cast<const float4 *>(out.nin_add + (size_t)b * K)[i];
+                    p.a[b][j] = f32x4_t{dv.x, dv.y, dv.z, dv.w};
+                }
+            }
+        }
+}
+// w8f_norm_input's arithmetic on pieces already requested (the same sums in
+// the same order); every thread of the block calls it (barriers).
+template <int NR>
+GDN_DEV void w8v_norm_finish(const W8Out &out, int K, NormPieces<NR> &p, uint16_t *xs, float *s_ss, bool writer) {
+    const int n4 = K / 4, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+        f32x4_t x[kW8vNormJ];
+        float ss = 0.f;
+        if (tid < 256) {
+#pragma unroll
+            for (int j = 0; j < kW8vNormJ; ++j) {
+                const int i = tid + 256 * j;
+                if (i < n4) {
+                    x[j] = p.h[b][j];
+                    if (out.nin_add) {
+                        x[j] += p.a[b][j];
+                        if (writer)
+                            reinterpret_cast<float4 *>(out.nin_hout + (size_t)b * K)[i] =
+                                make_float4(x[j][0], x[j][1], x[j][2], x[j][3]);
+                    }
+                    ss += x[j][0] * x[j][0] + x[j][1] * x[j][1] + x[j][2] * x[j][2] + x[j][3] * x[j][3];
+                }
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            if (lane == 0) s_ss[wave] = ss;
+        }
+        __syncthreads();
+        const float inv = 1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)K + out.nin_eps);
+        __syncthreads();  // s_ss is rewritten by the next row
+        if (tid < 256) {
+#pragma unroll
+            for (int j = 0; j < kW8vNormJ; ++j) {
+                const int i = tid + 256 * j;
+                if (i < n4) {
+                    const f32x4_t wv = p.w[j];
+                    uint2 o;
+                    o.x = (uint32_t)f32_to_f16_rne(x[j][0] * inv * (1.0f + wv[0])) |
+                          ((uint32_t)f32_to_f16_rne(x[j][1] * inv * (1.0f + wv[1])) << 16);
+                    o.y = (uint32_t)f32_to_f16_rne(x[j][2] * inv * (1.0f + wv[2])) |
+                          ((uint32_t)f32_to_f16_rne(x[j][3] * inv * (1.0f + wv[3])) << 16);
+                    *reinterpret_cast<uint2 *>(&xs[(size_t)b * K + 4 * i]) = o;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// NR = 0: input x[M][K]; NR = M (1 or 2): the normalised rows of W8Out::nin_h
+template <int WPT, int NS, int NR>
+__global__ __launch_bounds__(64 * WPT) void w8v_kernel(const uint16_t *__restrict__ x, const int8_t *__restrict__ W,
+                                                       const float *__restrict__ scale, int M, int N, int K,
+                                                       W8Out out) {
+    __shared__ f32x4_t red[WPT][64];
+    __shared__ float s_ss[4];
+    extern __shared__ __align__(16) uint16_t xs[];  // the block's input rows [M][K] fp16 (dynamic)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const int t = blockIdx.x;        // 16-channel tile
+    const int c = t >> 2, j = t & 3;  // its 64-channel group and place in the group
+    const int steps = K / kKStep;     // WPT * NS
+    const int s0 = wave * NS;         // this wave's first 64-k step
+    const bool row_ok = r < M;
+    // 1. the input's loads, ahead of every weight load
+    NormPieces<NR == 0 ? 1 : NR> np;
+    u32x4_t xin[kW8vPieces];
+    const int npieces = M * K / 8;  // 16-byte pieces of x
+    if constexpr (NR > 0) {
+        w8v_norm_load<NR>(out, K, np);
+    } else {
+#pragma unroll
+        for (int q = 0; q < kW8vPieces; ++q) {
+            const int i = threadIdx.x + q * 64 * WPT;
+            if (i < npieces) xin[q] = reinterpret_cast<const u32x4_t *>(x)[i];
+        }
+    }
+    // 2. every weight step of this wave
+    const int8_t *wp = W + ((size_t)c * steps + s0) * 4096 + j * 1024 + lane * 16;
+    u32x4_t wv[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+        wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(wp + (size_t)i * 4096));
+    // 3. the input rows into LDS
+    if constexpr (NR > 0) {
+        w8v_norm_finish<NR>(out, K, np, xs, s_ss, blockIdx.x == 0);
+    } else {
+#pragma unroll
+        for (int q = 0; q < kW8vPieces; ++q) {
+            const int i = threadIdx.x + q * 64 * WPT;
+            if (i < npieces) reinterpret_cast<u32x4_t *>(xs)[i] = xin[q];
+        }
+        __syncthreads();
+    }
+    // 4. the tile: lane (g, r) holds row r's k = 64 s + 16 g .. +15; lanes
+    // of rows past M read nothing and multiply zeros
+    const uint16_t *xp = &xs[(size_t)(row_ok ? r : 0) * K + s0 * kKStep + 16 * g];
+    f32x4_t acc = zero4();
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        u32x4_t xa = u32x4_t{0u, 0u, 0u, 0u}, xb = xa;
+        if (row_ok) {
+            xa = *reinterpret_cast<const u32x4_t *>(xp + i * kKStep);
+            xb = *reinterpret_cast<const u32x4_t *>(xp + i * kKStep + 8);
+        }
+        f16x8_t w0, w1;
+        i8x16_to_f16(wv[i], w0, w1);
+        acc = mfma_f16(w0, __builtin_bit_cast(f16x8_t, xa), acc);
+        acc = mfma_f16(w1, __builtin_bit_cast(f16x8_t, xb), acc);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4_t y = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < WPT; ++w) y += red[w][lane];
+    const int n = 16 * t + 4 * g;  // C lane (g, r): channels n .. n+3 of batch row r
+    y = y * *reinterpret_cast<const f32x4_t *>(scale + n);
+    if (out.mode == kW8SwiGLU) {
+        f32x4_t up;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) up[e] = __shfl_xor(y[e], 32);
+        if (g < 2 && row_ok) {
+            uint32_t h[2];
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const float a = y[e] / (1.0f + expf(-y[e])) * up[e];
+                const float b = y[e + 1] / (1.0f + expf(-y[e + 1])) * up[e + 1];
+                h[e / 2] = (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+            }
+            const int cc = 8 * t + 4 * g;
+            *reinterpret_cast<uint2 *>(out.x16 + (size_t)r * (N / 2) + cc) = make_uint2(h[0], h[1]);
+        }
+    } else if (row_ok && n < out.seg[out.nseg - 1].n_end) {  // channels past the last segment: padding
+        int sgi = 0, nb = 0;
+#pragma unroll
+        for (int q = 0; q < kW8MaxSegs - 1; ++q)
+            if (q < out.nseg - 1 && n >= out.seg[q].n_end) {
+                sgi = q + 1;
+                nb = out.seg[q].n_end;
+            }
+        float *dst = out.seg[0].dst;
+        int ld = out.seg[0].ld;
+#pragma unroll
+        for (int q = 1; q < kW8MaxSegs; ++q)
+            if (q == sgi) {
+                dst = out.seg[q].dst;
+                ld = out.seg[q].ld;
+            }
+        if (out.add_in) y = *reinterpret_cast<const f32x4_t *>(out.add_in + (size_t)r * out.add_ld + n) + y;
+        *reinterpret_cast<f32x4_t *>(dst + (size_t)r * ld + (n - nb)) = y;
     }
 }
 
@@ -466,9 +673,43 @@ hipError_t launch_w8f_tile(const int8_t *src, int8_t *dst, int N, int K, hipStre
     return hipGetLastError();
 }
 
+// The small-batch form's launch: hipErrorNotSupported where it has no
+// instantiation for the shape (the caller then takes another form).  Eight
+// waves per tile at K = 2560 (the hidden size: in-projections, gate|up),
+// sixteen at K = 4096 and 9216 (out_proj, o_proj, down: 160 tiles, fewer
+// blocks than CUs, so each block splits k finer).  The LM head (9496 tiles)
+// keeps w8f_kernel, whose 64-channel blocks form the norm a quarter as often.
+hipError_t launch_w8v(const uint16_t *x, const int8_t *W, const float *scale, int M, int N, int K,
+                      const W8Out &out, hipStream_t st) {
+    const int steps = K / kKStep, tiles = N / 16;
+    if (M > kW8vRows || N % kW8fGroup || K % kKStep || tiles > 2048) return hipErrorNotSupported;
+    const size_t lds = (size_t)M * K * 2;
+    if (out.nin_h) {
+        if (steps != 40 || K / 4 > 256 * kW8vNormJ || M != 1) return hipErrorNotSupported;
+        w8v_kernel<8, 5, 1><<<tiles, 512, lds, st>>>(x, W, scale, M, N, K, out);
+        return hipGetLastError();
+    }
+    const int wpt = steps == 40 ? 8 : 16;
+    if ((size_t)M * K / 8 > (size_t)kW8vPieces * 64 * wpt) return hipErrorNotSupported;
+    if (steps == 40) w8v_kernel<8, 5, 0><<<tiles, 512, lds, st>>>(x, W, scale, M, N, K, out);
+    else if (steps == 64) w8v_kernel<16, 4, 0><<<tiles, 1024, lds, st>>>(x, W, scale, M, N, K, out);
+    else if (steps == 144) w8v_kernel<16, 9, 0><<<tiles, 1024, lds, st>>>(x, W, scale, M, N, K, out);
+    else return hipErrorNotSupported;
+    return hipGetLastError();
+}
+
 hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, int M, int N, int K,
                       const W8Out &out, float *part, uint32_t *cnt, hipStream_t st, W8fShape sh) {
     if (M == 0 || N == 0) return hipSuccess;
+    if (out.nin_h && (M > kW8NormInRows || K > kW8NormInMaxK || K % 4 || !out.nin_w ||
+                      (out.nin_add && !out.nin_hout)))
+        return hipErrorInvalidValue;
+    if (out.add_in && (out.mode != kW8Segments || out.nseg != 1)) return hipErrorInvalidValue;
+    // batch <= kW8vRows: the small-batch form where it has one for the shape
+    if (sh.splits == 0) {
+        const hipError_t e = launch_w8v(x, W, scale, M, N, K, out, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     // the narrow single-output matrices: one tile per block, no k-split
     // (w8n_kernel), when no launch shape is asked for
     if (sh.splits == 0 && out.mode == kW8Segments && out.nseg == 1 && !out.nin_h && N % kW8fGroup == 0 &&
@@ -481,9 +722,6 @@ hipError_t launch_w8f(const uint16_t *x, const int8_t *W, const float *scale, in
     const int S = sh.splits;
     if (M > 16 || N % kW8fGroup != 0 || K % (S * sh.waves * sh.depth * kKStep) != 0) return hipErrorInvalidValue;
     if (S > 1 && (!part || !cnt || (size_t)S * M * N * 4 > 0x7FFFFFFFull)) return hipErrorInvalidValue;
-    if (out.nin_h && (M > kW8NormInRows || K > kW8NormInMaxK || K % 4 || !out.nin_w ||
-                      (out.nin_add && !out.nin_hout)))
-        return hipErrorInvalidValue;
     const dim3 grid(N / kW8fGroup, S);
 #define W8F_CASE(WV, DP)                                                                                  \
     if (sh.waves == WV && sh.depth == DP) {                                                                \

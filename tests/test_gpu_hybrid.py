@@ -204,15 +204,18 @@ def oracle_config(cfg):
 
 
 def test_hybrid_qwen35_4b_vs_oracle(hb):
-    """The full Qwen3.5-4B shape (hidden 2560, the 9216-wide MLP with its
-    split-k down matrix and fused residual norm at batch <= 2, the separate
-    norm kernel at batch 3, the 151936-wide LM head) against the CPU model,
-    at batch 2 and batch 3 after a drawn 8192-token context, two steps each."""
-    cfg = hb.qwen35_4b(3, 8200)
+    """The full Qwen3.5-4B shape (hidden 2560, the 9216-wide MLP, the
+    151936-wide LM head) against the CPU model after a drawn 8192-token
+    context, two steps each: batch 1 (the small-batch matrices with the
+    residual add in the branch matrices' epilogues and the norm formed in
+    the reading matrices) and batch 4 (the separate norm kernel, the
+    split-k down matrix).  Batches 2 and 3 give batch 1's rows bit for bit
+    (test_hybrid_qwen35_4b_rows_same_at_batch_1_2_3)."""
+    cfg = hb.qwen35_4b(4, 8200)
     gm = hb.HybridModel(cfg, 2468)
     om = orc.HybridModel(oracle_config(cfg), 2468)
     rs = np.random.RandomState(5)
-    for B in (2, 3):
+    for B in (1, 4):
         gm.reset(B, 8192, 31)
         om.reset(B, 8192, 31)
         for t in range(2):
@@ -221,6 +224,35 @@ def test_hybrid_qwen35_4b_vs_oracle(hb):
             _, olg = om.step(tok)
             assert_close(lg, olg, f"4B shape B={B} ctx 8192 step {t}", cfg.layers)
             assert_greedy(nxt, lg, olg, cfg.layers)
+    gm.close()
+
+
+def test_hybrid_qwen35_4b_rows_same_at_batch_1_2_3(hb):
+    """At the 4B shape a sequence's logits do not depend on the batch: batch
+    1 (norm formed inside the reading matrices, residual add in the branch
+    matrices' epilogues) and batches 2 and 3 (the norm kernel) give row 0
+    bit-identical logits and tokens over three steps from an empty context,
+    whatever the other rows are fed."""
+    torch = torch_mod()
+    cfg = hb.qwen35_4b(3, 64)
+    gm = hb.HybridModel(cfg, 97)
+    rs = np.random.RandomState(11)
+    toks = rs.randint(0, cfg.vocab, (3, 3)).astype(np.int32)
+    runs = []
+    for B in (1, 2, 3):
+        gm.reset(B, 0, 0)
+        run = []
+        for t in range(3):
+            nxt = empty((B,), torch.int32)
+            logits = empty((B, cfg.vocab), torch.float32)
+            gm.step(dev(toks[t, :B].copy()), nxt, logits)
+            run.append((host(nxt)[0], host(logits)[0].copy()))
+        runs.append(run)
+    for t in range(3):
+        assert np.isfinite(runs[0][t][1]).all()
+        for B in (2, 3):
+            assert np.array_equal(runs[B - 1][t][1], runs[0][t][1]), f"B={B} step {t}"
+            assert runs[B - 1][t][0] == runs[0][t][0]
     gm.close()
 
 
@@ -374,18 +406,21 @@ def test_hybrid_long_context_span_sizes_vs_oracle(hb, fixture):
 
 
 def test_hybrid_fused_and_separate_norms_agree(hb, fixture):
-    """Up to batch 2 the residual add and RMSNorm run in every block of the
-    matrices that read the norm (in-projections, gate|up, lm_head); from
-    batch 3 in a kernel of their own, with the same arithmetic in the same
-    order.  The same two sequences stepped at batch 2 and (with a third) at
-    batch 3 give bit-identical logits and greedy tokens."""
+    """At batch 1 the residual add runs in the branch matrices' epilogues and
+    the RMSNorm in every block of the matrices that read it (in-projections,
+    gate|up, lm_head); from batch 2 both run in a kernel of their own, with
+    the same arithmetic in the same order.  The same sequence stepped alone
+    and as row 0 of batch 2 and batch 3 gives bit-identical logits and
+    greedy tokens."""
     d, fields = fixture
     gm, _ = models(hb, fields, int(d["seed"]), max_batch=3)
     tokens = d["tokens"]
+    gm.reset(1, 0, 0)
+    one = [step(gm, tokens[:1, t], fields["vocab"]) for t in range(6)]
     gm.reset(2, 0, 0)
     two = [step(gm, tokens[:, t], fields["vocab"]) for t in range(6)]
     gm.reset(3, 0, 0)
     three = [step(gm, np.concatenate([tokens[:, t], tokens[:1, t]]), fields["vocab"]) for t in range(6)]
-    for t, ((n2, l2), (n3, l3)) in enumerate(zip(two, three)):
-        assert np.array_equal(l3[:2], l2), f"step {t}"
-        assert np.array_equal(n3[:2], n2), f"step {t}"
+    for t, ((n1, l1), (n2, l2), (n3, l3)) in enumerate(zip(one, two, three)):
+        assert np.array_equal(l2[:1], l1) and np.array_equal(l3[:1], l1), f"step {t}"
+        assert n2[0] == n1[0] and n3[0] == n1[0], f"step {t}"

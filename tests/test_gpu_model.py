@@ -95,6 +95,10 @@ def gpu_gemm_tiled(L, x16, q, s, reps=1):
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (5, 2560, 4096), (16, 12352, 2560), (3, 2560, 9216),
                                    (16, 1024, 512), (1, 18432, 2560),
+                                   # M <= 3: the small-batch form (8 waves per tile at K = 2560,
+                                   # 16 at 4096 and 9216)
+                                   (1, 2560, 4096), (2, 12352, 2560), (3, 640, 2560), (1, 2560, 9216),
+                                   (2, 10240, 2560), (3, 2560, 4096),
                                    # M > 16: the prefill GEMM (128-row blocks: ragged row tails,
                                    # a half channel block when N % 128 == 64, the 4B shapes)
                                    (17, 64, 256), (100, 192, 512), (300, 2560, 9216), (129, 18432, 2560),
