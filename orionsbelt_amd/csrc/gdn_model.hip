@@ -442,9 +442,9 @@ __global__ __launch_bounds__(64 * WAVES) void w8n_kernel(const uint16_t *__restr
 // waves over k, each wave NS consecutive 64-k steps (WPT * NS = K / 64).
 // The block's input reaches LDS before any weight is requested: the
 // activation rows (the block's threads copy x[M][K] in 16-byte pieces), or,
-// for NR = M <= kW8NormInRows rows with W8Out::nin_h, the loads of the
-// residual norm's inputs, whose arithmetic finishes after the weights are
-// requested.  Vector loads complete in issue order, so the input lands
+// for NR = M <= kW8NormInRows rows with W8Out::nin_h (and no pending
+// branch), the loads of the residual norm's inputs, whose arithmetic
+// finishes after the weights are requested.  Vector loads complete in issue order, so the input lands
 // first and the norm runs while the weights stream.  Every weight step of
 // a wave is requested up front, only the lanes of real rows read the input
 // from LDS, and the kernel stays near 64 VGPRs, so that several blocks
@@ -456,11 +456,13 @@ constexpr int kW8vRows = 3;
 constexpr int kW8vPieces = 4;  // 16-byte pieces of x per thread: M K <= 32 * threads
 constexpr int kW8vNormJ = 3;   // norm pieces per thread (of 256): K <= 3072
 
-// The first half of w8f_norm_input's work for NR rows: threads 0..255
-// request their pieces of h, add and w; w8v_norm_finish does the
-// arithmetic.  Pieces past K / 4 are not requested and not used.
+// The first half of w8f_norm_input's work for NR rows without a pending
+// branch (W8Out::nin_add null: the branch matrix added it in its
+// epilogue): threads 0..255 request their pieces of h and w;
+// w8v_norm_finish does the arithmetic.  Pieces past K / 4 are not
+// requested and not used.
 template <int NR> struct NormPieces {
-    f32x4_t h[NR][kW8vNormJ], a[NR][kW8vNormJ], w[kW8vNormJ];
+    f32x4_t h[NR][kW8vNormJ], w[kW8vNormJ];
 };
 template <int NR> GDN_DEV void w8v_norm_load(const W8Out &out, int K, NormPieces<NR> &p) {
     const int n4 = K / 4, tid = threadIdx.x;
@@ -481,17 +483,13 @@ template <int NR> GDN_DEV void w8v_norm_load(const W8Out &out, int K, NormPieces
             if (i < n4) {
                 const float4 hv = reinterpret_cast<const float4 *>(out.nin_h + (size_t)b * K)[i];
                 p.h[b][j] = f32x4_t{hv.x, hv.y, hv.z, hv.w};
-                if (out.nin_add) {
-                    const float4 dv = reinterpret_cast<const float4 *>(out.nin_add + (size_t)b * K)[i];
-                    p.a[b][j] = f32x4_t{dv.x, dv.y, dv.z, dv.w};
-                }
             }
         }
 }
 // w8f_norm_input's arithmetic on pieces already requested (the same sums in
 // the same order); every thread of the block calls it (barriers).
 template <int NR>
-GDN_DEV void w8v_norm_finish(const W8Out &out, int K, NormPieces<NR> &p, uint16_t *xs, float *s_ss, bool writer) {
+GDN_DEV void w8v_norm_finish(const W8Out &out, int K, NormPieces<NR> &p, uint16_t *xs, float *s_ss) {
     const int n4 = K / 4, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 #pragma unroll
     for (int b = 0; b < NR; ++b) {
@@ -503,12 +501,6 @@ GDN_DEV void w8v_norm_finish(const W8Out &out, int K, NormPieces<NR> &p, uint16_
                 const int i = tid + 256 * j;
                 if (i < n4) {
                     x[j] = p.h[b][j];
-                    if (out.nin_add) {
-                        x[j] += p.a[b][j];
-                        if (writer)
-                            reinterpret_cast<float4 *>(out.nin_hout + (size_t)b * K)[i] =
-                                make_float4(x[j][0], x[j][1], x[j][2], x[j][3]);
-                    }
                     ss += x[j][0] * x[j][0] + x[j][1] * x[j][1] + x[j][2] * x[j][2] + x[j][3] * x[j][3];
                 }
             }
@@ -574,7 +566,7 @@ __global__ __launch_bounds__(64 * WPT) void w8v_kernel(const uint16_t *__restric
         wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(wp + (size_t)i * 4096));
     // 3. the input rows into LDS
     if constexpr (NR > 0) {
-        w8v_norm_finish<NR>(out, K, np, xs, s_ss, blockIdx.x == 0);
+        w8v_norm_finish<NR>(out, K, np, xs, s_ss);
     } else {
 #pragma unroll
         for (int q = 0; q < kW8vPieces; ++q) {
@@ -685,7 +677,7 @@ hipError_t launch_w8v(const uint16_t *x, const int8_t *W, const float *scale, in
     if (M > kW8vRows || N % kW8fGroup || K % kKStep || tiles > 2048) return hipErrorNotSupported;
     const size_t lds = (size_t)M * K * 2;
     if (out.nin_h) {
-        if (steps != 40 || K / 4 > 256 * kW8vNormJ || M != 1) return hipErrorNotSupported;
+        if (steps != 40 || K / 4 > 256 * kW8vNormJ || M != 1 || out.nin_add) return hipErrorNotSupported;
         w8v_kernel<8, 5, 1><<<tiles, 512, lds, st>>>(x, W, scale, M, N, K, out);
         return hipGetLastError();
     }
