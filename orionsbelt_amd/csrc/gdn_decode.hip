@@ -239,30 +239,56 @@ __global__ __launch_bounds__(256) void gdn_step_fused_kernel(
     const int cgi = tid % TPR, rg = tid / TPR;
     const int c = cgi * 4;
     const int64_t sbase = (int64_t)bh * D * D;
-    // the state is independent of the prologue: request it first
+    // Loads in the order they are needed (vector loads complete in issue
+    // order): the conv inputs and gate scalars, the epilogue's z and norm
+    // weight (row group 0), then the 64 KB state, which streams in while the
+    // conv, the norms and the gates are formed.
+    // 1. conv + SiLU: thread t < 128 takes q channel t and v channel t,
+    //    thread t >= 128 k channel t - 128
+    struct ConvIn {
+        float4 st, wv;
+        float cur;
+    };
+    auto conv_load = [&](int64_t ch) {
+        const int64_t si = ((int64_t)b * C + ch) * 4;
+        return ConvIn{*reinterpret_cast<const float4 *>(conv_in + si), *reinterpret_cast<const float4 *>(conv_w + ch * 4),
+                      x[(int64_t)b * C + ch]};
+    };
+    auto conv = [&](int64_t ch, const ConvIn &in, bool write) {
+        const int64_t si = ((int64_t)b * C + ch) * 4;
+        float acc = in.st.y * in.wv.x + in.st.z * in.wv.y + in.st.w * in.wv.z + in.cur * in.wv.w;
+        acc = acc / (1.0f + expf(-acc));
+        if (write) *reinterpret_cast<float4 *>(conv_out + si) = make_float4(in.st.y, in.st.z, in.st.w, in.cur);
+        return acc;
+    };
+    const bool qk_writer = h % rep == 0;
+    const int64_t ch0 = tid < D ? (int64_t)kh * D + tid : (int64_t)Hk * D + (int64_t)kh * D + (tid - D);
+    const int64_t chv = (int64_t)2 * Hk * D + (int64_t)h * D + (tid & (D - 1));
+    const ConvIn in0 = conv_load(ch0);
+    ConvIn inv_;
+    if (tid < D) inv_ = conv_load(chv);
+    float ga = 0.f, gb = 0.f, gA = 0.f, gdt = 0.f;
+    if (tid == 0) {
+        ga = a_in[bh];
+        gdt = dt_bias[h];
+        gA = A_log[h];
+        gb = b_in[bh];
+    }
+    float4 zz = make_float4(0.f, 0.f, 0.f, 0.f), ww = zz;
+    if (rg == 0) {
+        zz = *reinterpret_cast<const float4 *>(z + (int64_t)bh * D + c);
+        ww = *reinterpret_cast<const float4 *>(norm_w + c);
+    }
     float4 s[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) s[i] = load_f4<true>(S + sbase + (int64_t)(rg + RG * i) * D + c);
 
-    // 1. conv + SiLU: thread t < 128 takes q channel t and v channel t,
-    //    thread t >= 128 k channel t - 128
-    auto conv = [&](int64_t ch, bool write) {
-        const int64_t si = ((int64_t)b * C + ch) * 4;
-        const float4 st = *reinterpret_cast<const float4 *>(conv_in + si);
-        const float4 wv = *reinterpret_cast<const float4 *>(conv_w + ch * 4);
-        const float cur = x[(int64_t)b * C + ch];
-        float acc = st.y * wv.x + st.z * wv.y + st.w * wv.z + cur * wv.w;
-        acc = acc / (1.0f + expf(-acc));
-        if (write) *reinterpret_cast<float4 *>(conv_out + si) = make_float4(st.y, st.z, st.w, cur);
-        return acc;
-    };
-    const bool qk_writer = h % rep == 0;
     float mine;
     if (tid < D) {
-        mine = conv((int64_t)kh * D + tid, qk_writer);
-        vs[tid] = conv((int64_t)2 * Hk * D + (int64_t)h * D + tid, true);
+        mine = conv(ch0, in0, qk_writer);
+        vs[tid] = conv(chv, inv_, true);
     } else {
-        mine = conv((int64_t)Hk * D + (int64_t)kh * D + (tid - D), qk_writer);
+        mine = conv(ch0, in0, qk_writer);
     }
     // 2. L2 norms (q: waves 0-1, k: waves 2-3) and the gates
     float ss = mine * mine;
@@ -270,10 +296,10 @@ __global__ __launch_bounds__(256) void gdn_step_fused_kernel(
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
     if (lane == 0) red_ss[wave] = ss;
     if (tid == 0) {
-        const float y = a_in[bh] + dt_bias[h];
+        const float y = ga + gdt;
         const float sp = y > 20.f ? y : log1pf(expf(y));
-        gate[0] = -expf(A_log[h]) * sp;
-        gate[1] = 1.0f / (1.0f + expf(-b_in[bh]));
+        gate[0] = -expf(gA) * sp;
+        gate[1] = 1.0f / (1.0f + expf(-gb));
     }
     __syncthreads();
     if (tid < D) qs[tid] = mine * (1.0f / sqrtf(red_ss[0] + red_ss[1] + 1e-6f)) * q_scale;
@@ -321,8 +347,6 @@ __global__ __launch_bounds__(256) void gdn_step_fused_kernel(
 #pragma unroll
     for (int o = 16; o >= 1; o >>= 1) q2 += __shfl_xor(q2, o, 32);
     const float inv = 1.0f / sqrtf(q2 / (float)D + eps);
-    const float4 zz = *reinterpret_cast<const float4 *>(z + (int64_t)bh * D + c);
-    const float4 ww = *reinterpret_cast<const float4 *>(norm_w + c);
     auto gn = [&](float ov, float zv, float wv) { return (wv * (ov * inv)) * (zv / (1.0f + expf(-zv))); };
     uint2 o;
     o.x = (uint32_t)f32_to_f16_rne(gn(o4.x, zz.x, ww.x)) | ((uint32_t)f32_to_f16_rne(gn(o4.y, zz.y, ww.y)) << 16);
