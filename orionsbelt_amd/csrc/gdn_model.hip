@@ -976,15 +976,21 @@ size_t attn_workspace_bytes(int B, int Hq, int L) {
     return (size_t)B * Hq * nspan * kAttPart * sizeof(float);
 }
 
-// Groups of 16 positions per wave.  256-position spans (G = 4), unless that
-// grid is small (under 2048 blocks) for a tiled-K cache: then the span is
-// sized so that the blocks fill 512 slots (2 per CU on 256 CUs) in one round
-// -- at B = 1 and 32K, 129 x 4 = 516 blocks of 256 positions would leave 4
-// blocks for a second round that doubles the kernel's time.
+// Groups of 16 positions per wave.  256-position spans (G = 4) for a
+// row-major K cache.  For a tiled-K cache the span is sized for a block
+// count: a grid of fewer than 2048 blocks of 256 positions fills 512 slots
+// (2 per CU on 256 CUs) in one round -- at B = 1 and 32K, 129 x 4 = 516
+// blocks of 256 positions would leave 4 blocks for a second round that
+// doubles the kernel's time -- and a larger grid is cut into about 2048
+// blocks: at B = 16 and 32K, spans of 16 groups (2112 blocks) took 356.5
+// against 381.4 us per layer with 4 groups (8256 blocks), decode and
+// combine, with 8 to 24 groups all within 364 us (longer spans read the
+// KV stream faster and leave fewer partials to combine).
 int attn_groups(int B, int Hkv, int L, bool k_tiled) {
     const long blocks256 = (long)B * Hkv * ((L + kAttSpan - 1) / kAttSpan);
-    if (!k_tiled || blocks256 >= 2048) return 4;
-    const int per_kv = max(1, 512 / (B * Hkv));
+    if (!k_tiled) return 4;
+    const int target = blocks256 >= 2048 ? 2048 : 512;
+    const int per_kv = max(1, target / (B * Hkv));
     return max(1, (L + 64 * per_kv - 1) / (64 * per_kv));
 }
 

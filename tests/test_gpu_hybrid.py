@@ -256,23 +256,27 @@ def test_hybrid_qwen35_4b_rows_same_at_batch_1_2_3(hb):
     gm.close()
 
 
-def test_hybrid_reduced_hidden_32k_context_vs_oracle(hb):
+@pytest.mark.parametrize("batch", [2, 4])
+def test_hybrid_reduced_hidden_32k_context_vs_oracle(hb, batch):
     """Attention over a 32K-position drawn context (the spans and their
     combine at the config-5 length) with the 4B head counts and a small
-    hidden size, against the CPU model: batch 2, two steps."""
+    hidden size, against the CPU model, two steps: batch 2 (a grid sized
+    to fill the GPU once) and batch 4 (over 2048 blocks of 256 positions,
+    so spans sized for about 2048 blocks: 5 groups of 16 positions per
+    wave)."""
     over = dict(layers=8, attn_every=4, hidden=512, inter=1024, vocab=2048, gdn_k_heads=16, gdn_v_heads=32,
-                attn_q_heads=16, attn_kv_heads=4, max_batch=2, max_context=32768 + 8, rope_theta=1e7,
+                attn_q_heads=16, attn_kv_heads=4, max_batch=batch, max_context=32768 + 8, rope_theta=1e7,
                 rms_eps=1e-6)
     gm = hb.HybridModel(hb.config(**over), 97)
     om = orc.HybridModel(orc.HybridConfig(*[over[n] for n, _ in orc.HybridConfig._fields_]), 97)
-    gm.reset(2, 32768, 3)
-    om.reset(2, 32768, 3)
+    gm.reset(batch, 32768, 3)
+    om.reset(batch, 32768, 3)
     rs = np.random.RandomState(6)
     for t in range(2):
-        tok = rs.randint(0, over["vocab"], 2)
+        tok = rs.randint(0, over["vocab"], batch)
         nxt, lg = step(gm, tok, over["vocab"])
         _, olg = om.step(tok)
-        assert_close(lg, olg, f"ctx 32768 step {t}")
+        assert_close(lg, olg, f"batch {batch} ctx 32768 step {t}")
         assert_greedy(nxt, lg, olg)
     assert gm.position == 32770
     gm.close()
