@@ -467,7 +467,7 @@ struct kai_gdn_hybrid {
     // prefill buffers, allocated by the first prefill for max_context rows
     struct Prefill {
         int rows = 0, tv = 0;  // capacity (positions) and the V^T row length
-        float *h = nullptr, *mix = nullptr, *qkv = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
+        float *h = nullptr, *qkv = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
         float *conv = nullptr, *g = nullptr, *beta = nullptr, *kx = nullptr, *vx = nullptr, *hist = nullptr;
         uint16_t *x16 = nullptr, *act16 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
         uint16_t *q16 = nullptr, *vT = nullptr;
@@ -851,7 +851,6 @@ hipError_t prefill_alloc(kai_gdn_hybrid *m) {
     p.tv = (int)((R + 63) / 64 * 64);
     const size_t x16w = std::max({(size_t)H, (size_t)V, (size_t)Hq * 256});
     TRY(alloc_t(m, &p.h, R * H));
-    TRY(alloc_t(m, &p.mix, R * H));
     TRY(alloc_t(m, &p.qkv, R * std::max((size_t)C, (size_t)Hq * 512)));
     TRY(alloc_t(m, &p.z, R * V));
     TRY(alloc_t(m, &p.a, R * Hv));
@@ -878,6 +877,14 @@ hipError_t prefill_alloc(kai_gdn_hybrid *m) {
 
 hipError_t w8p(const uint16_t *x, int ldx, const Mat &w, int M, const W8Out &o, hipStream_t st) {
     return launch_w8p(x, ldx, w.q, w.s, M, w.N, w.K, o, st);
+}
+// A branch matrix: h[t] += x[t] W^T for the T rows, the residual add in the
+// GEMM's epilogue (in place), so no branch array is written and read back.
+hipError_t w8p_residual(const uint16_t *x, int ldx, const Mat &w, int M, float *h, int H, hipStream_t st) {
+    W8Out o = segments({{h, H, H}});
+    o.add_in = h;
+    o.add_ld = H;
+    return w8p(x, ldx, w, M, o, st);
 }
 
 // One sequence's prompt through every layer at once: T rows of sequence b.
@@ -919,7 +926,7 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
                                                                                   c.rms_eps);
             TRY(hipGetLastError());
             TRY(mark(m, KAI_GDN_PHASE_GDN_CORE, st));
-            TRY(w8p(p.x16, V, L.out, T, segments({{p.mix, H, H}}), st));
+            TRY(w8p_residual(p.x16, V, L.out, T, p.h, H, st));
             TRY(mark(m, KAI_GDN_PHASE_GDN_OPROJ, st));
         } else {
             const int nq = Hq * 512, nkv = Hkv * 256;
@@ -932,15 +939,15 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
             const size_t kvrow = (size_t)b * Hkv * m->tmax * 256;
             TRY(launch_attn_prefill(p.q16, L.Kc + kvrow, p.vT, p.qkv + 256, nq, p.x16, T, Hq, Hkv, m->tmax, p.tv,
                                     1.0f / 16.0f, st));
-            TRY(w8p(p.x16, Hq * 256, L.out, T, segments({{p.mix, H, H}}), st));
+            TRY(w8p_residual(p.x16, Hq * 256, L.out, T, p.h, H, st));
             TRY(mark(m, KAI_GDN_PHASE_ATTN, st));
         }
-        addnorm_kernel<<<T, 256, 0, st>>>(p.h, p.mix, L.ln_post, p.x16, H, c.rms_eps);
+        addnorm_kernel<<<T, 256, 0, st>>>(p.h, nullptr, L.ln_post, p.x16, H, c.rms_eps);
         TRY(hipGetLastError());
         TRY(w8p(p.x16, H, L.gate_up, T, swiglu, st));
-        TRY(w8p(p.act16, I, L.down, T, segments({{p.mix, H, H}}), st));
+        TRY(w8p_residual(p.act16, I, L.down, T, p.h, H, st));
         const float *next_norm = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : m->final_norm;
-        addnorm_kernel<<<T, 256, 0, st>>>(p.h, p.mix, next_norm, p.x16, H, c.rms_eps);
+        addnorm_kernel<<<T, 256, 0, st>>>(p.h, nullptr, next_norm, p.x16, H, c.rms_eps);
         TRY(hipGetLastError());
         TRY(mark(m, KAI_GDN_PHASE_FFN, st));
     }

@@ -55,7 +55,7 @@ GDN_DEV void w8p_store_tile(const f32x16_t &acc, int row, int nt, int h2, const 
     for (int q = 0; q < 4; ++q) {
         const int n = nt + 8 * q + 4 * h2;
         const f32x4_t sc = *reinterpret_cast<const f32x4_t *>(scale + n);
-        const f32x4_t y = f32x4_t{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]} * sc;
+        f32x4_t y = f32x4_t{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]} * sc;
         if (out.mode == kW8SwiGLU) {
             // 16-channel groups: 8 gate channels (q even), then their 8 up channels (q + 1)
             if (q & 1) continue;
@@ -86,6 +86,9 @@ GDN_DEV void w8p_store_tile(const f32x16_t &acc, int row, int nt, int h2, const 
                     dst = out.seg[qq].dst;
                     ld = out.seg[qq].ld;
                 }
+            // the residual add (one segment): may be in place, each element
+            // is read and written by this lane only
+            if (out.add_in) y = *reinterpret_cast<const f32x4_t *>(out.add_in + (size_t)row * out.add_ld + n) + y;
             *reinterpret_cast<f32x4_t *>(dst + (size_t)row * ld + (n - nb)) = y;
         }
     }
@@ -562,7 +565,8 @@ hipError_t launch_w8p(const uint16_t *x, int ldx, const int8_t *W, const float *
     if (M <= 0) return hipSuccess;
     if (N <= 0 || N % 64 || K <= 0 || K % 64 || ldx < K || ldx % 8 || (uintptr_t)x % 16 ||
         (out.mode != kW8Segments && out.mode != kW8SwiGLU) || (out.mode == kW8SwiGLU && (N % 16 || !out.x16)) ||
-        (out.mode == kW8Segments && (out.nseg < 1 || out.nseg > kW8MaxSegs)))
+        (out.mode == kW8Segments && (out.nseg < 1 || out.nseg > kW8MaxSegs)) ||
+        (out.add_in && (out.mode != kW8Segments || out.nseg != 1)))
         return hipErrorInvalidValue;
     if (M >= kW8pLargeRows) {
         const long long mb = (M + kPBM2 - 1) / kPBM2;
