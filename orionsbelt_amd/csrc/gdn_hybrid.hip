@@ -468,7 +468,7 @@ struct kai_gdn_hybrid {
     struct Prefill {
         int rows = 0, tv = 0;  // capacity (positions) and the V^T row length
         float *h = nullptr, *qkv = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
-        float *conv = nullptr, *g = nullptr, *beta = nullptr, *kx = nullptr, *vx = nullptr, *hist = nullptr;
+        float *g = nullptr, *beta = nullptr, *kx = nullptr, *vx = nullptr, *hist = nullptr;
         uint16_t *x16 = nullptr, *act16 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
         uint16_t *q16 = nullptr, *vT = nullptr;
     } pf;
@@ -855,7 +855,6 @@ hipError_t prefill_alloc(kai_gdn_hybrid *m) {
     TRY(alloc_t(m, &p.z, R * V));
     TRY(alloc_t(m, &p.a, R * Hv));
     TRY(alloc_t(m, &p.b, R * Hv));
-    TRY(alloc_t(m, &p.conv, R * C));
     TRY(alloc_t(m, &p.g, R * Hv));
     TRY(alloc_t(m, &p.beta, R * Hv));
     TRY(alloc_t(m, &p.kx, R * Hkv * 256));
@@ -913,9 +912,8 @@ hipError_t prefill_seq(kai_gdn_hybrid *m, const int32_t *tokens, int b, int T, h
             // the decode step's conv cache: the last four conv inputs
             TRY(launch_conv_state_from_inputs(p.qkv, L.conv_state[0] + (size_t)b * C * 4, 1, T, C, st));
             TRY(hipMemsetAsync(p.hist, 0, (size_t)3 * C * sizeof(float), st));
-            TRY(launch_conv_k4(p.qkv, L.conv_wt, p.conv, p.hist, T, C, true, st));
-            TRY(launch_gating_prologue(true, p.conv, p.a, p.b, L.A_log, L.dt_bias, p.q, p.k, p.v, p.g, p.beta, T,
-                                       Hk, Hv, st));
+            TRY(launch_conv_gating(p.qkv, L.conv_wt, p.hist, p.a, p.b, L.A_log, L.dt_bias, p.q, p.k, p.v, p.g,
+                                   p.beta, T, Hk, Hv, st));
             float *S = L.S + (size_t)b * Hv * 128 * 128;
             TRY(hipMemsetAsync(S, 0, (size_t)Hv * 128 * 128 * sizeof(float), st));
             const int rc = kai_run_gdn_chunk_delta_rule_bf16_f32_hip(p.q, p.k, p.v, p.g, p.beta, p.o, S, 1, T, Hv,

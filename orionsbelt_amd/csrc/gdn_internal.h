@@ -97,6 +97,13 @@ hipError_t launch_prefill_seq(int narrow_state, const uint16_t *q, const uint16_
 
 // Gating prologue: conv output x [rows][(2 Hk + Hv) * 128] -> q, k (L2-normalised)
 // [rows][Hk][128], v [rows][Hv][128] (bf16 bit patterns or fp32), g, beta [rows][Hv].
+// The prefill's causal conv (K = 4, SiLU; tap-major weights conv_wt [4][C],
+// the three previous inputs in hist [3][C]) fused with the gating prologue
+// into bf16 q, k, v and fp32 g, beta: bit for bit launch_conv_k4 followed by
+// launch_gating_prologue, without the conv's output array.
+hipError_t launch_conv_gating(const float *x, const float *conv_wt, const float *hist, const float *a,
+                              const float *b, const float *A_log, const float *dt_bias, uint16_t *q, uint16_t *k,
+                              uint16_t *v, float *g, float *beta, int64_t T, int Hk, int Hv, hipStream_t st);
 hipError_t launch_gating_prologue(bool bf16, const float *x, const float *a, const float *b,
                                   const float *A_log, const float *dt_bias, void *q, void *k,
                                   void *v, float *g, float *beta, size_t rows, int Hk, int Hv,

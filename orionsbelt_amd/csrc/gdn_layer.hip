@@ -145,6 +145,96 @@ __global__ __launch_bounds__(kThreads) void gating_prologue_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// The causal conv (K = 4, SiLU) of a prompt's rows fused with the gating
+// prologue, so that the conv's fp32 output never reaches HBM.  Block (row
+// segment of kConvRows rows, 16 heads): 16-lane group s takes head
+// 16 blockIdx.y + s, lane l its channels 8l .. 8l+7, for every row of the
+// segment in order, with the three previous inputs in registers (from the
+// rows before the segment, or from `hist` for the first).  Each value is
+// conv_k4_kernel's (the same tap sum in the same order, no contraction, and
+// its SiLU), and each head row then gets gating_prologue_kernel's arithmetic,
+// so q, k, v, g and beta are bit for bit those of the two kernels in turn.
+// The block of head group 0 also forms the segment's gates.
+// ---------------------------------------------------------------------------
+constexpr int kConvRows = 64;  // rows per block
+constexpr int kConvU = 4;      // rows in flight per lane
+
+GDN_DEV float conv_silu(float h0, float h1, float h2, float cur, float w0, float w1, float w2, float w3) {
+#pragma clang fp contract(off)
+    const float acc = h0 * w0 + h1 * w1 + h2 * w2 + cur * w3;
+    return acc / (1.0f + expf(-acc));
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void conv_gating_kernel(
+    const float *__restrict__ x, const float *__restrict__ wt, const float *__restrict__ hist,
+    const float *__restrict__ a, const float *__restrict__ b, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, OutT *__restrict__ q, OutT *__restrict__ k, OutT *__restrict__ v,
+    float *__restrict__ g, float *__restrict__ beta, int64_t T, int Hk, int Hv) {
+    const int tid = threadIdx.x, lane = tid & 15, grp = tid >> 4;
+    const int H = 2 * Hk + Hv;
+    const int64_t C = (int64_t)H * D;
+    const int h = blockIdx.y * kGroups + grp;  // uniform over the group
+    const int64_t t0 = (int64_t)blockIdx.x * kConvRows, t1 = min(T, t0 + kConvRows);
+    if (h < H) {
+        const int64_t c = (int64_t)h * D + 8 * lane;
+        V8 w[4], hh[3];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = load8(wt + j * C + c);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) hh[j] = t0 == 0 ? load8(hist + j * C + c) : load8(x + (t0 - 3 + j) * C + c);
+        OutT *dst;
+        int64_t ld;
+        if (h < Hk) {
+            dst = q + (int64_t)h * D;
+            ld = (int64_t)Hk * D;
+        } else if (h < 2 * Hk) {
+            dst = k + (int64_t)(h - Hk) * D;
+            ld = (int64_t)Hk * D;
+        } else {
+            dst = v + (int64_t)(h - 2 * Hk) * D;
+            ld = (int64_t)Hv * D;
+        }
+        for (int64_t t = t0; t < t1; t += kConvU) {
+            // unconditional loads (rows past the end clamp to the last row and
+            // are not used), so the kConvU rows issue back to back
+            V8 cur[kConvU];
+#pragma unroll
+            for (int i = 0; i < kConvU; ++i) cur[i] = load8(x + min(t + i, T - 1) * C + c);
+#pragma unroll
+            for (int i = 0; i < kConvU; ++i) {
+                if (t + i >= t1) break;  // uniform over the block
+                V8 y;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    y.f[e] = conv_silu(hh[0].f[e], hh[1].f[e], hh[2].f[e], cur[i].f[e], w[0].f[e], w[1].f[e],
+                                       w[2].f[e], w[3].f[e]);
+                hh[0] = hh[1];
+                hh[1] = hh[2];
+                hh[2] = cur[i];
+                if (h < 2 * Hk) {
+                    const float inv = 1.0f / sqrtf(group_sum(sumsq8(y)) + 1e-6f);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) y.f[e] *= inv;
+                }
+                store8(dst + (t + i) * ld + 8 * lane, y);
+            }
+        }
+    }
+    if (blockIdx.y == 0) {
+        const int64_t n = (t1 - t0) * Hv;
+        for (int64_t i0 = tid; i0 < n; i0 += kThreads) {
+            const int64_t i = t0 * Hv + i0;
+            const int hv = (int)(i0 % Hv);
+            const float y = a[i] + dt_bias[hv];
+            const float sp = y > 20.f ? y : log1pf(expf(y));
+            g[i] = -expf(A_log[hv]) * sp;
+            beta[i] = 1.0f / (1.0f + expf(-b[i]));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Gated RMSNorm with the SiLU gate (HF Qwen3_5RMSNormGated.forward,
 // modeling_qwen3_5.py:175-184) over rows of 128 values; 16-lane group s of
 // block B takes rows 16 NP B + s + 16 j, j < NP.
@@ -206,6 +296,18 @@ hipError_t launch_gating_prologue(bool bf16, const float *x, const float *a, con
         gating_prologue_kernel<float><<<grid, kThreads, 0, st>>>(
             x, a, b, A_log, dt_bias, static_cast<float *>(q), static_cast<float *>(k),
             static_cast<float *>(v), g, beta, Hk, Hv);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_gating(const float *x, const float *conv_wt, const float *hist, const float *a,
+                              const float *b, const float *A_log, const float *dt_bias, uint16_t *q, uint16_t *k,
+                              uint16_t *v, float *g, float *beta, int64_t T, int Hk, int Hv, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    if (Hk <= 0 || Hv <= 0) return hipErrorInvalidValue;
+    const int H = 2 * Hk + Hv;
+    const dim3 grid((unsigned)((T + kConvRows - 1) / kConvRows), (unsigned)((H + kGroups - 1) / kGroups));
+    conv_gating_kernel<uint16_t><<<grid, kThreads, 0, st>>>(x, conv_wt, hist, a, b, A_log, dt_bias, q, k, v, g, beta,
+                                                            T, Hk, Hv);
     return hipGetLastError();
 }
 
