@@ -285,9 +285,9 @@ int kai_run_gdn_w8a16_gemm_hip(const uint16_t *x, const int8_t *Wq, const float 
  * workspace holds the partials and one counter per group, must be zeroed
  * once before its first use (each call leaves the counters at zero), and
  * calls that share it must not overlap.  0 workspace bytes: none needed.
- * For M <= 3 and K of 2560, 4096 or 9216 (the Qwen3.5-4B matrices) one
- * 16-channel tile per block runs instead, with no k-split; the workspace is
- * then unused.  M > 16 (a prompt's rows: the counterpart of the reference
+ * For M <= 3, N <= 32768 and K of 2560, 4096 or 9216 (the Qwen3.5-4B
+ * matrices but the LM head) one 16-channel tile per block runs instead,
+ * with no k-split; the workspace is then unused.  M > 16 (a prompt's rows: the counterpart of the reference
  * e2e loop's M > 1 gemm_int8_neon, gdn_e2e_decode.c:606-612) takes the
  * prefill GEMM on fp16 MFMA (128 x 128 output tiles below 512 rows, 256 x
  * 256 from 512), and no workspace. */
